@@ -1,0 +1,131 @@
+/*
+ * g4attn.h -- C ABI of the MI355X (gfx950) Gemma 4 E2B attention library
+ * (libg4attn.so, built from slang_amd/csrc/).
+ *
+ * Plain C: pointers, sizes and a config struct; no HIP or torch types. Every
+ * pointer argument except `cfg` is DEVICE memory owned by the caller; the
+ * library never allocates. `stream` is a hipStream_t passed as void* (NULL =
+ * the default stream). Calls are asynchronous on `stream`; argument errors are
+ * reported synchronously through the return code before anything is launched.
+ *
+ * Tensor layouts are the reference runners' (wakoan/slang gemma4_150):
+ *   q        [n_tokens][n_q_heads][head_dim]      (runner.py:408-423 outq;
+ *                                                  prefill_gpu.py:239 "q" [S][q_dim])
+ *   KV cache [position][n_kv_heads][head_dim]     (kernels_dsl.py:1634, 1681 index
+ *                                                  ((t*kvH + hKv)*hd + d)), f16 by
+ *                                                  default, f32 with G4A_KV_F32
+ *   out      [n_tokens][n_q_heads][head_dim]      (attn_101 "out", kernels_dsl.py:1749;
+ *                                                  attnh f16, prefill_gpu.py:311-313)
+ *   RoPE tables: rows of cos/sin f32 [half] aligned with the call's tokens: row s
+ *   belongs to the token at position start_pos+s (prefill, kv write) or to
+ *   sequence s's query (decode). Callers offset into their full [max_pos][half]
+ *   tables, as the runners pass pre-offset tables to attn_101 (runner.py:283-289)
+ *   and absolute tables to the batched kernels (prefill_wgpu.py:142-153).
+ *   Pairs i >= the RoPE cutoff are identity rows (cos 1, sin 0) in the tables.
+ */
+#ifndef G4ATTN_H
+#define G4ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* cfg.flags */
+#define G4A_KV_F32    0x1u /* caches hold f32 (the reference's own cache type); default f16 */
+#define G4A_IN_F16    0x2u /* g4a_kv_write: k/v inputs are f16 (kvnorm_b); default f32 (kvnorm) */
+#define G4A_NO_V_NORM 0x4u /* g4a_kv_write: store v as given instead of RMSNorm(v) */
+#define G4A_OUT_F32   0x8u /* g4a_prefill: f32 output (attn_prefill's "out"); default f16 (attnh) */
+
+typedef struct g4a_cfg {
+    uint32_t n_q_heads;  /* qHeads (params[3] of attn_101, params[1] of attn_prefill) */
+    uint32_t n_kv_heads; /* kvHeads; n_q_heads % n_kv_heads == 0, group size <= 8 */
+    uint32_t head_dim;   /* 256 (sliding layers) or 512 (global layers) */
+    uint32_t window;     /* sliding window W; 0 = global (params[5] / params[3]) */
+    uint32_t flags;      /* G4A_* */
+    float scale;         /* score scale: 1.0 for Gemma 4, 1/sqrt(head_dim) for Gemma 3 */
+    float eps;           /* RMSNorm epsilon, 1e-6 in the reference */
+    float out_q;         /* SRQ step of the output (attn_101's OUT_Q); 0 = pass-through */
+} g4a_cfg;
+
+/* return codes */
+#define G4A_OK            0
+#define G4A_EINVAL       -1 /* bad argument (null pointer, size, alignment) */
+#define G4A_EUNSUPPORTED -2 /* head_dim / group size this build does not instantiate */
+#define G4A_EWORKSPACE   -3 /* workspace missing or smaller than the *_ws_bytes size */
+#define G4A_EHIP         -4 /* a HIP call failed; g4a_last_error() names it */
+
+const char* g4a_strerror(int code);
+/* Detail of the last failure on the calling thread ("" if none). */
+const char* g4a_last_error(void);
+int g4a_version(void);
+
+/*
+ * Decode attention: one new query per sequence against its KV cache.
+ * Replaces the attn_101 dispatch (gemma4_150/kernels_dsl.py:1537-1749; bound at
+ * runner.py:430-441 and metal_runner.py:348-349 with slots
+ * [q, q_norm, cos, sin, k, v, partials, out, params]).
+ *
+ *   key_len[s]  int32, device: keys of sequence s (params[1] keyLen); the query
+ *               sits at position key_len[s]-1 (params[2] qOffset = pos).
+ *               Sequence s attends keys [max(0, key_len-W), key_len) (W = window, 0 = all).
+ *   max_key_len host upper bound of key_len[]; sizes the split-KV grid only.
+ *   q           f32 [n_seq][n_q_heads][head_dim], raw: RMSNorm*q_gain then RoPE
+ *               are applied in the kernel as attn_101 does (kernels_dsl.py:1593-1615).
+ *   q_gain      f32 [head_dim] or NULL (no q RMSNorm).
+ *   rope_cos/sin f32 [n_seq][head_dim/2] for each query's position, or NULL (no RoPE).
+ *   k_cache/v_cache sequence s at base + s*seq_stride elements, rows [pos][kvH][hd].
+ *   out         f32 [n_seq][n_q_heads][head_dim] (srq'd with out_q when nonzero).
+ *   ws          workspace of at least g4a_decode_ws_bytes() bytes, zero-filled ONCE
+ *               before first use (as the reference zeroes `partials` at setup,
+ *               runner.py:367-371); every call leaves its ticket counters at zero
+ *               again (kernels_dsl.py:1714-1715). Concurrent calls need distinct ws.
+ */
+size_t g4a_decode_ws_bytes(const g4a_cfg* cfg, int n_seq, int max_key_len);
+int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+               const float* q, const float* q_gain, const float* rope_cos, const float* rope_sin,
+               const void* k_cache, const void* v_cache, int64_t seq_stride, float* out,
+               void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Batched causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
+ * Replaces PrefillGPU._attn_gemm (prefill_gpu.py:259-313: qprep_b -> QK^T GEMM ->
+ * smax_b -> PV GEMM -> attnout_b) and the fused attn_prefill dispatch
+ * (kernels_dsl.py:1950-2098, bound at prefill_gpu.py:347-354 with slots
+ * [q, q_norm, cosT, sinT, k, v, out, (startPos, qH, kvH, W, S)]).
+ *
+ *   q        f32 [S][n_q_heads][head_dim] raw; RMSNorm*q_gain + RoPE are applied in
+ *            the kernel and the result is rounded to f16 (qprep_b, kernels_dsl.py:1872-1873).
+ *   rope_cos/sin f32 [S][head_dim/2] rows for the S positions, or NULL.
+ *   k_cache/v_cache rows [0, start_pos+S) already written (g4a_kv_write).
+ *   out      f16 [S][n_q_heads][head_dim] (attnh), or f32 with G4A_OUT_F32.
+ *   Token s attends keys [max(0, p+1-W), p] with p = start_pos+s (kernels_dsl.py:1986-1992).
+ *   ws/ws_bytes: g4a_prefill_ws_bytes() bytes (0 in this build: ws may be NULL).
+ */
+size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos);
+int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q, const float* q_gain,
+                const float* rope_cos, const float* rope_sin, const void* k_cache,
+                const void* v_cache, void* out, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * KV-cache write of S new tokens at rows start_pos..start_pos+S-1:
+ *   k <- RoPE(RMSNorm(srq(k, k_in_q)) * k_gain),  v <- RMSNorm(srq(v, v_in_q)) (no gain).
+ * Replaces kvnorm (kernels_dsl.py:573-618, dispatched at runner.py:424-429 with slots
+ * [outk, outv, k_norm, cos, sin, kc, vc, pkv]) and kvnorm_b (kernels_dsl.py:1789-1834,
+ * prefill_gpu.py:335-342, slots [kraw, vraw, k_norm, cosT, sinT, kc, vc, (startPos, kS, vS)]).
+ *
+ *   k, v     [S][n_kv_heads][head_dim], f32 (kvnorm) or f16 with G4A_IN_F16 (kvnorm_b).
+ *   k_gain   f32 [head_dim] or NULL (no k RMSNorm). G4A_NO_V_NORM skips the v norm.
+ *   rope_cos/sin f32 [S][head_dim/2] or NULL.
+ *   k_cache/v_cache rows of [pos][kvH][hd], f16 (or f32 with G4A_KV_F32).
+ */
+int g4a_kv_write(const g4a_cfg* cfg, int S, int start_pos, const void* k, const void* v,
+                 float k_in_q, float v_in_q, const float* k_gain, const float* rope_cos,
+                 const float* rope_sin, void* k_cache, void* v_cache, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4ATTN_H */

@@ -1,0 +1,91 @@
+"""ctypes binding of libg4attn.so (the C ABI declared in include/g4attn.h).
+
+The library must have been built (``__graft_entry__.build()`` or
+``python -m slang_amd.build``); loading fails loudly otherwise -- there is no
+fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libg4attn.so")
+
+# flags (g4attn.h)
+KV_F32 = 0x1
+IN_F16 = 0x2
+NO_V_NORM = 0x4
+OUT_F32 = 0x8
+
+# every function include/g4attn.h declares
+EXPORTS = (
+    "g4a_strerror", "g4a_last_error", "g4a_version",
+    "g4a_decode_ws_bytes", "g4a_decode",
+    "g4a_prefill_ws_bytes", "g4a_prefill",
+    "g4a_kv_write",
+)
+
+
+class G4ACfg(ctypes.Structure):
+    _fields_ = [
+        ("n_q_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("out_q", ctypes.c_float),
+    ]
+
+
+class G4AError(RuntimeError):
+    """A libg4attn call returned an error code."""
+
+    def __init__(self, code: int, detail: str):
+        super().__init__(f"g4attn error {code}: {detail}")
+        self.code = code
+
+
+_lib = None
+P = ctypes.c_void_p
+
+
+def load() -> ctypes.CDLL:
+    """Load libg4attn.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                           "(python -m slang_amd.build); there is no fallback path")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.g4a_strerror.restype = ctypes.c_char_p
+    lib.g4a_strerror.argtypes = [ctypes.c_int]
+    lib.g4a_last_error.restype = ctypes.c_char_p
+    lib.g4a_last_error.argtypes = []
+    lib.g4a_version.restype = ctypes.c_int
+    lib.g4a_version.argtypes = []
+    cfgp = ctypes.POINTER(G4ACfg)
+    lib.g4a_decode_ws_bytes.restype = ctypes.c_size_t
+    lib.g4a_decode_ws_bytes.argtypes = [cfgp, ctypes.c_int, ctypes.c_int]
+    lib.g4a_decode.restype = ctypes.c_int
+    lib.g4a_decode.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P,
+                               ctypes.c_int64, P, P, ctypes.c_size_t, P]
+    lib.g4a_prefill_ws_bytes.restype = ctypes.c_size_t
+    lib.g4a_prefill_ws_bytes.argtypes = [cfgp, ctypes.c_int, ctypes.c_int]
+    lib.g4a_prefill.restype = ctypes.c_int
+    lib.g4a_prefill.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, P,
+                                ctypes.c_size_t, P]
+    lib.g4a_kv_write.restype = ctypes.c_int
+    lib.g4a_kv_write.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_float,
+                                 ctypes.c_float, P, P, P, P, P, P]
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        lib = load()
+        raise G4AError(rc, f"{lib.g4a_strerror(rc).decode()}: {lib.g4a_last_error().decode()}")

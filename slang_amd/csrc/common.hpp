@@ -1,0 +1,89 @@
+// Shared device helpers and host-side argument checking for libg4attn (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/g4attn.h"
+
+namespace g4a {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float8v __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ---------------------------------------------------------------- host-side errors
+void set_error(const char* fmt, ...);
+int hip_error(hipError_t e, const char* what);
+bool check_cfg(const g4a_cfg* cfg, bool need_group_le8);
+
+// ---------------------------------------------------------------- lane shuffles
+// DPP row_ror:n (rotate right by n lanes within each row of 16 lanes).
+template <int N>
+__device__ __forceinline__ float dpp_ror(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_ror<8>(x);
+    x += dpp_ror<4>(x);
+    x += dpp_ror<2>(x);
+    x += dpp_ror<1>(x);
+    return x;
+}
+
+__device__ __forceinline__ float xor_shfl(float x, int m) { return __shfl_xor(x, m, 64); }
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    x += xor_shfl(x, 16);
+    x += xor_shfl(x, 32);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp_ror<8>(x));
+    x = fmaxf(x, dpp_ror<4>(x));
+    x = fmaxf(x, dpp_ror<2>(x));
+    x = fmaxf(x, dpp_ror<1>(x));
+    x = fmaxf(x, xor_shfl(x, 16));
+    x = fmaxf(x, xor_shfl(x, 32));
+    return x;
+}
+
+// ---------------------------------------------------------------- numerics
+// Static-range quantisation, identity when s == 0 (gemma4_150/reference.py:30-31).
+// x / s is the IEEE quotient and rintf rounds half to even, as numpy's round does.
+__device__ __forceinline__ float srq(float x, float s) {
+    if (s == 0.0f) return x;
+    return fminf(fmaxf(rintf(x / s), -128.0f), 127.0f) * s;
+}
+
+// 8 consecutive cache elements as f32, from f16 (one 16 B load) or f32 (two 16 B loads).
+__device__ __forceinline__ float8v load8(const half_t* p) {
+    half8 h = *reinterpret_cast<const half8*>(p);
+    return __builtin_convertvector(h, float8v);
+}
+__device__ __forceinline__ float8v load8(const float* p) {
+    float4v a = *reinterpret_cast<const float4v*>(p);
+    float4v b = *reinterpret_cast<const float4v*>(p + 4);
+    return float8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// 8 consecutive cache elements as f16 (the MFMA operand type).
+__device__ __forceinline__ half8 load8h(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+__device__ __forceinline__ half8 load8h(const float* p) {
+    return __builtin_convertvector(load8(p), half8);
+}
+
+__device__ __forceinline__ void store_elem(half_t* p, float v) { *p = (half_t)v; }
+__device__ __forceinline__ void store_elem(float* p, float v) { *p = v; }
+
+}  // namespace g4a

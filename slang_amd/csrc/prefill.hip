@@ -1,0 +1,324 @@
+// Batched causal prefill attention for gfx950 on f16 MFMA (v_mfma_f32_16x16x32_f16).
+//
+// Reference semantics: PrefillGPU._attn_gemm (gemma4_150/prefill_gpu.py:259-313) --
+// qprep_b rounds the RMSNorm'd, rotated q to f16 (kernels_dsl.py:1837-1873), scores
+// are q.k (scale 1.0 for Gemma 4), smax_b masks each row to [max(0, p+1-W), p]
+// (:1898-1908), P.V, attnout_b divides by the row sum and applies srq(o_in)
+// (:1752-1763). attn_prefill (:1950-2098) is the fused f32 form with the same mask.
+//
+// MI355X design: flash attention with an online softmax instead of the reference's
+// materialised [S*nH][T] score matrix. A workgroup owns one kv head and BQ = 64/G
+// query positions, i.e. 64 query columns = all G heads of the GQA group x BQ
+// positions, so each K/V tile staged in LDS serves every head that reads it. Each of
+// the 4 waves owns 16 columns. Scores are computed transposed, S^T = K . Q^T
+// (A = K tile from LDS, B = Q^T held in registers), which leaves every lane with 4
+// keys of ONE query column -- exactly the B-operand layout the P.V product needs
+// when it is also computed transposed, O^T = V^T . P^T (A = V^T from LDS, staged
+// transposed at load time). Scores stay f32 in the MFMA accumulators; P is rounded
+// to f16 only as the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last]
+// are skipped; boundary tiles are masked per element. Work-groups are launched
+// longest-causal-row first.
+#include "common.hpp"
+
+namespace g4a {
+
+struct PrefillArgs {
+    const float* q;
+    const float* q_gain;
+    const float* rcos;
+    const float* rsin;
+    const void* kc;
+    const void* vc;
+    void* out;
+    int S, start_pos, n_q_heads, n_kv_heads, window, n_qblocks;
+    float scale_log2, eps, out_q;
+};
+
+template <int HD>
+struct PrefillShape {
+    static constexpr int KT = HD == 512 ? 32 : 64;  // keys per LDS tile
+    static constexpr int KSTEPS = HD / 32;           // MFMA k-steps of the score product
+    static constexpr int NKT = KT / 16;              // 16-key sub-tiles of S^T
+    static constexpr int NU = KT / 32;               // 32-key k-steps of the P.V product
+    static constexpr int NDT = HD / 16;              // 16-dim tiles of O^T
+    static constexpr int KS = HD + 8;                // K tile row stride (halves), 16 B pad
+    static constexpr int VS = KT + 8;                // V^T row stride (halves)
+};
+
+__device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <int HD, int G, typename KVT, typename OUTT>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+    using Sh = PrefillShape<HD>;
+    constexpr int KT = Sh::KT, KSTEPS = Sh::KSTEPS, NKT = Sh::NKT, NU = Sh::NU, NDT = Sh::NDT;
+    constexpr int KS = Sh::KS, VS = Sh::VS;
+    constexpr int BQ = 64 / G;
+
+    __shared__ __attribute__((aligned(16))) half_t Ks[KT * KS];
+    __shared__ __attribute__((aligned(16))) half_t Vt[HD * VS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int qb = a.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
+    const int kh = blockIdx.y;
+    const int T_total = a.start_pos + a.S;
+
+    // ---- this lane's query column: head hh of the group, position offset po
+    const int qc = 16 * wave + n;
+    const int hh = qc / BQ, po = qc % BQ;
+    const int s_raw = qb * BQ + po;
+    const bool col_ok = s_raw < a.S;
+    const int s_idx = col_ok ? s_raw : a.S - 1;
+    const int pos = a.start_pos + s_idx;
+    const int h = kh * G + hh;
+
+    // ---- q prologue: RMSNorm*gain, RoPE, f16; lane holds dims 32s + 8g + i
+    half8 qf[KSTEPS];
+    {
+        float x[KSTEPS][8];
+        const float* qr = a.q + ((size_t)s_idx * a.n_q_heads + h) * HD;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            const float8v v = load8(qr + 32 * s + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = v[i];
+        }
+        if (a.q_gain) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
+            ss += xor_shfl(ss, 16);
+            ss += xor_shfl(ss, 32);
+            const float den = sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const float8v gv = load8(a.q_gain + 32 * s + 8 * g);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[i];
+            }
+        }
+        if (a.rcos) {
+            const float* cr = a.rcos + (size_t)s_idx * (HD / 2);
+            const float* sr = a.rsin + (size_t)s_idx * (HD / 2);
+#pragma unroll
+            for (int s = 0; s < KSTEPS / 2; ++s) {
+                const float8v cv = load8(cr + 32 * s + 8 * g);
+                const float8v sv = load8(sr + 32 * s + 8 * g);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
+                    x[s][i] = x0 * cv[i] - x1 * sv[i];
+                    x[s + KSTEPS / 2][i] = x1 * cv[i] + x0 * sv[i];
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+    }
+
+    // ---- key range of the workgroup and of this column
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, T_total);
+    const int wg_lo = (a.window > 0) ? max(0, p0 + 1 - a.window) : 0;
+    const int col_lo = (a.window > 0) ? pos + 1 - a.window : 0;
+    const size_t rstride = (size_t)a.n_kv_heads * HD;
+    const KVT* kcb = reinterpret_cast<const KVT*>(a.kc) + (size_t)kh * HD;
+    const KVT* vcb = reinterpret_cast<const KVT*>(a.vc) + (size_t)kh * HD;
+
+    float4v oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
+    float m_run = kNegInf, l_run = 0.0f;
+
+    for (int t0 = (wg_lo / KT) * KT; t0 < kv_hi; t0 += KT) {
+        __syncthreads();  // previous tile fully consumed
+        // K tile, row-major [key][dim] with a 16 B row pad
+        for (int idx = tid; idx < KT * (HD / 8); idx += 256) {
+            const int row = idx / (HD / 8), ch = idx % (HD / 8);
+            const int key = t0 + row;
+            half8 v = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (key < T_total) v = load8h(kcb + (size_t)key * rstride + 8 * ch);
+            *reinterpret_cast<half8*>(&Ks[row * KS + 8 * ch]) = v;
+        }
+        // V tile, transposed [dim][key]: 4 keys x 8 dims per unit
+        for (int idx = tid; idx < (KT / 4) * (HD / 8); idx += 256) {
+            const int jg = idx % (KT / 4), dg = idx / (KT / 4);
+            half8 v[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int key = t0 + 4 * jg + kk;
+                v[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                if (key < T_total) v[kk] = load8h(vcb + (size_t)key * rstride + 8 * dg);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                *reinterpret_cast<half4*>(&Vt[(8 * dg + i) * VS + 4 * jg]) = half4{v[0][i], v[1][i], v[2][i], v[3][i]};
+        }
+        __syncthreads();
+
+        // S^T = K . Q^T : sacc[kt][i] = score(key t0+16kt+4g+i, column n)
+        float4v sacc[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            float4v c4 = float4v{0, 0, 0, 0};
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const half8 av = *reinterpret_cast<const half8*>(&Ks[(16 * kt + n) * KS + 32 * s + 8 * g]);
+                c4 = mfma16(av, qf[s], c4);
+            }
+            sacc[kt] = c4;
+        }
+        // scale (log2 domain), mask, online softmax
+        float mt = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = t0 + 16 * kt + 4 * g + i;
+                const bool ok = key <= pos && key >= col_lo;
+                const float sv = ok ? sacc[kt][i] * a.scale_log2 : kNegInf;
+                sacc[kt][i] = sv;
+                mt = fmaxf(mt, sv);
+            }
+        mt = fmaxf(mt, xor_shfl(mt, 16));
+        mt = fmaxf(mt, xor_shfl(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        const float base = (m_new == kNegInf) ? 0.0f : m_new;
+        const float corr = exp2f(m_run - base);
+        float ps = 0.0f;
+        half8 pf[NU];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = exp2f(sacc[kt][i] - base);
+                ps += p;
+                pf[kt >> 1][(kt & 1) * 4 + i] = (half_t)p;
+            }
+        l_run = l_run * corr + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
+
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const half_t* vr = &Vt[(16 * dt + n) * VS + 32 * u + 4 * g];
+                const half4 lo4 = *reinterpret_cast<const half4*>(vr);
+                const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
+                const half8 av = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                oacc[dt] = mfma16(av, pf[u], oacc[dt]);
+            }
+    }
+
+    // ---- epilogue: row sum over the 4 lane groups, normalise, srq, store
+    float l_tot = l_run;
+    l_tot += xor_shfl(l_tot, 16);
+    l_tot += xor_shfl(l_tot, 32);
+    if (!col_ok) return;
+    OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + h) * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_elem(orow + 16 * dt + 4 * g + i, srq(oacc[dt][i] / l_tot, a.out_q));
+}
+
+typedef void (*prefill_fn)(PrefillArgs);
+
+template <int HD, int G, typename KVT>
+static prefill_fn pick_out(bool out32) {
+    return out32 ? prefill_kernel<HD, G, KVT, float> : prefill_kernel<HD, G, KVT, half_t>;
+}
+template <int HD, int G>
+static prefill_fn pick_kv(bool kv32, bool out32) {
+    return kv32 ? pick_out<HD, G, float>(out32) : pick_out<HD, G, half_t>(out32);
+}
+template <int HD>
+static prefill_fn pick_g(int G, bool kv32, bool out32) {
+    switch (G) {
+        case 1: return pick_kv<HD, 1>(kv32, out32);
+        case 2: return pick_kv<HD, 2>(kv32, out32);
+        case 4: return pick_kv<HD, 4>(kv32, out32);
+        case 8: return pick_kv<HD, 8>(kv32, out32);
+    }
+    return nullptr;
+}
+
+}  // namespace g4a
+
+using namespace g4a;
+
+extern "C" size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos) {
+    (void)cfg;
+    (void)S;
+    (void)start_pos;
+    return 0;
+}
+
+extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q,
+                           const float* q_gain, const float* rope_cos, const float* rope_sin,
+                           const void* k_cache, const void* v_cache, void* out, void* ws,
+                           size_t ws_bytes, void* stream) {
+    (void)ws;
+    (void)ws_bytes;
+    if (!check_cfg(cfg, true)) return G4A_EINVAL;
+    if (S <= 0 || start_pos < 0) {
+        set_error("S (%d) must be positive and start_pos (%d) non-negative", S, start_pos);
+        return G4A_EINVAL;
+    }
+    if (!q || !k_cache || !v_cache || !out) {
+        set_error("q, k_cache, v_cache and out must be non-NULL");
+        return G4A_EINVAL;
+    }
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) {
+        set_error("rope_cos and rope_sin must both be given or both be NULL");
+        return G4A_EINVAL;
+    }
+    const int HD = (int)cfg->head_dim, G = (int)(cfg->n_q_heads / cfg->n_kv_heads);
+    if (HD != 256 && HD != 512) {
+        set_error("head_dim %d not supported (256 or 512)", HD);
+        return G4A_EUNSUPPORTED;
+    }
+    if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)out) % 16 ||
+        (q_gain && (uintptr_t)q_gain % 16) || (rope_cos && ((uintptr_t)rope_cos | (uintptr_t)rope_sin) % 16)) {
+        set_error("q, q_gain, rope tables, caches and out must be 16-byte aligned");
+        return G4A_EINVAL;
+    }
+    const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
+    prefill_fn fn = HD == 256 ? pick_g<256>(G, kv32, out32) : pick_g<512>(G, kv32, out32);
+    if (!fn) {
+        set_error("no prefill kernel for group size %d", G);
+        return G4A_EUNSUPPORTED;
+    }
+    PrefillArgs a;
+    a.q = q;
+    a.q_gain = q_gain;
+    a.rcos = rope_cos;
+    a.rsin = rope_sin;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.out = out;
+    a.S = S;
+    a.start_pos = start_pos;
+    a.n_q_heads = (int)cfg->n_q_heads;
+    a.n_kv_heads = (int)cfg->n_kv_heads;
+    a.window = (int)cfg->window;
+    const int BQ = 64 / G;
+    a.n_qblocks = (S + BQ - 1) / BQ;
+    a.scale_log2 = cfg->scale * kLog2e;
+    a.eps = cfg->eps;
+    a.out_q = cfg->out_q;
+    dim3 grid(a.n_qblocks, cfg->n_kv_heads);
+    hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "prefill launch");
+    return G4A_OK;
+}

@@ -1,0 +1,107 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what include/g4attn.h
+declares, and rejects bad arguments before launching anything (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from slang_amd import _lib
+from slang_amd._lib import G4ACfg
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "g4attn.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(g4a_[a-z_0-9]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libg4attn.so is not built: run __graft_entry__.build() first")
+    return _lib.load()
+
+
+def test_exports_match_header(lib):
+    decl = declared_functions()
+    assert decl == sorted(_lib.EXPORTS), f"header declares {decl}, binding lists {sorted(_lib.EXPORTS)}"
+    for name in decl:
+        assert hasattr(lib, name), f"{name} not exported by libg4attn.so"
+
+
+def test_cfg_struct_layout_matches_header():
+    assert ctypes.sizeof(G4ACfg) == 8 * 4
+    assert [f[0] for f in G4ACfg._fields_] == ["n_q_heads", "n_kv_heads", "head_dim", "window",
+                                                "flags", "scale", "eps", "out_q"]
+
+
+def test_strerror_and_version(lib):
+    assert lib.g4a_version() >= 1
+    for code in (0, -1, -2, -3, -4):
+        assert lib.g4a_strerror(code)
+
+
+def cfg(**kw):
+    base = dict(n_q_heads=8, n_kv_heads=2, head_dim=256, window=0, flags=0, scale=1.0, eps=1e-6, out_q=0.0)
+    base.update(kw)
+    return G4ACfg(**base)
+
+
+FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every case fails validation first
+
+
+def decode(lib, c, **kw):
+    a = dict(n_seq=1, max_key_len=64, key_len=FAKE, q=FAKE, gain=None, cos=None, sin=None, k=FAKE,
+             v=FAKE, stride=0, out=FAKE, ws=FAKE, ws_bytes=1 << 30)
+    a.update(kw)
+    return lib.g4a_decode(ctypes.byref(c) if c is not None else None, a["n_seq"], a["max_key_len"],
+                          a["key_len"], a["q"], a["gain"], a["cos"], a["sin"], a["k"], a["v"],
+                          a["stride"], a["out"], a["ws"], a["ws_bytes"], None)
+
+
+def test_decode_argument_errors(lib):
+    assert decode(lib, None) == -1
+    assert decode(lib, cfg(n_q_heads=6, n_kv_heads=4)) == -1          # not a multiple
+    assert decode(lib, cfg(n_q_heads=12, n_kv_heads=1)) == -1         # group 12 > 8
+    assert decode(lib, cfg(head_dim=128)) == -2                       # not instantiated
+    assert decode(lib, cfg(), n_seq=0) == -1
+    assert decode(lib, cfg(), q=None) == -1
+    assert decode(lib, cfg(), cos=FAKE) == -1                         # sin missing
+    assert decode(lib, cfg(), ws_bytes=16) == -3                      # workspace too small
+    assert decode(lib, cfg(), ws=None) == -3
+    assert b"workspace" in lib.g4a_last_error()
+
+
+def test_decode_ws_bytes(lib):
+    c = cfg()
+    small = lib.g4a_decode_ws_bytes(ctypes.byref(c), 1, 64)
+    big = lib.g4a_decode_ws_bytes(ctypes.byref(c), 16, 32768)
+    assert 0 < small < big
+    assert lib.g4a_decode_ws_bytes(ctypes.byref(c), 0, 64) == 0
+
+
+def test_prefill_and_kv_write_argument_errors(lib):
+    c = cfg()
+    P = lib.g4a_prefill
+    assert P(ctypes.byref(c), 0, 0, FAKE, None, None, None, FAKE, FAKE, FAKE, None, 0, None) == -1
+    assert P(ctypes.byref(c), 4, -1, FAKE, None, None, None, FAKE, FAKE, FAKE, None, 0, None) == -1
+    assert P(ctypes.byref(cfg(head_dim=64)), 4, 0, FAKE, None, None, None, FAKE, FAKE, FAKE, None, 0, None) == -2
+    assert P(ctypes.byref(c), 4, 0, ctypes.c_void_p(0x10004), None, None, None, FAKE, FAKE, FAKE,
+             None, 0, None) == -1                                     # misaligned q
+    K = lib.g4a_kv_write
+    assert K(ctypes.byref(c), 1, 0, None, FAKE, 0.0, 0.0, None, None, None, FAKE, FAKE, None) == -1
+    assert K(ctypes.byref(c), 1, 0, FAKE, FAKE, -1.0, 0.0, None, None, None, FAKE, FAKE, None) == -1
+    assert K(ctypes.byref(cfg(head_dim=100)), 1, 0, FAKE, FAKE, 0.0, 0.0, None, None, None, FAKE,
+             FAKE, None) == -2
+
+
+def test_host_mirror_raises_without_library(monkeypatch, tmp_path):
+    """The product path has no fallback: a missing library is an error, not a CPU path."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.load()

@@ -1,0 +1,219 @@
+"""GPU parity of decode attention (libg4attn g4a_decode) against the CPU oracle and the
+golden vectors, at the contract tolerance |d| <= 2e-3 + 1e-2|ref|; mask sets exact.
+
+Cases follow the reference's own decode tests (tests/test_gemma3_kernels_gpu.py:372-395,
+tests/test_gemma4_kernels_gpu.py:63-80, tests/test_kernels_dsl_parity.py:726-782) and
+BASELINE configs 1, 2 (global and sliding) and 4.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as O
+import slang_amd as sa
+from helpers import contract_close, gold, srq_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def t(x, dtype=None):
+    x = torch.from_numpy(np.ascontiguousarray(x))
+    return (x if dtype is None else x.to(dtype)).to(DEV)
+
+
+def run(q, k, v, key_len, cfg, **kw):
+    out = sa.decode(t(q), t(k), t(v), key_len, cfg, **{n: (t(a) if isinstance(a, np.ndarray) else a)
+                                                       for n, a in kw.items()})
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# ---------------------------------------------------------------- golden vectors
+def test_golden_g3_fused_f32_cache():
+    z = gold("g3_fused.npz")
+    k32, v32 = z["k"].astype(np.float32), z["v"].astype(np.float32)
+    for i, kl in enumerate(z["key_len"]):
+        cfg = sa.AttnConfig(4, 1, 256, int(z["window"][i]), float(z["scale"]))
+        got = run(z["q"], k32, v32, [int(kl)], cfg)
+        contract_close(got, z["expected"][i], f"g3_fused kv_len={kl}")
+
+
+@pytest.mark.parametrize("tag", ["hd256_s0", "hd512_s0", "hd256_s3", "hd512_s5"])
+def test_golden_g4_fused(tag):
+    z = gold("g4_fused.npz")
+    hd = int(tag[2:5])
+    cfg = sa.AttnConfig(8, 1, hd, int(z[f"{tag}_window"]))
+    got = run(z[f"{tag}_q"], z[f"{tag}_k"], z[f"{tag}_v"], [int(z["key_len"])], cfg)
+    contract_close(got, z[f"{tag}_expected"], tag)
+
+
+@pytest.mark.parametrize("tag", ["hd256_len90", "hd512_len90"])
+def test_golden_attn101(tag):
+    """attn_101's own test case (q-norm, random gain and tables, G = 8) incl. the OUT_Q srq."""
+    z = gold("attn101.npz")
+    hd, kl = int(tag[2:5]), int(tag.split("len")[1])
+    kw = dict(q_gain=z[f"{tag}_w"], rope_cos=z[f"{tag}_cos"][None], rope_sin=z[f"{tag}_sin"][None])
+    got = run(z[f"{tag}_q"], z[f"{tag}_k"], z[f"{tag}_v"], [kl], sa.AttnConfig(8, 1, hd), **kw)
+    contract_close(got, z[f"{tag}_expected"], tag)
+    oq = float(z["out_q"])
+    gq = run(z[f"{tag}_q"], z[f"{tag}_k"], z[f"{tag}_v"], [kl], sa.AttnConfig(8, 1, hd, out_q=oq), **kw)
+    srq_close(gq, z[f"{tag}_expected"], oq, tag)
+
+
+@pytest.mark.parametrize("window", [0, 40])
+def test_golden_g4e2b(window):
+    z = gold("g4e2b_decode.npz")
+    got = run(z["q"], z["k"], z["v"], [int(z["key_len"])], sa.AttnConfig(8, 2, 256, window),
+              q_gain=z["w"], rope_cos=z["cos"][None], rope_sin=z["sin"][None])
+    contract_close(got, z[f"expected_w{window}"], f"g4e2b w={window}")
+
+
+# ---------------------------------------------------------------- BASELINE configs
+def config2_inputs(T, theta, seed=7, nH=8, kvH=2, hd=256):
+    """Config 2: q, k, v ~ N(0,1); k RMSNorm*gain + RoPE and v RMSNorm written as f16 rows."""
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((nH, hd)).astype(np.float32)
+    qg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kr = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    vr = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    cos, sin = O.rope_tables(np.arange(T), hd, theta)
+    k, v = O.kv_write(kr, vr, kg, cos, sin)
+    return q, qg, k, v, cos[T - 1], sin[T - 1]
+
+
+@pytest.mark.parametrize("window,theta", [(0, 1e6), (512, 1e4)])
+def test_config2(window, theta):
+    T = 4096
+    q, qg, k, v, c, s = config2_inputs(T, theta)
+    cfg = sa.AttnConfig(8, 2, 256, window)
+    got = run(q, k, v, [T], cfg, q_gain=qg, rope_cos=c[None], rope_sin=s[None])
+    ref = O.decode_attention(q, k, v, T, 2, q_gain=qg, cos=c, sin=s, window=window)
+    contract_close(got, ref, f"config2 W={window}")
+
+
+def test_config1_f32_cache_no_norm():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((4, 256)).astype(np.float32)
+    k = rng.standard_normal((1024, 1, 256)).astype(np.float32)
+    v = rng.standard_normal((1024, 1, 256)).astype(np.float32)
+    cfg = sa.AttnConfig(4, 1, 256, 0, 1 / 16)
+    got = run(q, k, v, [1024], cfg)
+    contract_close(got, O.decode_attention(q, k, v, 1024, 1, scale=1 / 16), "config1")
+
+
+def test_config4_batched_long_context():
+    """16 sequences, key lengths ~ U[1024, 32768], contiguous per-sequence caches."""
+    B, nH, kvH, hd, Tmax = 16, 8, 2, 256, 32768
+    lens = np.random.default_rng(4).integers(1024, 32769, size=B).astype(np.int32)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    q = torch.randn(B, nH, hd, device=DEV, generator=g)
+    k = torch.randn(B, Tmax, kvH, hd, device=DEV, generator=g).half()
+    v = torch.randn(B, Tmax, kvH, hd, device=DEV, generator=g).half()
+    out = sa.decode(q, k, v, t(lens), sa.AttnConfig(nH, kvH, hd))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    qn = q.cpu().numpy()
+    for b in range(B):
+        L = int(lens[b])
+        ref = O.decode_attention(qn[b], k[b, :L].cpu().numpy(), v[b, :L].cpu().numpy(), L, kvH)
+        contract_close(got[b], ref, f"config4 seq {b} len {L}")
+
+
+# ---------------------------------------------------------------- shapes and edges
+@pytest.mark.parametrize("nH,kvH,hd", [(2, 2, 256), (4, 2, 256), (8, 1, 512), (4, 1, 512), (8, 8, 256)])
+@pytest.mark.parametrize("T,window", [(1, 0), (17, 0), (300, 0), (1500, 0), (300, 64), (2049, 512)])
+def test_group_sizes_and_lengths(nH, kvH, hd, T, window):
+    rng = np.random.default_rng(T * 31 + nH)
+    q = rng.standard_normal((nH, hd)).astype(np.float32)
+    qg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    k = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    v = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    k, v = O.kv_write(k, v, (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    c, s = O.rope_tables([T - 1], hd, 1e4)
+    got = run(q, k, v, [T], sa.AttnConfig(nH, kvH, hd, window), q_gain=qg, rope_cos=c, rope_sin=s)
+    ref = O.decode_attention(q, k, v, T, kvH, q_gain=qg, cos=c[0], sin=s[0], window=window)
+    contract_close(got, ref, f"nH={nH} kvH={kvH} hd={hd} T={T} W={window}")
+
+
+def test_ragged_batch_with_window():
+    B, nH, kvH, hd, Tmax = 5, 8, 2, 256, 700
+    lens = np.array([1, 16, 17, 512, 700], np.int32)
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((B, nH, hd)).astype(np.float32)
+    k = rng.standard_normal((B, Tmax, kvH, hd)).astype(np.float16)
+    v = rng.standard_normal((B, Tmax, kvH, hd)).astype(np.float16)
+    c, s = O.rope_tables(lens - 1, hd, 1e4)
+    cfg = sa.AttnConfig(nH, kvH, hd, 300)
+    got = run(q, k, v, t(lens), cfg, rope_cos=c, rope_sin=s)
+    ref = O.decode_attention_batched(q, k, v, lens, kvH, cos=c, sin=s, window=300)
+    contract_close(got, ref, "ragged batch")
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 255, 256, 257, 511])
+@pytest.mark.parametrize("dw", [None, -1, 0, 1])
+def test_mask_set_exact(T, dw):
+    """q = 0 gives every attended key weight 1/n; one-hot V rows (v_j = e_j, hd 512) turn the
+    output into the indicator of the attended set, which must be exactly [max(0,T-W), T)."""
+    hd = 512
+    window = 0 if dw is None else max(1, T + dw)
+    k = np.random.default_rng(T).standard_normal((T, 1, hd)).astype(np.float16)
+    v = np.zeros((T, 1, hd), np.float16)
+    v[np.arange(T), 0, np.arange(T)] = 1
+    got = run(np.zeros((2, hd), np.float32), k, v, [T], sa.AttnConfig(2, 1, hd, window))
+    lo = max(0, T - window) if window else 0
+    assert set(np.nonzero(got[0] > 1e-6)[0]) == set(range(lo, T))
+    np.testing.assert_allclose(got[0][lo:T], 1.0 / (T - lo), rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,window", [(4096, 0), (4096, 512), (1000, 999), (1000, 1)])
+def test_mask_leak_marker(T, window):
+    """Keys outside the window score +8 and carry V = 1000; inside keys score 0, V = 1.
+    Any leaked key pulls the output far above 1."""
+    hd = 256
+    lo = max(0, T - window) if window else 0
+    q = np.zeros((4, hd), np.float32)
+    q[:, 0] = 1.0
+    k = np.zeros((T, 1, hd), np.float16)
+    v = np.ones((T, 1, hd), np.float16)
+    k[:lo, 0, 0] = 8.0
+    v[:lo] = 1000.0
+    got = run(q, k, v, [T], sa.AttnConfig(4, 1, hd, window))
+    np.testing.assert_allclose(got, 1.0, atol=1e-5)
+
+
+def test_tickets_reset_and_deterministic():
+    """Every call leaves its ticket counters at zero (kernels_dsl.py:1714-1715,
+    tests/test_kernels_dsl_parity.py:780) and repeats bit-identically."""
+    T = 4096
+    q, qg, k, v, c, s = config2_inputs(T, 1e6, seed=3)
+    ws = sa.DecodeWorkspace(DEV)
+    cfg = sa.AttnConfig(8, 2, 256)
+    args = (t(q), t(k), t(v), [T], cfg)
+    kw = dict(q_gain=t(qg), rope_cos=t(c[None]), rope_sin=t(s[None]), workspace=ws)
+    a = sa.decode(*args, **kw).clone()
+    b = sa.decode(*args, **kw).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert int(ws.buf[:256].count_nonzero()) == 0, "ticket counters not reset"
+    assert int(a.count_nonzero()) > 0
+
+
+def test_attn_101_mirror_matches_decode():
+    """The reference-slot drop-in (params = (1, keyLen, pos, qH, kvH, W, 0, 0))."""
+    z = gold("attn101.npz")
+    tag, hd, kl = "hd256_len90", 256, 90
+    maxseq = 128
+    kc = np.zeros((maxseq, 1, hd), np.float16)
+    vc = np.zeros((maxseq, 1, hd), np.float16)
+    kc[:kl], vc[:kl] = z[f"{tag}_k"], z[f"{tag}_v"]
+    out = torch.zeros(8 * hd, device=DEV)
+    sa.attn_101(t(z[f"{tag}_q"].reshape(-1)), t(z[f"{tag}_w"]), t(z[f"{tag}_cos"]), t(z[f"{tag}_sin"]),
+                t(kc.reshape(-1)), t(vc.reshape(-1)), sa.DecodeWorkspace(DEV), out,
+                (1, kl, kl - 1, 8, 1, 0, 0, 0), head_dim=hd)
+    torch.cuda.synchronize()
+    contract_close(out.cpu().numpy().reshape(8, hd), z[f"{tag}_expected"], "attn_101 mirror")
+    with pytest.raises(ValueError):
+        sa.attn_101(t(z[f"{tag}_q"].reshape(-1)), None, None, None, t(kc.reshape(-1)),
+                    t(vc.reshape(-1)), None, out, (1, kl, kl, 8, 1, 0, 0, 0), head_dim=hd)
