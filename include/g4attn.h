@@ -38,6 +38,9 @@ extern "C" {
 #define G4A_IN_F16    0x2u /* g4a_kv_write: k/v inputs are f16 (kvnorm_b); default f32 (kvnorm) */
 #define G4A_NO_V_NORM 0x4u /* g4a_kv_write: store v as given instead of RMSNorm(v) */
 #define G4A_OUT_F32   0x8u /* g4a_prefill: f32 output (attn_prefill's "out"); default f16 (attnh) */
+#define G4A_Q_HILO    0x10u /* g4a_prefill: keep q at f32 accuracy (f16 hi + lo MFMA operands),
+                               as attn_prefill's f32 q (kernels_dsl.py:2007-2014); default rounds
+                               q to f16 as qprep_b does (kernels_dsl.py:1872-1873) */
 
 typedef struct g4a_cfg {
     uint32_t n_q_heads;  /* qHeads (params[3] of attn_101, params[1] of attn_prefill) */
@@ -108,6 +111,16 @@ size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos);
 int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q, const float* q_gain,
                 const float* rope_cos, const float* rope_sin, const void* k_cache,
                 const void* v_cache, void* out, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * q RMSNorm*q_gain + RoPE for S*n_q_heads rows, stored f16 [S][n_q_heads][head_dim].
+ * Replaces qprep_b (kernels_dsl.py:1837-1873, dispatched at prefill_gpu.py:283-285 with
+ * slots [q, q_norm, cosT, sinT, qf16, (startPos, qHeads)]). Uses the same arithmetic and
+ * lane layout as g4a_prefill's prologue, so it yields exactly the f16 q g4a_prefill
+ * feeds its MFMAs (without G4A_Q_HILO). rope_cos/sin: [S][head_dim/2] rows or NULL.
+ */
+int g4a_qprep(const g4a_cfg* cfg, int S, const float* q, const float* q_gain,
+              const float* rope_cos, const float* rope_sin, void* q16, void* stream);
 
 /*
  * KV-cache write of S new tokens at rows start_pos..start_pos+S-1:

@@ -17,12 +17,13 @@ KV_F32 = 0x1
 IN_F16 = 0x2
 NO_V_NORM = 0x4
 OUT_F32 = 0x8
+Q_HILO = 0x10
 
 # every function include/g4attn.h declares
 EXPORTS = (
     "g4a_strerror", "g4a_last_error", "g4a_version",
     "g4a_decode_ws_bytes", "g4a_decode",
-    "g4a_prefill_ws_bytes", "g4a_prefill",
+    "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
 )
 
@@ -78,6 +79,8 @@ def load() -> ctypes.CDLL:
     lib.g4a_prefill.restype = ctypes.c_int
     lib.g4a_prefill.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, P,
                                 ctypes.c_size_t, P]
+    lib.g4a_qprep.restype = ctypes.c_int
+    lib.g4a_qprep.argtypes = [cfgp, ctypes.c_int, P, P, P, P, P, P]
     lib.g4a_kv_write.restype = ctypes.c_int
     lib.g4a_kv_write.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_float,
                                  ctypes.c_float, P, P, P, P, P, P]

@@ -25,8 +25,8 @@ from . import _lib
 from ._lib import G4ACfg, check
 
 __all__ = [
-    "AttnConfig", "DecodeWorkspace", "decode", "prefill", "kv_write", "rope_tables",
-    "attn_101", "kvnorm", "kvnorm_b", "attn_prefill", "attn_gemm",
+    "AttnConfig", "DecodeWorkspace", "decode", "prefill", "qprep", "kv_write", "rope_tables",
+    "attn_101", "kvnorm", "kvnorm_b", "attn_prefill", "attn_gemm", "qprep_b",
 ]
 
 
@@ -152,11 +152,13 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
 
 
 def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
-            rope_sin=None, out=None, out_dtype=torch.float16):
+            rope_sin=None, out=None, out_dtype=torch.float16, q_hilo: bool = False):
     """Causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
 
     q [S][nH][hd] f32 raw; caches [>= start_pos+S][kvH][hd] f16/f32; rope_cos/sin
     [S][hd/2] rows for those positions. Returns out [S][nH][hd] (f16 by default).
+    q_hilo keeps the normalised, rotated q at f32 accuracy (two f16 MFMA operands)
+    instead of rounding it to f16 as qprep_b does.
     """
     S = q.shape[0]
     if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
@@ -177,12 +179,30 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None
         out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     _need(out, "out", (torch.float16, torch.float32))
     flags = (_lib.KV_F32 if k_cache.dtype == torch.float32 else 0) | \
-            (_lib.OUT_F32 if out.dtype == torch.float32 else 0)
+            (_lib.OUT_F32 if out.dtype == torch.float32 else 0) | (_lib.Q_HILO if q_hilo else 0)
     c = cfg.c(flags)
     lib = _lib.load()
     check(lib.g4a_prefill(ctypes.byref(c), S, int(start_pos), _ptr(q), _ptr(q_gain), _ptr(rope_cos),
                           _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), None, 0,
                           ctypes.c_void_p(_stream())))
+    return out
+
+
+def qprep(q, cfg: AttnConfig, *, q_gain=None, rope_cos=None, rope_sin=None, out=None):
+    """qprep_b (kernels_dsl.py:1837-1873): f16 [S][nH][hd] = f16(RoPE(RMSNorm(q) * q_gain)).
+
+    Bit-identical to the f16 q that ``prefill`` feeds its MFMAs (without q_hilo)."""
+    S = q.shape[0]
+    if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
+        raise ValueError(f"q shape {tuple(q.shape)} does not match {cfg}")
+    for t, nm in ((q, "q"), (q_gain, "q_gain"), (rope_cos, "rope_cos"), (rope_sin, "rope_sin")):
+        _need(t, nm, torch.float32)
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    _need(out, "out", torch.float16)
+    c = cfg.c(0)
+    check(_lib.load().g4a_qprep(ctypes.byref(c), S, _ptr(q), _ptr(q_gain), _ptr(rope_cos),
+                                _ptr(rope_sin), _ptr(out), ctypes.c_void_p(_stream())))
     return out
 
 
@@ -273,6 +293,17 @@ def attn_prefill(q, q_norm, cosT, sinT, kc, vc, out, params, *, head_dim, out_q=
             start, cfg, q_gain=q_norm, rope_cos=cosT.view(-1, half)[start:start + S],
             rope_sin=sinT.view(-1, half)[start:start + S], out=out.view(S, qh, head_dim))
     return out
+
+
+def qprep_b(q, q_norm, cosT, sinT, qf16, p, *, S, head_dim):
+    """qprep_b (kernels_dsl.py:1837-1873; prefill_gpu.py:283-285): slots [q, q_norm, cosT, sinT,
+    qf16, p] with p = (startPos, qHeads); cosT/sinT absolute-position tables [max_pos][hd/2]."""
+    start, qh = int(p[0]), int(p[1])
+    half = head_dim // 2
+    cfg = AttnConfig(qh, qh, head_dim)
+    qprep(q.view(S, qh, head_dim), cfg, q_gain=q_norm, rope_cos=cosT.view(-1, half)[start:start + S],
+          rope_sin=sinT.view(-1, half)[start:start + S], out=qf16.view(S, qh, head_dim))
+    return qf16
 
 
 def attn_gemm(q, q_norm, cosT, sinT, kc, vc, attnh, *, S, start_pos, n_q_heads, n_kv_heads,

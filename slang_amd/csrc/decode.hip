@@ -34,7 +34,7 @@ struct DecodeArgs {
     uint32_t* tickets;  // [pairs]
     float2* part_ml;    // [pairs][max_splits][G] (m, l)
     float* part_o;      // [pairs][max_splits][G][HD]
-    int n_q_heads, n_kv_heads, window, max_splits, min_chunk;
+    int n_q_heads, n_kv_heads, window, max_splits, chunk;
     float scale_log2, eps, out_q;
 };
 
@@ -117,11 +117,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             for (int e = tid; e < G * HD; e += 256) outp[e] = 0.0f;
         return;
     }
-    int n_act = (active + a.min_chunk - 1) / a.min_chunk;
-    n_act = n_act < 1 ? 1 : (n_act > a.max_splits ? a.max_splits : n_act);
-    int chunk = (active + n_act - 1) / n_act;
-    chunk = (chunk + 15) & ~15;
-    n_act = (active + chunk - 1) / chunk;
+    int chunk = a.chunk;  // keys per split (multiple of 16), chosen on the host
+    int n_act = (active + chunk - 1) / chunk;
+    if (n_act > a.max_splits) {  // a key_len above the host's max_key_len: widen the splits
+        chunk = (((active + a.max_splits - 1) / a.max_splits) + 15) & ~15;
+        n_act = (active + chunk - 1) / chunk;
+    }
     if (ci >= n_act) return;
     const int k0 = lo + ci * chunk;
     const int k1 = min(k0 + chunk, hi);
@@ -182,8 +183,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         for (int e = 0; e < NE; ++e) acc[hh][e] = 0.0f;
     }
 
-    for (int blk = k0 + wave * BK; blk < k1; blk += 4 * BK) {
-        raw_t kr[NS][NCH], vr[NS][NCH];
+    // K/V of the next block are loaded while the current one is processed
+    raw_t kr[NS][NCH], vr[NS][NCH];
+    auto load_block = [&](int blk, raw_t (&kk)[NS][NCH], raw_t (&vv)[NS][NCH]) {
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
             const int key = blk + t * KPS + r;
@@ -191,10 +193,16 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int j = 0; j < NCH; ++j) {
                 const size_t off = (size_t)key * rstride + 8 * LPK * j;
-                kr[t][j] = ok ? RC::load(kbase + off) : RC::zero();
-                vr[t][j] = ok ? RC::load(vbase + off) : RC::zero();
+                kk[t][j] = ok ? RC::load(kbase + off) : RC::zero();
+                vv[t][j] = ok ? RC::load(vbase + off) : RC::zero();
             }
         }
+    };
+    int blk = k0 + wave * BK;
+    if (blk < k1) load_block(blk, kr, vr);
+    for (; blk < k1; blk += 4 * BK) {
+        raw_t kn[NS][NCH], vn[NS][NCH];
+        load_block(blk + 4 * BK, kn, vn);  // keys >= k1 load nothing
         float s[NS][G];
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
@@ -244,6 +252,13 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
                 for (int i = 0; i < 8; ++i)
 #pragma unroll
                     for (int hh = 0; hh < G; ++hh) acc[hh][8 * j + i] = fmaf(s[t][hh], vf[i], acc[hh][8 * j + i]);
+            }
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                kr[t][j] = kn[t][j];
+                vr[t][j] = vn[t][j];
             }
     }
 
@@ -327,20 +342,41 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         if (lane == 0) s_L[hh] = lsum;
     }
     __syncthreads();
-    const float* pob = a.part_o + (size_t)pair * a.max_splits * (G * HD);
-    for (int e = tid; e < G * HD; e += 256) {
-        const int hh = e / HD;
+    // each thread owns 4 consecutive outputs and streams the splits 16 at a time
+    const float4* pob4 = reinterpret_cast<const float4*>(a.part_o + (size_t)pair * a.max_splits * (G * HD));
+    constexpr int STRIDE4 = G * HD / 4;
+    for (int e4 = tid; e4 < STRIDE4; e4 += 256) {
+        const int hh = (4 * e4) / HD;
         const float* wh = wts + hh * 256;
-        float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
         int t = 0;
-        for (; t + 4 <= n_act; t += 4) {
-            o0 = fmaf(wh[t + 0], pob[(size_t)(t + 0) * (G * HD) + e], o0);
-            o1 = fmaf(wh[t + 1], pob[(size_t)(t + 1) * (G * HD) + e], o1);
-            o2 = fmaf(wh[t + 2], pob[(size_t)(t + 2) * (G * HD) + e], o2);
-            o3 = fmaf(wh[t + 3], pob[(size_t)(t + 3) * (G * HD) + e], o3);
+        for (; t + 16 <= n_act; t += 16) {
+            float4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)(t + u) * STRIDE4 + e4];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float w = wh[t + u];
+                o.x = fmaf(w, v[u].x, o.x);
+                o.y = fmaf(w, v[u].y, o.y);
+                o.z = fmaf(w, v[u].z, o.z);
+                o.w = fmaf(w, v[u].w, o.w);
+            }
         }
-        for (; t < n_act; ++t) o0 = fmaf(wh[t], pob[(size_t)t * (G * HD) + e], o0);
-        outp[e] = srq(((o0 + o1) + (o2 + o3)) / s_L[hh], a.out_q);
+        for (; t < n_act; ++t) {
+            const float4 v = pob4[(size_t)t * STRIDE4 + e4];
+            const float w = wh[t];
+            o.x = fmaf(w, v.x, o.x);
+            o.y = fmaf(w, v.y, o.y);
+            o.z = fmaf(w, v.z, o.z);
+            o.w = fmaf(w, v.w, o.w);
+        }
+        const float L = s_L[hh];
+        float* op = outp + 4 * e4;
+        op[0] = srq(o.x / L, a.out_q);
+        op[1] = srq(o.y / L, a.out_q);
+        op[2] = srq(o.z / L, a.out_q);
+        op[3] = srq(o.w / L, a.out_q);
     }
 }
 
@@ -350,25 +386,27 @@ static int env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-static int min_chunk_keys() {
-    static int v = 0;
-    if (!v) {
-        v = env_int("G4A_DECODE_MIN_CHUNK", 32);
-        if (v < 16) v = 16;
-        v = (v + 15) & ~15;
-    }
-    return v;
+// Keys per split: spread the worst-case work (every sequence at max_key_len) over about
+// G4A_DECODE_TARGET_WGS workgroups, but never below G4A_DECODE_MIN_CHUNK keys, so the
+// partial (G*hd floats) stays small next to the K/V it summarises.
+static int decode_chunk(const g4a_cfg* cfg, int n_seq, int max_key_len) {
+    const long pairs = (long)n_seq * cfg->n_kv_heads;
+    long max_active = max_key_len;
+    if (cfg->window > 0 && (long)cfg->window < max_active) max_active = cfg->window;
+    const long target = env_int("G4A_DECODE_TARGET_WGS", 1024);
+    long min_chunk = env_int("G4A_DECODE_MIN_CHUNK", 32);
+    long chunk = (max_active * pairs + target - 1) / target;
+    if (chunk < min_chunk) chunk = min_chunk;
+    if ((max_active + chunk - 1) / chunk > 256) chunk = (max_active + 255) / 256;
+    return (int)((chunk + 15) & ~15L);
 }
 
 static int decode_splits(const g4a_cfg* cfg, int n_seq, int max_key_len) {
-    const int pairs = n_seq * (int)cfg->n_kv_heads;
-    int max_active = max_key_len;
-    if (cfg->window > 0 && (int)cfg->window < max_active) max_active = (int)cfg->window;
-    const int target = env_int("G4A_DECODE_TARGET_WGS", 512);
-    int want = (target + pairs - 1) / pairs;
-    const int by_len = (max_active + min_chunk_keys() - 1) / min_chunk_keys();
-    int s = want < by_len ? want : by_len;
-    return s < 1 ? 1 : (s > 256 ? 256 : s);
+    long max_active = max_key_len;
+    if (cfg->window > 0 && (long)cfg->window < max_active) max_active = cfg->window;
+    const int chunk = decode_chunk(cfg, n_seq, max_key_len);
+    const long s = (max_active + chunk - 1) / chunk;
+    return (int)(s < 1 ? 1 : s);
 }
 
 struct WsLayout {
@@ -474,7 +512,7 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
     a.max_splits = splits;
-    a.min_chunk = min_chunk_keys();
+    a.chunk = decode_chunk(cfg, n_seq, max_key_len);
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;

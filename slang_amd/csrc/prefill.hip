@@ -49,7 +49,78 @@ __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <int HD, int G, typename KVT, typename OUTT>
+// q RMSNorm*gain then split-half RoPE for one query row, in the MFMA B-operand layout:
+// the lane of k-group g holds dims 32s + 8g + i (s < hd/32, i < 8), so the RoPE partner
+// d + hd/2 sits in the same lane at step s + hd/64 and the row's sum of squares needs
+// only the two cross-group shuffles. Shared by g4a_prefill and g4a_qprep, whose lane
+// layouts match, so both round the same f32 values to f16.
+template <int HD>
+__device__ __forceinline__ void prep_q_column(const float* qr, const float* gain, const float* cr,
+                                              const float* sr, float eps, int g, float (&x)[HD / 32][8]) {
+    constexpr int KSTEPS = HD / 32;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        const float8v v = load8(qr + 32 * s + 8 * g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[s][i] = v[i];
+    }
+    if (gain) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
+        ss += xor_shfl(ss, 16);
+        ss += xor_shfl(ss, 32);
+        const float den = sqrtf(ss / (float)HD + eps);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            const float8v gv = load8(gain + 32 * s + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[i];
+        }
+    }
+    if (cr) {
+#pragma unroll
+        for (int s = 0; s < KSTEPS / 2; ++s) {
+            const float8v cv = load8(cr + 32 * s + 8 * g);
+            const float8v sv = load8(sr + 32 * s + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
+                x[s][i] = x0 * cv[i] - x1 * sv[i];
+                x[s + KSTEPS / 2][i] = x1 * cv[i] + x0 * sv[i];
+            }
+        }
+    }
+}
+
+// qprep_b (kernels_dsl.py:1837-1873): q RMSNorm*gain + RoPE for S*nH rows, stored f16.
+// A wave handles 16 rows with the same lane layout as the prefill prologue.
+template <int HD>
+__global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float* gain, const float* rcos,
+                                                    const float* rsin, half_t* out, int rows, int n_q_heads,
+                                                    float eps) {
+    constexpr int KSTEPS = HD / 32;
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + n;
+    const bool ok = row < rows;
+    const int rr = ok ? row : rows - 1;
+    const int s_idx = rr / n_q_heads;
+    float x[KSTEPS][8];
+    prep_q_column<HD>(q + (size_t)rr * HD, gain, rcos ? rcos + (size_t)s_idx * (HD / 2) : nullptr,
+                      rsin ? rsin + (size_t)s_idx * (HD / 2) : nullptr, eps, g, x);
+    if (!ok) return;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        half8 hv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = (half_t)x[s][i];
+        *reinterpret_cast<half8*>(out + (size_t)row * HD + 32 * s + 8 * g) = hv;
+    }
+}
+
+template <int HD, int G, typename KVT, typename OUTT, bool HILO>
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     using Sh = PrefillShape<HD>;
     constexpr int KT = Sh::KT, KSTEPS = Sh::KSTEPS, NKT = Sh::NKT, NU = Sh::NU, NDT = Sh::NDT;
@@ -75,51 +146,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const int h = kh * G + hh;
 
     // ---- q prologue: RMSNorm*gain, RoPE, f16; lane holds dims 32s + 8g + i
-    half8 qf[KSTEPS];
+    half8 qf[KSTEPS], ql[HILO ? KSTEPS : 1];
     {
         float x[KSTEPS][8];
-        const float* qr = a.q + ((size_t)s_idx * a.n_q_heads + h) * HD;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            const float8v v = load8(qr + 32 * s + 8 * g);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[s][i] = v[i];
-        }
-        if (a.q_gain) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
-            ss += xor_shfl(ss, 16);
-            ss += xor_shfl(ss, 32);
-            const float den = sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                const float8v gv = load8(a.q_gain + 32 * s + 8 * g);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[i];
-            }
-        }
-        if (a.rcos) {
-            const float* cr = a.rcos + (size_t)s_idx * (HD / 2);
-            const float* sr = a.rsin + (size_t)s_idx * (HD / 2);
-#pragma unroll
-            for (int s = 0; s < KSTEPS / 2; ++s) {
-                const float8v cv = load8(cr + 32 * s + 8 * g);
-                const float8v sv = load8(sr + 32 * s + 8 * g);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
-                    x[s][i] = x0 * cv[i] - x1 * sv[i];
-                    x[s + KSTEPS / 2][i] = x1 * cv[i] + x0 * sv[i];
-                }
-            }
-        }
+        prep_q_column<HD>(a.q + ((size_t)s_idx * a.n_q_heads + h) * HD, a.q_gain,
+                          a.rcos ? a.rcos + (size_t)s_idx * (HD / 2) : nullptr,
+                          a.rsin ? a.rsin + (size_t)s_idx * (HD / 2) : nullptr, a.eps, g, x);
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+            for (int i = 0; i < 8; ++i) {
+                const half_t hv = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+                qf[s][i] = hv;
+                if constexpr (HILO) ql[s][i] = col_ok ? (half_t)(x[s][i] - (float)hv) : (half_t)0.0f;
+            }
     }
 
     // ---- key range of the workgroup and of this column
@@ -171,6 +211,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             for (int s = 0; s < KSTEPS; ++s) {
                 const half8 av = *reinterpret_cast<const half8*>(&Ks[(16 * kt + n) * KS + 32 * s + 8 * g]);
                 c4 = mfma16(av, qf[s], c4);
+                if constexpr (HILO) c4 = mfma16(av, ql[s], c4);
             }
             sacc[kt] = c4;
         }
@@ -233,21 +274,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 
 typedef void (*prefill_fn)(PrefillArgs);
 
+template <int HD, int G, typename KVT, typename OUTT>
+static prefill_fn pick_hilo(bool hilo) {
+    return hilo ? prefill_kernel<HD, G, KVT, OUTT, true> : prefill_kernel<HD, G, KVT, OUTT, false>;
+}
 template <int HD, int G, typename KVT>
-static prefill_fn pick_out(bool out32) {
-    return out32 ? prefill_kernel<HD, G, KVT, float> : prefill_kernel<HD, G, KVT, half_t>;
+static prefill_fn pick_out(bool out32, bool hilo) {
+    return out32 ? pick_hilo<HD, G, KVT, float>(hilo) : pick_hilo<HD, G, KVT, half_t>(hilo);
 }
 template <int HD, int G>
-static prefill_fn pick_kv(bool kv32, bool out32) {
-    return kv32 ? pick_out<HD, G, float>(out32) : pick_out<HD, G, half_t>(out32);
+static prefill_fn pick_kv(bool kv32, bool out32, bool hilo) {
+    return kv32 ? pick_out<HD, G, float>(out32, hilo) : pick_out<HD, G, half_t>(out32, hilo);
 }
 template <int HD>
-static prefill_fn pick_g(int G, bool kv32, bool out32) {
+static prefill_fn pick_g(int G, bool kv32, bool out32, bool hilo) {
     switch (G) {
-        case 1: return pick_kv<HD, 1>(kv32, out32);
-        case 2: return pick_kv<HD, 2>(kv32, out32);
-        case 4: return pick_kv<HD, 4>(kv32, out32);
-        case 8: return pick_kv<HD, 8>(kv32, out32);
+        case 1: return pick_kv<HD, 1>(kv32, out32, hilo);
+        case 2: return pick_kv<HD, 2>(kv32, out32, hilo);
+        case 4: return pick_kv<HD, 4>(kv32, out32, hilo);
+        case 8: return pick_kv<HD, 8>(kv32, out32, hilo);
     }
     return nullptr;
 }
@@ -293,7 +338,8 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         return G4A_EINVAL;
     }
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
-    prefill_fn fn = HD == 256 ? pick_g<256>(G, kv32, out32) : pick_g<512>(G, kv32, out32);
+    const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
+    prefill_fn fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
@@ -320,5 +366,40 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
+    return G4A_OK;
+}
+
+extern "C" int g4a_qprep(const g4a_cfg* cfg, int S, const float* q, const float* q_gain,
+                         const float* rope_cos, const float* rope_sin, void* q16, void* stream) {
+    if (!check_cfg(cfg, false)) return G4A_EINVAL;
+    if (S <= 0 || !q || !q16) {
+        set_error("S must be positive and q, q16 non-NULL");
+        return G4A_EINVAL;
+    }
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) {
+        set_error("rope_cos and rope_sin must both be given or both be NULL");
+        return G4A_EINVAL;
+    }
+    const int HD = (int)cfg->head_dim;
+    if (HD != 256 && HD != 512) {
+        set_error("head_dim %d not supported (256 or 512)", HD);
+        return G4A_EUNSUPPORTED;
+    }
+    if (((uintptr_t)q | (uintptr_t)q16) % 16 || (q_gain && (uintptr_t)q_gain % 16) ||
+        (rope_cos && ((uintptr_t)rope_cos | (uintptr_t)rope_sin) % 16)) {
+        set_error("q, q_gain, rope tables and q16 must be 16-byte aligned");
+        return G4A_EINVAL;
+    }
+    const long rows = (long)S * cfg->n_q_heads;
+    if (rows > 0x7fffffffL - 64) {
+        set_error("S*n_q_heads too large");
+        return G4A_EINVAL;
+    }
+    const int blocks = (int)((rows + 63) / 64);
+    auto fn = HD == 256 ? qprep_kernel<256> : qprep_kernel<512>;
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, (hipStream_t)stream, q, q_gain, rope_cos, rope_sin,
+                       (half_t*)q16, (int)rows, (int)cfg->n_q_heads, cfg->eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "qprep launch");
     return G4A_OK;
 }

@@ -1,8 +1,12 @@
 """GPU parity of batched causal prefill attention (g4a_prefill) against the CPU oracle and
 the golden vectors, at |d| <= 2e-3 + 1e-2|ref|; attended sets exact per query row.
 
-The oracle consumes the same f16-rounded q the kernel feeds its MFMAs (qprep_b's rounding
-point, kernels_dsl.py:1872-1873) and the same f16 caches. Cases
+Two q precisions. Default: q is rounded to f16 after RMSNorm+RoPE (qprep_b's rounding
+point, kernels_dsl.py:1872-1873); the oracle is fed exactly that f16 q, taken from
+g4a_qprep (bit-identical to the prefill prologue, checked below), because with scale 1.0
+a one-ulp difference in a rounded q element moves scores by up to ~1e-2 and can push an
+output past 2e-3. G4A_Q_HILO: q kept at f32 accuracy and compared with the f32-q oracle
+(reference.py:150-151 semantics). Both modes see the same f16 caches. Cases
 (S = 1024, global and window 512), the reference's S = 300 tile-crossing case
 (gemma4_150/prefill_research/test_attn_prefill.py:17-27), continuation prefill
 (start_pos > 0), ragged S, one-hot mask sets, and an S = 8192 layer (config 5).
@@ -13,7 +17,7 @@ import torch
 
 import oracle.attention as O
 import slang_amd as sa
-from helpers import contract_close, gold, srq_close
+from helpers import contract_close, f16_ulp_close, gold, srq_close
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -23,11 +27,34 @@ def t(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
 
 
-def run(q, k, v, start, cfg, out_dtype=torch.float16, **kw):
-    out = sa.prefill(t(q), t(k), t(v), start, cfg, out_dtype=out_dtype,
+def run(q, k, v, start, cfg, out_dtype=torch.float16, q_hilo=False, **kw):
+    out = sa.prefill(t(q), t(k), t(v), start, cfg, out_dtype=out_dtype, q_hilo=q_hilo,
                      **{n: (t(a) if isinstance(a, np.ndarray) else a) for n, a in kw.items()})
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
+
+
+def kernel_q16(q, cfg, q_gain=None, cos=None, sin=None):
+    """The f16 q the prefill kernel feeds its MFMAs, via g4a_qprep."""
+    out = sa.qprep(t(q), cfg, q_gain=None if q_gain is None else t(q_gain),
+                   rope_cos=None if cos is None else t(cos), rope_sin=None if sin is None else t(sin))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check_both_modes(q, k, v, start, cfg, qg, cos, sin, what, out_q=0.0):
+    """Default mode vs the oracle on the kernel's f16 q; HILO mode vs the f32-q oracle."""
+    kvH, W = cfg.n_kv_heads, cfg.window
+    kw = dict(q_gain=qg, rope_cos=cos, rope_sin=sin)
+    q16 = kernel_q16(q, cfg, qg, cos, sin).astype(np.float32)
+    ref16 = O.prefill_attention(q16, k, v, start, kvH, window=W, scale=cfg.scale)
+    got = run(q, k, v, start, cfg, out_dtype=torch.float32, **kw)
+    contract_close(got, ref16, f"{what} (f16 q)")
+    ref32 = O.prefill_attention(q, k, v, start, kvH, q_gain=qg, cos=cos, sin=sin, window=W,
+                                scale=cfg.scale, q_round_f16=False)
+    got32 = run(q, k, v, start, cfg, out_dtype=torch.float32, q_hilo=True, **kw)
+    contract_close(got32, ref32, f"{what} (hilo q)")
+    return ref16, ref32
 
 
 def test_golden_prefill_core_exact_q():
@@ -50,6 +77,16 @@ def test_golden_prefill_end_to_end(window):
     contract_close(got, ref, f"oracle e2e w={window}")
 
 
+@pytest.mark.parametrize("window", [0, 16])
+def test_golden_prefill_hilo(window):
+    """G4A_Q_HILO against the float64 restatement with f32 q (reference.py's q precision)."""
+    z = gold("prefill.npz")
+    got = run(z["q"], z["k"], z["v"], int(z["start_pos"]), sa.AttnConfig(4, 2, 256, window),
+              out_dtype=torch.float32, q_hilo=True, q_gain=z["w"], rope_cos=z["cos"], rope_sin=z["sin"])
+    contract_close(got, z[f"expected_w{window}"], f"golden hilo w={window}")
+    assert np.abs(got - z[f"expected_w{window}"]).max() < 5e-4
+
+
 def config3_inputs(S=1024, theta=1e6, seed=3, H=1536, nH=8, kvH=2, hd=256):
     """h ~ N(0,1) [S][H] projected by f16 Wq/Wk/Wv ~ N(0, 0.02); k/v through the cache write."""
     rng = np.random.default_rng(seed)
@@ -70,16 +107,46 @@ def config3_inputs(S=1024, theta=1e6, seed=3, H=1536, nH=8, kvH=2, hd=256):
 @pytest.mark.parametrize("window,theta", [(0, 1e6), (512, 1e4)])
 def test_config3(window, theta):
     q, qg, k, v, cos, sin = config3_inputs(theta=theta)
-    got = run(q, k, v, 0, sa.AttnConfig(8, 2, 256, window), q_gain=qg, rope_cos=cos, rope_sin=sin)
-    ref = O.prefill_attention(q, k, v, 0, 2, q_gain=qg, cos=cos, sin=sin, window=window)
-    contract_close(got, ref, f"config3 W={window}")
+    cfg = sa.AttnConfig(8, 2, 256, window)
+    check_both_modes(q, k, v, 0, cfg, qg, cos, sin, f"config3 W={window}")
+    # end to end against the oracle's own f16 rounding of q (realistic gains ~N(1, 0.1))
+    got = run(q, k, v, 0, cfg, q_gain=qg, rope_cos=cos, rope_sin=sin)
+    contract_close(got, O.prefill_attention(q, k, v, 0, 2, q_gain=qg, cos=cos, sin=sin, window=window),
+                   f"config3 W={window} e2e")
+
+
+def test_qprep_is_the_prefill_prologue():
+    """prefill(raw q) is bit-identical to prefill(qprep(q)) with the prologue switched off, and
+    qprep's f16 q matches the oracle's rounding except for rare one-ulp boundary cases."""
+    q, qg, k, v, cos, sin = config3_inputs(S=256, seed=11)
+    cfg = sa.AttnConfig(8, 2, 256)
+    a = run(q, k, v, 0, cfg, q_gain=qg, rope_cos=cos, rope_sin=sin)
+    q16 = kernel_q16(q, cfg, qg, cos, sin)
+    b = run(q16.astype(np.float32), k, v, 0, cfg)
+    np.testing.assert_array_equal(a, b)
+    ref = O.apply_rope(O.rms_norm(q, qg), cos[:, None, :], sin[:, None, :]).astype(np.float16)
+    assert (q16 != ref).mean() < 0.01
+    f16_ulp_close(q16, ref, "qprep vs oracle")
+
+
+def test_qprep_b_mirror():
+    rng = np.random.default_rng(2)
+    S, nH, hd, start = 10, 8, 512, 5
+    q = rng.standard_normal((S, nH, hd)).astype(np.float32)
+    w = rng.standard_normal(hd).astype(np.float32)
+    cosT, sinT = O.rope_tables(np.arange(32), hd, 1e6, cutoff=64)
+    qf16 = torch.zeros(S * nH * hd, dtype=torch.float16, device=DEV)
+    sa.qprep_b(t(q.reshape(-1)), t(w), t(cosT), t(sinT), qf16, (start, nH), S=S, head_dim=hd)
+    torch.cuda.synchronize()
+    ref = O.apply_rope(O.rms_norm(q, w), cosT[start:start + S, None, :], sinT[start:start + S, None, :])
+    f16_ulp_close(qf16.cpu().numpy().reshape(S, nH, hd), ref, "qprep_b")
 
 
 @pytest.mark.parametrize("hd", [256, 512])
 @pytest.mark.parametrize("window", [0, 64])
 def test_s300_crosses_tiles_with_srq(hd, window):
     """The reference's attn_prefill check: S = 300 (> one 256-key tile), inputs N(0,1)*0.5,
-    seed 5, nH 8 kvH 1, output srq'd with o_in."""
+    seed 5, nH 8 kvH 1, gain ~N(0,1), output srq'd with o_in."""
     rng = np.random.default_rng(5)
     S, nH = 300, 8
     q = (0.5 * rng.standard_normal((S, nH, hd))).astype(np.float32)
@@ -89,12 +156,13 @@ def test_s300_crosses_tiles_with_srq(hd, window):
     cos, sin = O.rope_tables(np.arange(S), hd, 1e4)
     k, v = O.kv_write(kr, vr, g, cos, sin)
     oq = 0.014886821620166302
+    cfg = sa.AttnConfig(nH, 1, hd, window)
+    ref16, ref32 = check_both_modes(q, k, v, 0, cfg, g, cos, sin, f"S300 hd={hd} W={window}")
     kw = dict(q_gain=g, rope_cos=cos, rope_sin=sin)
-    ref = O.prefill_attention(q, k, v, 0, 1, q_gain=g, cos=cos, sin=sin, window=window)
-    got = run(q, k, v, 0, sa.AttnConfig(nH, 1, hd, window), out_dtype=torch.float32, **kw)
-    contract_close(got, ref, f"S300 hd={hd} W={window}")
-    gq = run(q, k, v, 0, sa.AttnConfig(nH, 1, hd, window, out_q=oq), out_dtype=torch.float32, **kw)
-    srq_close(gq, ref, oq, f"S300 srq hd={hd} W={window}")
+    cq = sa.AttnConfig(nH, 1, hd, window, out_q=oq)
+    srq_close(run(q, k, v, 0, cq, out_dtype=torch.float32, **kw), ref16, oq, f"S300 srq hd={hd} W={window}")
+    srq_close(run(q, k, v, 0, cq, out_dtype=torch.float32, q_hilo=True, **kw), ref32, oq,
+              f"S300 srq hilo hd={hd} W={window}")
 
 
 @pytest.mark.parametrize("S,start,window", [(100, 700, 512), (37, 0, 0), (1, 0, 0), (1, 900, 0),
@@ -111,9 +179,8 @@ def test_continuation_and_ragged(S, start, window, nH, kvH):
     k, v = O.kv_write(k.astype(np.float32), v.astype(np.float32),
                       (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
     cos, sin = O.rope_tables(np.arange(start, T), hd, 1e4)
-    got = run(q, k, v, start, sa.AttnConfig(nH, kvH, hd, window), q_gain=qg, rope_cos=cos, rope_sin=sin)
-    ref = O.prefill_attention(q, k, v, start, kvH, q_gain=qg, cos=cos, sin=sin, window=window)
-    contract_close(got, ref, f"S={S} start={start} W={window} nH={nH} kvH={kvH}")
+    check_both_modes(q, k, v, start, sa.AttnConfig(nH, kvH, hd, window), qg, cos, sin,
+                     f"S={S} start={start} W={window} nH={nH} kvH={kvH}")
 
 
 @pytest.mark.parametrize("S,start", [(300, 0), (200, 100), (64, 447), (1, 0)])
