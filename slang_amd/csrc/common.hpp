@@ -86,4 +86,62 @@ __device__ __forceinline__ half8 load8h(const float* p) {
 __device__ __forceinline__ void store_elem(half_t* p, float v) { *p = (half_t)v; }
 __device__ __forceinline__ void store_elem(float* p, float v) { *p = v; }
 
+// Stand-ins for absent operands, so operand loads never sit behind a null test and
+// can all be issued before any arithmetic: gain 1 (used only when a norm is asked for)
+// and the identity rotation cos 1 / sin 0, which leaves x exactly unchanged.
+#define G4A_ONES8 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f
+#define G4A_ONES64 G4A_ONES8, G4A_ONES8, G4A_ONES8, G4A_ONES8, G4A_ONES8, G4A_ONES8, G4A_ONES8, G4A_ONES8
+__device__ __attribute__((aligned(16))) static const float kOnes[512] = {
+    G4A_ONES64, G4A_ONES64, G4A_ONES64, G4A_ONES64, G4A_ONES64, G4A_ONES64, G4A_ONES64, G4A_ONES64};
+__device__ __attribute__((aligned(16))) static const float kZeros[512] = {};
+
+// q RMSNorm*gain then split-half RoPE for one query row, in the MFMA B-operand layout:
+// the lane of k-group g holds dims 32s + 8g + i (s < hd/32, i < 8), so the RoPE partner
+// d + hd/2 sits in the same lane at step s + hd/64 and the row's sum of squares needs
+// only the two cross-group shuffles. Every operand is loaded before any arithmetic
+// (one memory round trip). `gain` and `cr`/`sr` must be valid: kOnes / kZeros stand in
+// for absent operands; `norm` says whether to normalise at all. Shared by the prefill
+// and qprep kernels, whose lane layouts match, so both round the same values to f16.
+template <int HD>
+__device__ __forceinline__ void prep_q_column(const float* qr, const float* gain, const float* cr,
+                                              const float* sr, bool norm, float eps, int g,
+                                              float (&x)[HD / 32][8]) {
+    constexpr int KSTEPS = HD / 32;
+    float8v gv[KSTEPS], cv[KSTEPS / 2], sv[KSTEPS / 2];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        const float8v v = load8(qr + 32 * s + 8 * g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[s][i] = v[i];
+        gv[s] = load8(gain + 32 * s + 8 * g);
+    }
+#pragma unroll
+    for (int s = 0; s < KSTEPS / 2; ++s) {
+        cv[s] = load8(cr + 32 * s + 8 * g);
+        sv[s] = load8(sr + 32 * s + 8 * g);
+    }
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
+        ss += xor_shfl(ss, 16);
+        ss += xor_shfl(ss, 32);
+        const float den = sqrtf(ss / (float)HD + eps);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[s][i];
+    }
+#pragma unroll
+    for (int s = 0; s < KSTEPS / 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
+            x[s][i] = x0 * cv[s][i] - x1 * sv[s][i];
+            x[s + KSTEPS / 2][i] = x1 * cv[s][i] + x0 * sv[s][i];
+        }
+}
+
 }  // namespace g4a

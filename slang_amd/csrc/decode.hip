@@ -6,14 +6,22 @@
 // online softmax per key chunk, partials (acc, m, l) merged by the last chunk to
 // finish, which also resets its ticket (:1700-1749); GQA hKv = h / (qH / kvH) (:1581).
 //
-// MI355X design (not the reference's): one workgroup per (key split, kv head, sequence)
-// carries ALL query heads of its GQA group, so each K/V row is read from HBM once.
-// Within a workgroup the 4 waves take 16-key blocks round-robin; each wave keeps its
-// own online softmax in registers and the waves are merged through LDS. Each K/V row
-// (hd f16 = 512 B at hd 256) is read by LPK lanes with 16 B loads, so every load
-// instruction moves full 128 B lines; the per-key dot products are reduced with DPP
-// row rotations. Scores live in the log2 domain (q is pre-scaled by scale*log2 e)
-// so the softmax uses exp2.
+// MI355X design (not the reference's):
+//  * One workgroup per (key split, kv head, sequence) carries ALL G query heads of its
+//    GQA group, so each K/V row leaves HBM once. The 4 waves take 16-key blocks in turn.
+//  * Scores on the matrix cores: S^T = K . Q^T with v_mfma_f32_16x16x32_f16. A = 16 keys
+//    of the block straight from HBM (16 B per lane), B = the G query rows split into an
+//    f16 high part (rows 0..G-1) and an f16 low part (rows G..2G-1), so the sum of the
+//    two columns is the f32-accurate score; a DPP row shift adds them.
+//  * P.V on the VALU from V rows loaded with full 128 B lines (MFMA would need V^T);
+//    P reaches the V lanes through a 16xG slice of LDS per wave.
+//  * The first block's K/V loads are issued before the q prologue, so the HBM round
+//    trip overlaps the norm/RoPE work; rows past the split end are clamped to the last
+//    valid row (loaded, then masked), so every load is unconditional.
+//  * Waves merge through LDS; splits merge in the last workgroup to finish (one
+//    agent-scope release per workgroup, one acquire in the merger), which issues all
+//    of its partial loads before it needs them.
+// Scores are in the log2 domain (q carries scale*log2 e), so the softmax uses exp2.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -40,70 +48,76 @@ struct DecodeArgs {
 
 template <int HD, int G>
 struct DecodeShape {
-    static constexpr int LPK0 = G * HD / 64;                  // lanes per key so that q+acc fit
-    static constexpr int LPK = LPK0 < 16 ? 16 : (LPK0 > 64 ? 64 : LPK0);
-    static constexpr int KPS = 64 / LPK;                      // keys per wave step
-    static constexpr int NCH = HD / (8 * LPK);                // 8-element chunks per lane
-    static constexpr int NE = 8 * NCH;                        // elements per lane
-    static constexpr int NS0 = 16 / KPS;
-    static constexpr int NS = (NS0 * G > 32) ? (32 / G) : NS0;  // wave steps per block
-    static constexpr int BK = KPS * NS;                       // keys per wave block
-    static constexpr int LDS_FLOATS = 4 * G * HD;             // wave partials (aliases q)
+    static constexpr int KSTEPS = HD / 32;        // MFMA k-steps per 16-key tile
+    static constexpr int VLANES = HD / 8;         // lanes per V row (8 dims, 16 B each)
+    static constexpr int VROWS = 64 / VLANES;     // V rows per load instruction
+    static constexpr int VLOADS = 16 / VROWS;     // V load instructions per 16-key block
+    static constexpr int LDS_FLOATS = 4 * G * HD; // wave partials
 };
 
-template <int LPK>
-__device__ __forceinline__ float key_sum(float x) {
-    x = row16_sum(x);
-    if constexpr (LPK >= 32) x += xor_shfl(x, 16);
-    if constexpr (LPK >= 64) x += xor_shfl(x, 32);
-    return x;
+__device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// reduce across the 64/LPK rows of a wave (lanes holding different keys)
-template <int LPK>
-__device__ __forceinline__ float rows_max(float x) {
-    if constexpr (LPK <= 16) x = fmaxf(x, xor_shfl(x, 16));
-    if constexpr (LPK <= 32) x = fmaxf(x, xor_shfl(x, 32));
-    return x;
-}
-template <int LPK>
-__device__ __forceinline__ float rows_sum(float x) {
-    if constexpr (LPK <= 16) x += xor_shfl(x, 16);
-    if constexpr (LPK <= 32) x += xor_shfl(x, 32);
-    return x;
-}
-
+// K chunk of 8 dims as the f16 MFMA operand; f32 caches are split into high and low
+// f16 parts so the score keeps f32 accuracy (the reference's own cache type).
 template <typename KVT>
-struct RawChunk;
+struct KOp;
 template <>
-struct RawChunk<half_t> {
-    typedef half8 type;
+struct KOp<half_t> {
+    struct raw { half8 h; };
+    static __device__ __forceinline__ raw load(const half_t* p) { return raw{*reinterpret_cast<const half8*>(p)}; }
+    static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16(k.h, q, c); }
+};
+template <>
+struct KOp<float> {
+    struct raw { float8v f; };
+    static __device__ __forceinline__ raw load(const float* p) { return raw{load8(p)}; }
+    static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) {
+        const half8 hi = __builtin_convertvector(k.f, half8);
+        const half8 lo = __builtin_convertvector(k.f - __builtin_convertvector(hi, float8v), half8);
+        return mfma16(lo, q, mfma16(hi, q, c));
+    }
+};
+template <typename KVT>
+struct VOp;
+template <>
+struct VOp<half_t> {
+    typedef half8 raw;
     static __device__ __forceinline__ half8 load(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
-    static __device__ __forceinline__ half8 zero() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
     static __device__ __forceinline__ float8v cvt(half8 h) { return __builtin_convertvector(h, float8v); }
 };
 template <>
-struct RawChunk<float> {
-    typedef float8v type;
+struct VOp<float> {
+    typedef float8v raw;
     static __device__ __forceinline__ float8v load(const float* p) { return load8(p); }
-    static __device__ __forceinline__ float8v zero() { return float8v{0, 0, 0, 0, 0, 0, 0, 0}; }
     static __device__ __forceinline__ float8v cvt(float8v f) { return f; }
 };
+
+// lane n of each 16-lane row reads lane n+N of the same row
+template <int N>
+__device__ __forceinline__ float dpp_row_shl(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + N, 0xF, 0xF, false));
+}
 
 template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     using Sh = DecodeShape<HD, G>;
-    constexpr int LPK = Sh::LPK, KPS = Sh::KPS, NCH = Sh::NCH, NE = Sh::NE, NS = Sh::NS, BK = Sh::BK;
-    using RC = RawChunk<KVT>;
-    typedef typename RC::type raw_t;
+    constexpr int KSTEPS = Sh::KSTEPS, VLANES = Sh::VLANES, VROWS = Sh::VROWS, VLOADS = Sh::VLOADS;
+    using KO = KOp<KVT>;
+    using VO = VOp<KVT>;
+    typedef typename KO::raw kraw_t;
+    typedef typename VO::raw vraw_t;
 
-    __shared__ __attribute__((aligned(16))) float lds[Sh::LDS_FLOATS];  // [4][G][HD] wave partials; q at start
+    __shared__ __attribute__((aligned(16))) float lds[Sh::LDS_FLOATS];  // wave partials / merge weights
+    __shared__ __attribute__((aligned(16))) float lds_p[4][16][G];      // P of the current block, per wave
     __shared__ float lds_m[4][G], lds_l[4][G];
     __shared__ float s_M[G], s_L[G];
     __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane / LPK, c = lane % LPK;
+    const int n = lane & 15, g = lane >> 4;
     const int ci = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pair = b * a.n_kv_heads + kh;
 
@@ -127,163 +141,173 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     const int k0 = lo + ci * chunk;
     const int k1 = min(k0 + chunk, hi);
 
-    // ---- q prologue: RMSNorm*gain, RoPE, scale*log2e, into LDS [G][HD]
-    {
-        const float* qb = a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
-        constexpr int PER = HD / 64;
-        for (int hh = wave; hh < G; hh += 4) {
-            float x[PER];
+    // ---- block loads: K in the MFMA A layout (lane n,g: key n, dims 32s+8g..), V rows
+    const size_t rstride = (size_t)a.n_kv_heads * HD;
+    const KVT* kbase = reinterpret_cast<const KVT*>(a.kc) + (size_t)b * a.seq_stride + (size_t)kh * HD + 8 * g;
+    const KVT* vbase = reinterpret_cast<const KVT*>(a.vc) + (size_t)b * a.seq_stride + (size_t)kh * HD +
+                       8 * (lane % VLANES);
+    const int vrow = lane / VLANES;
+    kraw_t kr[KSTEPS];
+    vraw_t vr[VLOADS];
+    auto load_block = [&](int blk) {
+        const int kk = min(blk + n, k1 - 1);
 #pragma unroll
-            for (int m = 0; m < PER; ++m) x[m] = qb[hh * HD + lane + 64 * m];
-            if (a.q_gain) {
-                float ss = 0.0f;
+        for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::load(kbase + (size_t)kk * rstride + 32 * s);
 #pragma unroll
-                for (int m = 0; m < PER; ++m) ss += x[m] * x[m];
-                ss = wave_sum(ss);
-                const float den = sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-                for (int m = 0; m < PER; ++m) x[m] = x[m] / den * a.q_gain[lane + 64 * m];
-            }
-            if (a.rcos) {
-                const float* cs = a.rcos + (size_t)b * (HD / 2);
-                const float* sn = a.rsin + (size_t)b * (HD / 2);
-#pragma unroll
-                for (int m = 0; m < PER / 2; ++m) {
-                    const int d = lane + 64 * m;
-                    const float x0 = x[m], x1 = x[m + PER / 2];
-                    x[m] = x0 * cs[d] - x1 * sn[d];
-                    x[m + PER / 2] = x1 * cs[d] + x0 * sn[d];
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < PER; ++m) lds[hh * HD + lane + 64 * m] = x[m] * a.scale_log2;
+        for (int i = 0; i < VLOADS; ++i) {
+            const int kv = min(blk + VROWS * i + vrow, k1 - 1);
+            vr[i] = VO::load(vbase + (size_t)kv * rstride);
         }
+    };
+    int blk = k0 + wave * 16;
+    if (blk < k1) load_block(blk);  // in flight during the q prologue
+
+    // ---- q prologue. The G query rows, the gain and this sequence's cos/sin rows are
+    // staged through LDS with one coalesced request per thread (all in flight together
+    // with the K/V block above). Then rows n < G of the MFMA B operand take the high f16
+    // part of head n, rows G..2G-1 the low part, rows >= 2G zero.
+    half8 qop[KSTEPS];
+    {
+        float* sq = lds;                 // [G][HD] q, then [HD] gain, [HD/2] cos, [HD/2] sin
+        float* sg = lds + G * HD;
+        float* sc_ = sg + HD;
+        float* ss_ = sc_ + HD / 2;
+        const float4* q4 = reinterpret_cast<const float4*>(a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD);
+        const float4* g4 = reinterpret_cast<const float4*>(a.q_gain ? a.q_gain : kOnes);
+        const float4* c4p = reinterpret_cast<const float4*>(a.rcos ? a.rcos + (size_t)b * (HD / 2) : kOnes);
+        const float4* s4p = reinterpret_cast<const float4*>(a.rsin ? a.rsin + (size_t)b * (HD / 2) : kZeros);
+        constexpr int NQ4 = G * HD / 4, NT4 = NQ4 + HD / 4 + HD / 4;
+        float4 st[(NT4 + 255) / 256];
+#pragma unroll
+        for (int u = 0; u < (NT4 + 255) / 256; ++u) {
+            const int idx = tid + 256 * u;
+            if (idx < NQ4) st[u] = q4[idx];
+            else if (idx < NQ4 + HD / 4) st[u] = g4[idx - NQ4];
+            else if (idx < NQ4 + HD / 4 + HD / 8) st[u] = c4p[idx - NQ4 - HD / 4];
+            else if (idx < NT4) st[u] = s4p[idx - NQ4 - HD / 4 - HD / 8];
+        }
+#pragma unroll
+        for (int u = 0; u < (NT4 + 255) / 256; ++u)
+            if (tid + 256 * u < NT4) reinterpret_cast<float4*>(sq)[tid + 256 * u] = st[u];
+        __syncthreads();
+        const int h = (n < 2 * G) ? (n % G) : 0;
+        float x[KSTEPS][8];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = sq[h * HD + 32 * s + 8 * g + i];
+        if (a.q_gain) {
+            float ssum = 0.0f;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ssum += x[s][i] * x[s][i];
+            ssum += xor_shfl(ssum, 16);
+            ssum += xor_shfl(ssum, 32);
+            const float den = sqrtf(ssum / (float)HD + a.eps);
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * sg[32 * s + 8 * g + i];
+        }
+#pragma unroll
+        for (int s = 0; s < KSTEPS / 2; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int d = 32 * s + 8 * g + i;
+                const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
+                x[s][i] = x0 * sc_[d] - x1 * ss_[d];
+                x[s + KSTEPS / 2][i] = x1 * sc_[d] + x0 * ss_[d];
+            }
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = x[s][i] * a.scale_log2;
+                const half_t vh = (half_t)v;
+                qop[s][i] = n < G ? vh : (n < 2 * G ? (half_t)(v - (float)vh) : (half_t)0.0f);
+            }
+        __syncthreads();  // the staging area is reused for the wave partials
     }
-    __syncthreads();
-    float qv[G][NE];
+
+    // ---- main loop: per wave, 16-key blocks with an online softmax
+    float m_run = kNegInf, l_run = 0.0f;  // head n (lanes n < G)
+    float acc[G][8];                      // O[h][8 dims of this lane's V column]
 #pragma unroll
     for (int hh = 0; hh < G; ++hh)
 #pragma unroll
-        for (int j = 0; j < NCH; ++j)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qv[hh][8 * j + i] = lds[hh * HD + 8 * LPK * j + 8 * c + i];
-    __syncthreads();  // the q region is reused for the wave partials below
+        for (int j = 0; j < 8; ++j) acc[hh][j] = 0.0f;
 
-    // ---- main loop: 16-key-ish blocks per wave, online softmax in registers
-    const int rstride = a.n_kv_heads * HD;
-    const KVT* kbase = reinterpret_cast<const KVT*>(a.kc) + (size_t)b * a.seq_stride + (size_t)kh * HD + 8 * c;
-    const KVT* vbase = reinterpret_cast<const KVT*>(a.vc) + (size_t)b * a.seq_stride + (size_t)kh * HD + 8 * c;
-
-    float m_run[G], l_run[G], acc[G][NE];
+    for (; blk < k1; blk += 64) {
+        float4v c4 = float4v{0, 0, 0, 0};
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-        m_run[hh] = kNegInf;
-        l_run[hh] = 0.0f;
+        for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
+        float sc[4], mloc = kNegInf;
 #pragma unroll
-        for (int e = 0; e < NE; ++e) acc[hh][e] = 0.0f;
-    }
-
-    // K/V of the next block are loaded while the current one is processed
-    raw_t kr[NS][NCH], vr[NS][NCH];
-    auto load_block = [&](int blk, raw_t (&kk)[NS][NCH], raw_t (&vv)[NS][NCH]) {
-#pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            const int key = blk + t * KPS + r;
-            const bool ok = key < k1;
-#pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-                const size_t off = (size_t)key * rstride + 8 * LPK * j;
-                kk[t][j] = ok ? RC::load(kbase + off) : RC::zero();
-                vv[t][j] = ok ? RC::load(vbase + off) : RC::zero();
-            }
+        for (int i = 0; i < 4; ++i) {
+            const float v = c4[i] + dpp_row_shl<G>(c4[i]);  // high + low column
+            sc[i] = (blk + 4 * g + i < k1) ? v : kNegInf;
+            mloc = fmaxf(mloc, sc[i]);
         }
-    };
-    int blk = k0 + wave * BK;
-    if (blk < k1) load_block(blk, kr, vr);
-    for (; blk < k1; blk += 4 * BK) {
-        raw_t kn[NS][NCH], vn[NS][NCH];
-        load_block(blk + 4 * BK, kn, vn);  // keys >= k1 load nothing
-        float s[NS][G];
+        mloc = fmaxf(mloc, xor_shfl(mloc, 16));
+        mloc = fmaxf(mloc, xor_shfl(mloc, 32));
+        const float m_new = fmaxf(m_run, mloc);  // finite: key blk is valid
+        const float corr = exp2f(m_run - m_new);
+        float ps = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            float part[G];
-#pragma unroll
-            for (int hh = 0; hh < G; ++hh) part[hh] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-                const float8v kf = RC::cvt(kr[t][j]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-#pragma unroll
-                    for (int hh = 0; hh < G; ++hh) part[hh] = fmaf(qv[hh][8 * j + i], kf[i], part[hh]);
-            }
-            const bool ok = blk + t * KPS + r < k1;
-#pragma unroll
-            for (int hh = 0; hh < G; ++hh) {
-                const float v = key_sum<LPK>(part[hh]);
-                s[t][hh] = ok ? v : kNegInf;
-            }
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = exp2f(sc[i] - m_new);
+            ps += sc[i];
         }
+        l_run = l_run * corr + ps;
+        m_run = m_new;
+        if (n < G) {
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-            float mb = s[0][hh];
-#pragma unroll
-            for (int t = 1; t < NS; ++t) mb = fmaxf(mb, s[t][hh]);
-            mb = rows_max<LPK>(mb);
-            const float m_new = fmaxf(m_run[hh], mb);  // finite: key blk is always valid
-            const float corr = exp2f(m_run[hh] - m_new);
-            float ps = 0.0f;
-#pragma unroll
-            for (int t = 0; t < NS; ++t) {
-                s[t][hh] = exp2f(s[t][hh] - m_new);
-                ps += s[t][hh];
-            }
-            l_run[hh] = l_run[hh] * corr + ps;
-            m_run[hh] = m_new;
-#pragma unroll
-            for (int e = 0; e < NE; ++e) acc[hh][e] *= corr;
+            for (int i = 0; i < 4; ++i) lds_p[wave][4 * g + i][n] = sc[i];
         }
+        float cr[G];
 #pragma unroll
-        for (int t = 0; t < NS; ++t)
+        for (int hh = 0; hh < G; ++hh) cr[hh] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), hh));
+        vraw_t vcur[VLOADS];
 #pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-                const float8v vf = RC::cvt(vr[t][j]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-#pragma unroll
-                    for (int hh = 0; hh < G; ++hh) acc[hh][8 * j + i] = fmaf(s[t][hh], vf[i], acc[hh][8 * j + i]);
-            }
-#pragma unroll
-        for (int t = 0; t < NS; ++t)
-#pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-                kr[t][j] = kn[t][j];
-                vr[t][j] = vn[t][j];
-            }
-    }
-
-    // ---- wave partial: sum over rows (lanes with different keys), then to LDS
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-        l_run[hh] = rows_sum<LPK>(l_run[hh]);
-#pragma unroll
-        for (int e = 0; e < NE; ++e) acc[hh][e] = rows_sum<LPK>(acc[hh][e]);
-    }
-    if (r == 0) {
+        for (int i = 0; i < VLOADS; ++i) vcur[i] = vr[i];
+        if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during P.V
 #pragma unroll
         for (int hh = 0; hh < G; ++hh)
 #pragma unroll
-            for (int j = 0; j < NCH; ++j)
+            for (int j = 0; j < 8; ++j) acc[hh][j] *= cr[hh];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    lds[(wave * G + hh) * HD + 8 * LPK * j + 8 * c + i] = acc[hh][8 * j + i];
-    }
-    if (lane == 0) {
+        for (int i = 0; i < VLOADS; ++i) {
+            const float8v vf = VO::cvt(vcur[i]);
+            const float* pr = &lds_p[wave][VROWS * i + vrow][0];
+            float p[G];
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-            lds_m[wave][hh] = m_run[hh];
-            lds_l[wave][hh] = l_run[hh];
+            for (int hh = 0; hh < G; ++hh) p[hh] = pr[hh];
+#pragma unroll
+            for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[hh][j] = fmaf(p[hh], vf[j], acc[hh][j]);
         }
+    }
+
+    // ---- wave partial: rows of the same V column summed, then to LDS
+    l_run += xor_shfl(l_run, 16);
+    l_run += xor_shfl(l_run, 32);
+    if constexpr (VROWS == 2) {
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[hh][j] += xor_shfl(acc[hh][j], 32);
+    }
+    if (lane < VLANES) {
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lds[(wave * G + hh) * HD + 8 * lane + j] = acc[hh][j];
+    }
+    if (lane < G) {
+        lds_m[wave][lane] = m_run;
+        lds_l[wave][lane] = l_run;
     }
     __syncthreads();
     if (tid < G) {
@@ -312,64 +336,74 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     if (single) return;
     if (tid < G) a.part_ml[((size_t)pair * a.max_splits + ci) * G + tid] = make_float2(s_M[tid], s_L[tid]);
 
-    // ---- publish, take a ticket; the last split of the pair merges all partials
-    __threadfence();
+    // ---- publish, take a ticket; the last split of the pair merges all partials.
+    // The barrier completes every wave's partial stores; one agent-scope release by
+    // thread 0 then makes them visible beyond this XCD's L2, and only the last
+    // arriver pays the acquire before reading the other splits' partials.
     __syncthreads();
     if (tid == 0) {
-        const uint32_t t = __hip_atomic_fetch_add(a.tickets + pair, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (t == (uint32_t)(n_act - 1));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const uint32_t t = __hip_atomic_fetch_add(a.tickets + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = (t == (uint32_t)(n_act - 1));
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __hip_atomic_store(a.tickets + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_last = last;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    if (tid == 0) __hip_atomic_store(a.tickets + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    // per-head global max / weights / denominator; weights in LDS [G][n_act]
-    float* wts = lds;  // n_act <= max_splits <= 256
+    // Each thread owns 4 consecutive outputs (float4) and streams the splits 16 at a time.
+    // Loads are unconditional (split index clamped; weights of the padding are 0), and the
+    // first batch is requested before the weights are computed.
+    constexpr int STRIDE4 = G * HD / 4;
+    const float4* pob4 = reinterpret_cast<const float4*>(a.part_o + (size_t)pair * a.max_splits * (G * HD));
     const float2* ml = a.part_ml + (size_t)pair * a.max_splits * G;
+    float* wts = lds;  // [G][256]; n_act <= max_splits <= 256
+    float4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(u, n_act - 1) * STRIDE4 + tid];
+    const int n_pad = (n_act + 15) & ~15;
     for (int hh = wave; hh < G; hh += 4) {
         float mloc = kNegInf;
         for (int t = lane; t < n_act; t += 64) mloc = fmaxf(mloc, ml[t * G + hh].x);
         const float M = wave_max(mloc);
         float lsum = 0.0f;
-        for (int t = lane; t < n_act; t += 64) {
-            const float2 v = ml[t * G + hh];
-            const float w = exp2f(v.x - M);
+        for (int t = lane; t < n_pad; t += 64) {
+            float w = 0.0f;
+            if (t < n_act) {
+                const float2 w2 = ml[t * G + hh];
+                w = exp2f(w2.x - M);
+                lsum += w2.y * w;
+            }
             wts[hh * 256 + t] = w;
-            lsum += v.y * w;
         }
         lsum = wave_sum(lsum);
         if (lane == 0) s_L[hh] = lsum;
     }
     __syncthreads();
-    // each thread owns 4 consecutive outputs and streams the splits 16 at a time
-    const float4* pob4 = reinterpret_cast<const float4*>(a.part_o + (size_t)pair * a.max_splits * (G * HD));
-    constexpr int STRIDE4 = G * HD / 4;
     for (int e4 = tid; e4 < STRIDE4; e4 += 256) {
+        if (e4 != tid) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(u, n_act - 1) * STRIDE4 + e4];
+        }
         const int hh = (4 * e4) / HD;
         const float* wh = wts + hh * 256;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        int t = 0;
-        for (; t + 16 <= n_act; t += 16) {
-            float4 v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)(t + u) * STRIDE4 + e4];
+        for (int t0 = 0;;) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                const float w = wh[t + u];
+                const float w = wh[t0 + u];
                 o.x = fmaf(w, v[u].x, o.x);
                 o.y = fmaf(w, v[u].y, o.y);
                 o.z = fmaf(w, v[u].z, o.z);
                 o.w = fmaf(w, v[u].w, o.w);
             }
-        }
-        for (; t < n_act; ++t) {
-            const float4 v = pob4[(size_t)t * STRIDE4 + e4];
-            const float w = wh[t];
-            o.x = fmaf(w, v.x, o.x);
-            o.y = fmaf(w, v.y, o.y);
-            o.z = fmaf(w, v.z, o.z);
-            o.w = fmaf(w, v.w, o.w);
+            t0 += 16;
+            if (t0 >= n_act) break;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(t0 + u, n_act - 1) * STRIDE4 + e4];
         }
         const float L = s_L[hh];
         float* op = outp + 4 * e4;
@@ -475,9 +509,10 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     }
     const bool f32 = (cfg->flags & G4A_KV_F32) != 0;
     const size_t esz = f32 ? 4 : 2;
-    if (((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 || ((uintptr_t)q % 4) ||
+    if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)out) % 16 ||
+        (q_gain && (uintptr_t)q_gain % 16) || (rope_cos && ((uintptr_t)rope_cos | (uintptr_t)rope_sin) % 16) ||
         (seq_stride * esz) % 16) {
-        set_error("k_cache/v_cache and seq_stride*elem_size must be 16-byte aligned");
+        set_error("q, q_gain, rope tables, caches, out and seq_stride*elem_size must be 16-byte aligned");
         return G4A_EINVAL;
     }
     if (n_seq > 1 && seq_stride < (int64_t)cfg->n_kv_heads * HD) {

@@ -49,52 +49,6 @@ __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// q RMSNorm*gain then split-half RoPE for one query row, in the MFMA B-operand layout:
-// the lane of k-group g holds dims 32s + 8g + i (s < hd/32, i < 8), so the RoPE partner
-// d + hd/2 sits in the same lane at step s + hd/64 and the row's sum of squares needs
-// only the two cross-group shuffles. Shared by g4a_prefill and g4a_qprep, whose lane
-// layouts match, so both round the same f32 values to f16.
-template <int HD>
-__device__ __forceinline__ void prep_q_column(const float* qr, const float* gain, const float* cr,
-                                              const float* sr, float eps, int g, float (&x)[HD / 32][8]) {
-    constexpr int KSTEPS = HD / 32;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-        const float8v v = load8(qr + 32 * s + 8 * g);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[s][i] = v[i];
-    }
-    if (gain) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
-        ss += xor_shfl(ss, 16);
-        ss += xor_shfl(ss, 32);
-        const float den = sqrtf(ss / (float)HD + eps);
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            const float8v gv = load8(gain + 32 * s + 8 * g);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[i];
-        }
-    }
-    if (cr) {
-#pragma unroll
-        for (int s = 0; s < KSTEPS / 2; ++s) {
-            const float8v cv = load8(cr + 32 * s + 8 * g);
-            const float8v sv = load8(sr + 32 * s + 8 * g);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
-                x[s][i] = x0 * cv[i] - x1 * sv[i];
-                x[s + KSTEPS / 2][i] = x1 * cv[i] + x0 * sv[i];
-            }
-        }
-    }
-}
-
 // qprep_b (kernels_dsl.py:1837-1873): q RMSNorm*gain + RoPE for S*nH rows, stored f16.
 // A wave handles 16 rows with the same lane layout as the prefill prologue.
 template <int HD>
@@ -108,8 +62,8 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
     const int rr = ok ? row : rows - 1;
     const int s_idx = rr / n_q_heads;
     float x[KSTEPS][8];
-    prep_q_column<HD>(q + (size_t)rr * HD, gain, rcos ? rcos + (size_t)s_idx * (HD / 2) : nullptr,
-                      rsin ? rsin + (size_t)s_idx * (HD / 2) : nullptr, eps, g, x);
+    prep_q_column<HD>(q + (size_t)rr * HD, gain ? gain : kOnes, rcos ? rcos + (size_t)s_idx * (HD / 2) : kOnes,
+                      rsin ? rsin + (size_t)s_idx * (HD / 2) : kZeros, gain != nullptr, eps, g, x);
     if (!ok) return;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
@@ -149,9 +103,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     half8 qf[KSTEPS], ql[HILO ? KSTEPS : 1];
     {
         float x[KSTEPS][8];
-        prep_q_column<HD>(a.q + ((size_t)s_idx * a.n_q_heads + h) * HD, a.q_gain,
-                          a.rcos ? a.rcos + (size_t)s_idx * (HD / 2) : nullptr,
-                          a.rsin ? a.rsin + (size_t)s_idx * (HD / 2) : nullptr, a.eps, g, x);
+        prep_q_column<HD>(a.q + ((size_t)s_idx * a.n_q_heads + h) * HD, a.q_gain ? a.q_gain : kOnes,
+                          a.rcos ? a.rcos + (size_t)s_idx * (HD / 2) : kOnes,
+                          a.rsin ? a.rsin + (size_t)s_idx * (HD / 2) : kZeros, a.q_gain != nullptr, a.eps, g, x);
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
