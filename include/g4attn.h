@@ -81,10 +81,10 @@ int g4a_version(void);
  *   rope_cos/sin f32 [n_seq][head_dim/2] for each query's position, or NULL (no RoPE).
  *   k_cache/v_cache sequence s at base + s*seq_stride elements, rows [pos][kvH][hd].
  *   out         f32 [n_seq][n_q_heads][head_dim] (srq'd with out_q when nonzero).
- *   ws          workspace of at least g4a_decode_ws_bytes() bytes, zero-filled ONCE
- *               before first use (as the reference zeroes `partials` at setup,
- *               runner.py:367-371); every call leaves its ticket counters at zero
- *               again (kernels_dsl.py:1714-1715). Concurrent calls need distinct ws.
+ *   ws          workspace of at least g4a_decode_ws_bytes() bytes (256-byte aligned) for
+ *               the split partials (acc, m, l) that attn_101 keeps in `partials`; it needs
+ *               no initialisation. Long sequences are split over workgroups and merged by a
+ *               second kernel on the same stream. Concurrent calls need distinct ws.
  */
 size_t g4a_decode_ws_bytes(const g4a_cfg* cfg, int n_seq, int max_key_len);
 int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,

@@ -82,11 +82,10 @@ def rope_tables(positions, head_dim: int, theta: float, cutoff: int | None = Non
 
 
 class DecodeWorkspace:
-    """Split-KV partials + ticket counters for ``decode`` (the reference's `partials`).
+    """Split-KV partials for ``decode`` (the reference's `partials` buffer, runner.py:367-371).
 
-    Zero-filled once at allocation (runner.py:367-371); each call leaves the
-    tickets at zero for the next one (kernels_dsl.py:1714-1715). Grows on demand.
-    Calls that may run concurrently need separate workspaces.
+    Grows on demand; needs no initialisation. Calls that may run concurrently
+    need separate workspaces.
     """
 
     def __init__(self, device="cuda"):
@@ -95,7 +94,7 @@ class DecodeWorkspace:
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self.buf
 
 

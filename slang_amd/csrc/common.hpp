@@ -39,24 +39,37 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-__device__ __forceinline__ float xor_shfl(float x, int m) { return __shfl_xor(x, m, 64); }
-
-__device__ __forceinline__ float wave_sum(float x) {
-    x = row16_sum(x);
-    x += xor_shfl(x, 16);
-    x += xor_shfl(x, 32);
-    return x;
+// Cross-row exchange with gfx950's v_permlane16/32_swap (one VALU op, no LDS crossbar).
+// Swapping x with itself returns the pair {x[lane], x[lane ^ 16]} (resp. ^ 32) in the same
+// order in both partner lanes, so op(pair) is an exact, lane-consistent reduction step.
+__device__ __forceinline__ float2 pair16(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return make_float2(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
 }
+__device__ __forceinline__ float2 pair32(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return make_float2(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+}
+__device__ __forceinline__ float add16(float x) { const float2 p = pair16(x); return p.x + p.y; }
+__device__ __forceinline__ float add32(float x) { const float2 p = pair32(x); return p.x + p.y; }
+__device__ __forceinline__ float max16(float x) { const float2 p = pair16(x); return fmaxf(p.x, p.y); }
+__device__ __forceinline__ float max32(float x) { const float2 p = pair32(x); return fmaxf(p.x, p.y); }
+
+__device__ __forceinline__ float wave_sum(float x) { return add32(add16(row16_sum(x))); }
 
 __device__ __forceinline__ float wave_max(float x) {
     x = fmaxf(x, dpp_ror<8>(x));
     x = fmaxf(x, dpp_ror<4>(x));
     x = fmaxf(x, dpp_ror<2>(x));
     x = fmaxf(x, dpp_ror<1>(x));
-    x = fmaxf(x, xor_shfl(x, 16));
-    x = fmaxf(x, xor_shfl(x, 32));
-    return x;
+    return max32(max16(x));
 }
+
+// 2^x on the transcendental unit (v_exp_f32); 2^-inf = 0. Results below 2^-126 flush to
+// zero, which a softmax weight relative to the running maximum can afford.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------- numerics
 // Static-range quantisation, identity when s == 0 (gemma4_150/reference.py:30-31).
@@ -126,13 +139,12 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
             for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
-        ss += xor_shfl(ss, 16);
-        ss += xor_shfl(ss, 32);
-        const float den = sqrtf(ss / (float)HD + eps);
+        ss = add32(add16(ss));
+        const float rs = 1.0f / sqrtf(ss / (float)HD + eps);  // x * rs * w, as the reference kernels
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * gv[s][i];
+            for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rs * gv[s][i];
     }
 #pragma unroll
     for (int s = 0; s < KSTEPS / 2; ++s)

@@ -9,18 +9,26 @@
 // MI355X design (not the reference's):
 //  * One workgroup per (key split, kv head, sequence) carries ALL G query heads of its
 //    GQA group, so each K/V row leaves HBM once. The 4 waves take 16-key blocks in turn.
-//  * Scores on the matrix cores: S^T = K . Q^T with v_mfma_f32_16x16x32_f16. A = 16 keys
-//    of the block straight from HBM (16 B per lane), B = the G query rows split into an
-//    f16 high part (rows 0..G-1) and an f16 low part (rows G..2G-1), so the sum of the
-//    two columns is the f32-accurate score; a DPP row shift adds them.
-//  * P.V on the VALU from V rows loaded with full 128 B lines (MFMA would need V^T);
-//    P reaches the V lanes through a 16xG slice of LDS per wave.
-//  * The first block's K/V loads are issued before the q prologue, so the HBM round
-//    trip overlaps the norm/RoPE work; rows past the split end are clamped to the last
-//    valid row (loaded, then masked), so every load is unconditional.
-//  * Waves merge through LDS; splits merge in the last workgroup to finish (one
-//    agent-scope release per workgroup, one acquire in the merger), which issues all
-//    of its partial loads before it needs them.
+//  * Both products on the matrix cores, transposed so that no data moves between them:
+//    S^T = K . Q^T (v_mfma_f32_16x16x32_f16; A = 16 keys straight from HBM, B = the query
+//    rows, f16 high parts in rows 0..G-1 and low parts in rows G..2G-1, so high + low
+//    column is the f32-accurate score), then O^T += V^T . P^T (v_mfma_f32_16x16x16_f16).
+//    The S^T accumulator layout (lane n,g: keys 4g..4g+3 of column n) is exactly the
+//    P^T B-operand layout, and V^T comes from a row-major LDS copy of the block through
+//    ds_read_tr16_b64, so P never leaves registers and V is never transposed in memory.
+//  * q RMSNorm/RoPE/split is done once per workgroup (one wave per head), its operand
+//    loads issued at kernel entry together with the first block's K/V.
+//  * Software pipeline without extra registers: once the score MFMAs consumed the K
+//    registers and V sits in LDS, the next block's loads reuse both register sets.
+//  * Rows past the split end are clamped to the last valid row (loaded, then masked),
+//    so every load is unconditional.
+//  * Waves merge through LDS. Splits merge in a second, wide kernel (decode_merge_kernel):
+//    the kernel boundary publishes the partials, so no workgroup pays a cache-writeback
+//    fence or a ticket round trip, and the merge of one (sequence, kv head) is spread over
+//    HD/16 workgroups whose threads load all of their splits in one batch. (A last-arriver
+//    merge inside this kernel, as attn_101 does, measured 2-4x slower on MI355X: its
+//    agent-scope release has to write back the XCD's L2 and the merger then walks every
+//    partial serially.)
 // Scores are in the log2 domain (q carries scale*log2 e), so the softmax uses exp2.
 #include <stdio.h>
 #include <stdlib.h>
@@ -39,7 +47,6 @@ struct DecodeArgs {
     const void* vc;
     int64_t seq_stride;
     float* out;
-    uint32_t* tickets;  // [pairs]
     float2* part_ml;    // [pairs][max_splits][G] (m, l)
     float* part_o;      // [pairs][max_splits][G][HD]
     int n_q_heads, n_kv_heads, window, max_splits, chunk;
@@ -48,15 +55,33 @@ struct DecodeArgs {
 
 template <int HD, int G>
 struct DecodeShape {
-    static constexpr int KSTEPS = HD / 32;        // MFMA k-steps per 16-key tile
-    static constexpr int VLANES = HD / 8;         // lanes per V row (8 dims, 16 B each)
-    static constexpr int VROWS = 64 / VLANES;     // V rows per load instruction
-    static constexpr int VLOADS = 16 / VROWS;     // V load instructions per 16-key block
-    static constexpr int LDS_FLOATS = 4 * G * HD; // wave partials
+    static constexpr int KSTEPS = HD / 32;         // score MFMA k-steps per 16-key block
+    static constexpr int NDT = HD / 16;            // 16-dim output tiles
+    static constexpr int VLANES = HD / 8;          // lanes per V row (8 dims, 16 B each)
+    static constexpr int VROWS = 64 / VLANES;      // V rows per load instruction
+    static constexpr int VLOADS = 16 / VROWS;      // V load instructions per block
+    static constexpr int VSTR = HD + 16;           // LDS V row stride (halves): tr reads conflict-free
+    static constexpr int QSTR = HD + 8;            // LDS q row stride (halves)
+    static constexpr int V_HALVES = 4 * 16 * VSTR; // per-wave V blocks
+    static constexpr int Q_HALVES = 2 * G * QSTR;  // high rows then low rows
+    static constexpr int PART_FLOATS = 4 * G * HD; // wave partials / merge weights
+    static constexpr int LDS_BYTES_A = V_HALVES * 2 > Q_HALVES * 2 ? V_HALVES * 2 : Q_HALVES * 2;
+    static constexpr int LDS_BYTES = LDS_BYTES_A > PART_FLOATS * 4 ? LDS_BYTES_A : PART_FLOATS * 4;
 };
 
-__device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
+__device__ __forceinline__ float4v mfma16x32(half8 a, half8 b, float4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float4v mfma16x16(half4 a, half4 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// 4 halves of column n of a row-major LDS tile, transposed across each 16-lane group:
+// lane n of the group receives element n%4 of the chunks of lanes n/4 + 4j (j < 4).
+__device__ __forceinline__ half4 lds_read_tr16(const half_t* p) {
+    typedef short short4_ __attribute__((ext_vector_type(4)));
+    const short4_ t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_*)(p));
+    return __builtin_bit_cast(half4, t);
 }
 
 // K chunk of 8 dims as the f16 MFMA operand; f32 caches are split into high and low
@@ -67,7 +92,7 @@ template <>
 struct KOp<half_t> {
     struct raw { half8 h; };
     static __device__ __forceinline__ raw load(const half_t* p) { return raw{*reinterpret_cast<const half8*>(p)}; }
-    static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16(k.h, q, c); }
+    static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16x32(k.h, q, c); }
 };
 template <>
 struct KOp<float> {
@@ -76,22 +101,23 @@ struct KOp<float> {
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) {
         const half8 hi = __builtin_convertvector(k.f, half8);
         const half8 lo = __builtin_convertvector(k.f - __builtin_convertvector(hi, float8v), half8);
-        return mfma16(lo, q, mfma16(hi, q, c));
+        return mfma16x32(lo, q, mfma16x32(hi, q, c));
     }
 };
+// V chunk of 8 dims, stored to LDS as f16 (f32 caches are rounded, as srqh_b does).
 template <typename KVT>
 struct VOp;
 template <>
 struct VOp<half_t> {
     typedef half8 raw;
     static __device__ __forceinline__ half8 load(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
-    static __device__ __forceinline__ float8v cvt(half8 h) { return __builtin_convertvector(h, float8v); }
+    static __device__ __forceinline__ half8 h(half8 v) { return v; }
 };
 template <>
 struct VOp<float> {
     typedef float8v raw;
     static __device__ __forceinline__ float8v load(const float* p) { return load8(p); }
-    static __device__ __forceinline__ float8v cvt(float8v f) { return f; }
+    static __device__ __forceinline__ half8 h(float8v v) { return __builtin_convertvector(v, half8); }
 };
 
 // lane n of each 16-lane row reads lane n+N of the same row
@@ -101,45 +127,82 @@ __device__ __forceinline__ float dpp_row_shl(float x) {
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + N, 0xF, 0xF, false));
 }
 
+// Keys attended by sequence b and how they are split: every kernel of a call derives the
+// same plan from key_len[b]. Active keys [lo, lo+active); split c covers
+// [lo + c*chunk, min(lo + (c+1)*chunk, hi)), c < n_act.
+struct SplitPlan {
+    int lo, hi, active, chunk, n_act;
+};
+__device__ __forceinline__ SplitPlan split_plan(const DecodeArgs& a, int b) {
+    SplitPlan p;
+    p.hi = a.key_len[b];
+    p.lo = (a.window > 0 && p.hi > a.window) ? p.hi - a.window : 0;
+    p.active = p.hi - p.lo;
+    p.chunk = a.chunk;  // keys per split (multiple of 16), chosen on the host
+    p.n_act = p.active > 0 ? (p.active + p.chunk - 1) / p.chunk : 0;
+    if (p.n_act > a.max_splits) {  // a key_len above the host's max_key_len: widen the splits
+        p.chunk = (((p.active + a.max_splits - 1) / a.max_splits) + 15) & ~15;
+        p.n_act = (p.active + p.chunk - 1) / p.chunk;
+    }
+    return p;
+}
+
 template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     using Sh = DecodeShape<HD, G>;
-    constexpr int KSTEPS = Sh::KSTEPS, VLANES = Sh::VLANES, VROWS = Sh::VROWS, VLOADS = Sh::VLOADS;
+    constexpr int KSTEPS = Sh::KSTEPS, NDT = Sh::NDT, VLANES = Sh::VLANES, VROWS = Sh::VROWS;
+    constexpr int VLOADS = Sh::VLOADS, VSTR = Sh::VSTR, QSTR = Sh::QSTR;
     using KO = KOp<KVT>;
     using VO = VOp<KVT>;
     typedef typename KO::raw kraw_t;
     typedef typename VO::raw vraw_t;
 
-    __shared__ __attribute__((aligned(16))) float lds[Sh::LDS_FLOATS];  // wave partials / merge weights
-    __shared__ __attribute__((aligned(16))) float lds_p[4][16][G];      // P of the current block, per wave
+    // one LDS arena, reused: q rows (prologue) -> V blocks (main loop) -> partials (merges)
+    __shared__ __attribute__((aligned(16))) char arena[Sh::LDS_BYTES];
+    half_t* sQ = reinterpret_cast<half_t*>(arena);
+    half_t* sV = reinterpret_cast<half_t*>(arena);
+    float* lds = reinterpret_cast<float*>(arena);
     __shared__ float lds_m[4][G], lds_l[4][G];
-    __shared__ float s_M[G], s_L[G];
-    __shared__ int s_last;
+    __shared__ float s_M[G], s_L[G], s_W[4][G];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int ci = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pair = b * a.n_kv_heads + kh;
 
-    // ---- attended keys and this workgroup's split (identical in every WG of the pair)
-    const int hi = a.key_len[b];
-    const int lo = (a.window > 0 && hi > a.window) ? hi - a.window : 0;
-    const int active = hi - lo;
+    // ---- q operand loads first: they depend on nothing but the sequence and kv head
+    constexpr int QP = HD / 128;  // elements per lane in each half of a head row
+    const int d0 = QP * lane;     // this lane: dims d0.. and d0+HD/2..
+    float qx[2][QP], qgv[2][QP], qcv[QP], qsv[QP];
+    {
+        const float* qb = a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
+        const float* gp = a.q_gain ? a.q_gain : kOnes;
+        const float* cp = a.rcos ? a.rcos + (size_t)b * (HD / 2) : kOnes;
+        const float* sp = a.rsin ? a.rsin + (size_t)b * (HD / 2) : kZeros;
+        const int hh = wave < G ? wave : 0;
+#pragma unroll
+        for (int e = 0; e < QP; ++e) {
+            qx[0][e] = qb[hh * HD + d0 + e];
+            qx[1][e] = qb[hh * HD + HD / 2 + d0 + e];
+            qgv[0][e] = gp[d0 + e];
+            qgv[1][e] = gp[HD / 2 + d0 + e];
+            qcv[e] = cp[d0 + e];
+            qsv[e] = sp[d0 + e];
+        }
+    }
+
+    // ---- attended keys and this workgroup's split
+    const SplitPlan sp = split_plan(a, b);
     float* outp = a.out + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
-    if (active <= 0) {  // no keys: defined output of zeros
+    if (sp.active <= 0) {  // no keys: defined output of zeros
         if (ci == 0)
             for (int e = tid; e < G * HD; e += 256) outp[e] = 0.0f;
         return;
     }
-    int chunk = a.chunk;  // keys per split (multiple of 16), chosen on the host
-    int n_act = (active + chunk - 1) / chunk;
-    if (n_act > a.max_splits) {  // a key_len above the host's max_key_len: widen the splits
-        chunk = (((active + a.max_splits - 1) / a.max_splits) + 15) & ~15;
-        n_act = (active + chunk - 1) / chunk;
-    }
+    const int n_act = sp.n_act;
     if (ci >= n_act) return;
-    const int k0 = lo + ci * chunk;
-    const int k1 = min(k0 + chunk, hi);
+    const int k0 = sp.lo + ci * sp.chunk;
+    const int k1 = min(k0 + sp.chunk, sp.hi);
 
     // ---- block loads: K in the MFMA A layout (lane n,g: key n, dims 32s+8g..), V rows
     const size_t rstride = (size_t)a.n_kv_heads * HD;
@@ -162,159 +225,124 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     int blk = k0 + wave * 16;
     if (blk < k1) load_block(blk);  // in flight during the q prologue
 
-    // ---- q prologue. The G query rows, the gain and this sequence's cos/sin rows are
-    // staged through LDS with one coalesced request per thread (all in flight together
-    // with the K/V block above). Then rows n < G of the MFMA B operand take the high f16
-    // part of head n, rows G..2G-1 the low part, rows >= 2G zero.
-    half8 qop[KSTEPS];
-    {
-        float* sq = lds;                 // [G][HD] q, then [HD] gain, [HD/2] cos, [HD/2] sin
-        float* sg = lds + G * HD;
-        float* sc_ = sg + HD;
-        float* ss_ = sc_ + HD / 2;
-        const float4* q4 = reinterpret_cast<const float4*>(a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD);
-        const float4* g4 = reinterpret_cast<const float4*>(a.q_gain ? a.q_gain : kOnes);
-        const float4* c4p = reinterpret_cast<const float4*>(a.rcos ? a.rcos + (size_t)b * (HD / 2) : kOnes);
-        const float4* s4p = reinterpret_cast<const float4*>(a.rsin ? a.rsin + (size_t)b * (HD / 2) : kZeros);
-        constexpr int NQ4 = G * HD / 4, NT4 = NQ4 + HD / 4 + HD / 4;
-        float4 st[(NT4 + 255) / 256];
+    // ---- q prologue: wave w prepares head w (and w+4): RMSNorm*gain, RoPE, scale*log2 e,
+    // split into f16 high/low rows of the B operand, staged in LDS.
 #pragma unroll
-        for (int u = 0; u < (NT4 + 255) / 256; ++u) {
-            const int idx = tid + 256 * u;
-            if (idx < NQ4) st[u] = q4[idx];
-            else if (idx < NQ4 + HD / 4) st[u] = g4[idx - NQ4];
-            else if (idx < NQ4 + HD / 4 + HD / 8) st[u] = c4p[idx - NQ4 - HD / 4];
-            else if (idx < NT4) st[u] = s4p[idx - NQ4 - HD / 4 - HD / 8];
+    for (int hh = wave; hh < G; hh += 4) {
+        float x[2][QP];
+        if (hh != wave) {  // G = 8: second head of this wave
+            const float* qb = a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G + hh) * HD;
+#pragma unroll
+            for (int e = 0; e < QP; ++e) {
+                qx[0][e] = qb[d0 + e];
+                qx[1][e] = qb[HD / 2 + d0 + e];
+            }
         }
 #pragma unroll
-        for (int u = 0; u < (NT4 + 255) / 256; ++u)
-            if (tid + 256 * u < NT4) reinterpret_cast<float4*>(sq)[tid + 256 * u] = st[u];
-        __syncthreads();
-        const int h = (n < 2 * G) ? (n % G) : 0;
-        float x[KSTEPS][8];
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[s][i] = sq[h * HD + 32 * s + 8 * g + i];
+        for (int e = 0; e < QP; ++e) {
+            x[0][e] = qx[0][e];
+            x[1][e] = qx[1][e];
+        }
         if (a.q_gain) {
-            float ssum = 0.0f;
+            float ss = 0.0f;
 #pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
+            for (int e = 0; e < QP; ++e) ss += x[0][e] * x[0][e] + x[1][e] * x[1][e];
+            const float rs = 1.0f / sqrtf(wave_sum(ss) / (float)HD + a.eps);  // attn_101's q * nscale * w
 #pragma unroll
-                for (int i = 0; i < 8; ++i) ssum += x[s][i] * x[s][i];
-            ssum += xor_shfl(ssum, 16);
-            ssum += xor_shfl(ssum, 32);
-            const float den = sqrtf(ssum / (float)HD + a.eps);
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] / den * sg[32 * s + 8 * g + i];
+            for (int e = 0; e < QP; ++e) {
+                x[0][e] = x[0][e] * rs * qgv[0][e];
+                x[1][e] = x[1][e] * rs * qgv[1][e];
+            }
         }
 #pragma unroll
-        for (int s = 0; s < KSTEPS / 2; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int d = 32 * s + 8 * g + i;
-                const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
-                x[s][i] = x0 * sc_[d] - x1 * ss_[d];
-                x[s + KSTEPS / 2][i] = x1 * sc_[d] + x0 * ss_[d];
-            }
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float v = x[s][i] * a.scale_log2;
-                const half_t vh = (half_t)v;
-                qop[s][i] = n < G ? vh : (n < 2 * G ? (half_t)(v - (float)vh) : (half_t)0.0f);
-            }
-        __syncthreads();  // the staging area is reused for the wave partials
+        for (int e = 0; e < QP; ++e) {
+            const float x0 = x[0][e], x1 = x[1][e];
+            const float r0 = (x0 * qcv[e] - x1 * qsv[e]) * a.scale_log2;
+            const float r1 = (x1 * qcv[e] + x0 * qsv[e]) * a.scale_log2;
+            const half_t h0 = (half_t)r0, h1 = (half_t)r1;
+            sQ[hh * QSTR + d0 + e] = h0;
+            sQ[hh * QSTR + HD / 2 + d0 + e] = h1;
+            sQ[(G + hh) * QSTR + d0 + e] = (half_t)(r0 - (float)h0);
+            sQ[(G + hh) * QSTR + HD / 2 + d0 + e] = (half_t)(r1 - (float)h1);
+        }
     }
+    __syncthreads();
+    half8 qop[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+        qop[s] = n < 2 * G ? *reinterpret_cast<const half8*>(&sQ[n * QSTR + 32 * s + 8 * g])
+                           : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    __syncthreads();  // the arena now holds the V blocks
 
-    // ---- main loop: per wave, 16-key blocks with an online softmax
-    float m_run = kNegInf, l_run = 0.0f;  // head n (lanes n < G)
-    float acc[G][8];                      // O[h][8 dims of this lane's V column]
+    // ---- main loop: per wave, 16-key blocks with an online softmax per head column
+    half_t* myV = sV + wave * 16 * VSTR;
+    float m_run = kNegInf, l_run = 0.0f;  // column n (heads: n < G)
+    float4v oacc[NDT];                    // O^T[16dt + 4g + i][column n]
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[hh][j] = 0.0f;
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
 
     for (; blk < k1; blk += 64) {
+#pragma unroll
+        for (int i = 0; i < VLOADS; ++i)
+            *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
         float4v c4 = float4v{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
+        if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during softmax and P.V
         float sc[4], mloc = kNegInf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float v = c4[i] + dpp_row_shl<G>(c4[i]);  // high + low column
-            sc[i] = (blk + 4 * g + i < k1) ? v : kNegInf;
+            sc[i] = (n < G && blk + 4 * g + i < k1) ? v : kNegInf;
             mloc = fmaxf(mloc, sc[i]);
         }
-        mloc = fmaxf(mloc, xor_shfl(mloc, 16));
-        mloc = fmaxf(mloc, xor_shfl(mloc, 32));
-        const float m_new = fmaxf(m_run, mloc);  // finite: key blk is valid
-        const float corr = exp2f(m_run - m_new);
+        mloc = max32(max16(mloc));
+        const float m_new = fmaxf(m_run, mloc);            // finite for heads: key blk is valid
+        const float m_use = (m_new == kNegInf) ? 0.0f : m_new;  // padding columns stay at zero
+        half4 pb;
         float ps = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            sc[i] = exp2f(sc[i] - m_new);
-            ps += sc[i];
+            const float p = fexp2(sc[i] - m_use);
+            ps += p;
+            pb[i] = (half_t)p;
         }
+        const float corr = fexp2(m_run - m_use);
         l_run = l_run * corr + ps;
         m_run = m_new;
-        if (n < G) {
+        if (__any(corr != 1.0f)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) lds_p[wave][4 * g + i][n] = sc[i];
+            for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
         }
-        float cr[G];
+        // O^T += V^T . P^T : lane n of group g supplies V[key 4g + n/4][16dt + 4(n%4) ..]
+        const half_t* vrd = myV + (4 * g + (n >> 2)) * VSTR + 4 * (n & 3);
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) cr[hh] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), hh));
-        vraw_t vcur[VLOADS];
-#pragma unroll
-        for (int i = 0; i < VLOADS; ++i) vcur[i] = vr[i];
-        if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during P.V
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[hh][j] *= cr[hh];
-#pragma unroll
-        for (int i = 0; i < VLOADS; ++i) {
-            const float8v vf = VO::cvt(vcur[i]);
-            const float* pr = &lds_p[wave][VROWS * i + vrow][0];
-            float p[G];
-#pragma unroll
-            for (int hh = 0; hh < G; ++hh) p[hh] = pr[hh];
-#pragma unroll
-            for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[hh][j] = fmaf(p[hh], vf[j], acc[hh][j]);
-        }
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma16x16(lds_read_tr16(vrd + 16 * dt), pb, oacc[dt]);
     }
 
-    // ---- wave partial: rows of the same V column summed, then to LDS
-    l_run += xor_shfl(l_run, 16);
-    l_run += xor_shfl(l_run, 32);
-    if constexpr (VROWS == 2) {
+    // ---- wave partial: column sums, then the head columns to LDS
+    l_run = add32(add16(l_run));
+    __syncthreads();  // every wave is done with its V block: the arena takes the partials
+    if (n < G) {
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[hh][j] += xor_shfl(acc[hh][j], 32);
-    }
-    if (lane < VLANES) {
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) lds[(wave * G + hh) * HD + 8 * lane + j] = acc[hh][j];
-    }
-    if (lane < G) {
-        lds_m[wave][lane] = m_run;
-        lds_l[wave][lane] = l_run;
+            for (int i = 0; i < 4; ++i) lds[(wave * G + n) * HD + 16 * dt + 4 * g + i] = oacc[dt][i];
+        if (g == 0) {
+            lds_m[wave][n] = m_run;
+            lds_l[wave][n] = l_run;
+        }
     }
     __syncthreads();
     if (tid < G) {
         float M = kNegInf;
         for (int w = 0; w < 4; ++w) M = fmaxf(M, lds_m[w][tid]);
         float L = 0.0f;
-        for (int w = 0; w < 4; ++w) L += lds_l[w][tid] * exp2f(lds_m[w][tid] - M);
+        for (int w = 0; w < 4; ++w) {
+            const float wt = fexp2(lds_m[w][tid] - M);
+            s_W[w][tid] = wt;
+            L += lds_l[w][tid] * wt;
+        }
         s_M[tid] = M;
         s_L[tid] = L;
     }
@@ -324,93 +352,72 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     float* po = a.part_o + ((size_t)pair * a.max_splits + ci) * (G * HD);
     for (int e = tid; e < G * HD; e += 256) {
         const int hh = e / HD;
-        const float M = s_M[hh];
         float o = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) o += lds[w * G * HD + e] * exp2f(lds_m[w][hh] - M);
+        for (int w = 0; w < 4; ++w) o += lds[w * G * HD + e] * s_W[w][hh];
         if (single)
-            outp[e] = srq(o / s_L[hh], a.out_q);
+            outp[e] = srq(o * (1.0f / s_L[hh]), a.out_q);
         else
             po[e] = o;
     }
     if (single) return;
     if (tid < G) a.part_ml[((size_t)pair * a.max_splits + ci) * G + tid] = make_float2(s_M[tid], s_L[tid]);
+}
 
-    // ---- publish, take a ticket; the last split of the pair merges all partials.
-    // The barrier completes every wave's partial stores; one agent-scope release by
-    // thread 0 then makes them visible beyond this XCD's L2, and only the last
-    // arriver pays the acquire before reading the other splits' partials.
+// Merge of the split partials: out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max_c m_c
+// (the flash-decoding identity attn_101 applies in its last chunk, kernels_dsl.py:1717-1749).
+// One workgroup per (64 output dims, kv head, sequence): thread (split group sg, dim d) loads
+// splits c = sg, sg+4, ... of its output element in one batch of up to 16 (loads are
+// unconditional: the index is clamped and padded splits weigh 0), then the four split groups
+// are summed through LDS. Sequences whose keys fit one split were finished by decode_kernel.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+    constexpr int E = G * HD;
+    __shared__ float wts[256];
+    __shared__ float red[4][64];
+    __shared__ float s_red[4], s_L;
+    const int tid = threadIdx.x, lane = tid & 63, sg = tid >> 6;
+    const int e = blockIdx.x * 64 + lane, hh = (blockIdx.x * 64) / HD;
+    const int kh = blockIdx.y, b = blockIdx.z, pair = b * a.n_kv_heads + kh;
+    const SplitPlan sp = split_plan(a, b);
+    const int n_act = sp.n_act;
+    if (n_act <= 1) return;
+    const float* po = a.part_o + (size_t)pair * a.max_splits * E + e;
+    const float2* ml = a.part_ml + (size_t)pair * a.max_splits * G + hh;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(sg + 4 * u, n_act - 1) * E];
+    // weights of every split for this head
+    const float2 mlt = ml[(size_t)min(tid, n_act - 1) * G];
+    float mloc = tid < n_act ? mlt.x : kNegInf;
+    mloc = wave_max(mloc);
+    if (lane == 0) s_red[sg] = mloc;
     __syncthreads();
-    if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t t = __hip_atomic_fetch_add(a.tickets + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = (t == (uint32_t)(n_act - 1));
-        if (last) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __hip_atomic_store(a.tickets + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float w = tid < n_act ? fexp2(mlt.x - M) : 0.0f;
+    wts[tid] = w;
+    const float lw = wave_sum(w * (tid < n_act ? mlt.y : 0.0f));
+    __syncthreads();
+    if (lane == 0) s_red[sg] = lw;
+    __syncthreads();
+    if (tid == 0) s_L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    float o = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) o = fmaf(wts[min(sg + 4 * u, 255)] * (sg + 4 * u < n_act ? 1.0f : 0.0f), v[u], o);
+    for (int c0 = 64; c0 < n_act; c0 += 64) {  // more than 64 splits: further batches
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(c0 + sg + 4 * u, n_act - 1) * E];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int c = c0 + sg + 4 * u;
+            o = fmaf(c < n_act ? wts[c] : 0.0f, v[u], o);
         }
-        s_last = last;
     }
+    red[sg][lane] = o;
     __syncthreads();
-    if (!s_last) return;
-
-    // Each thread owns 4 consecutive outputs (float4) and streams the splits 16 at a time.
-    // Loads are unconditional (split index clamped; weights of the padding are 0), and the
-    // first batch is requested before the weights are computed.
-    constexpr int STRIDE4 = G * HD / 4;
-    const float4* pob4 = reinterpret_cast<const float4*>(a.part_o + (size_t)pair * a.max_splits * (G * HD));
-    const float2* ml = a.part_ml + (size_t)pair * a.max_splits * G;
-    float* wts = lds;  // [G][256]; n_act <= max_splits <= 256
-    float4 v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(u, n_act - 1) * STRIDE4 + tid];
-    const int n_pad = (n_act + 15) & ~15;
-    for (int hh = wave; hh < G; hh += 4) {
-        float mloc = kNegInf;
-        for (int t = lane; t < n_act; t += 64) mloc = fmaxf(mloc, ml[t * G + hh].x);
-        const float M = wave_max(mloc);
-        float lsum = 0.0f;
-        for (int t = lane; t < n_pad; t += 64) {
-            float w = 0.0f;
-            if (t < n_act) {
-                const float2 w2 = ml[t * G + hh];
-                w = exp2f(w2.x - M);
-                lsum += w2.y * w;
-            }
-            wts[hh * 256 + t] = w;
-        }
-        lsum = wave_sum(lsum);
-        if (lane == 0) s_L[hh] = lsum;
-    }
-    __syncthreads();
-    for (int e4 = tid; e4 < STRIDE4; e4 += 256) {
-        if (e4 != tid) {
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(u, n_act - 1) * STRIDE4 + e4];
-        }
-        const int hh = (4 * e4) / HD;
-        const float* wh = wts + hh * 256;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int t0 = 0;;) {
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float w = wh[t0 + u];
-                o.x = fmaf(w, v[u].x, o.x);
-                o.y = fmaf(w, v[u].y, o.y);
-                o.z = fmaf(w, v[u].z, o.z);
-                o.w = fmaf(w, v[u].w, o.w);
-            }
-            t0 += 16;
-            if (t0 >= n_act) break;
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = pob4[(size_t)min(t0 + u, n_act - 1) * STRIDE4 + e4];
-        }
-        const float L = s_L[hh];
-        float* op = outp + 4 * e4;
-        op[0] = srq(o.x / L, a.out_q);
-        op[1] = srq(o.y / L, a.out_q);
-        op[2] = srq(o.z / L, a.out_q);
-        op[3] = srq(o.w / L, a.out_q);
+    if (sg == 0) {
+        const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+        a.out[((size_t)b * a.n_q_heads + (size_t)kh * G) * HD + e] = srq(t * (1.0f / s_L), a.out_q);
     }
 }
 
@@ -444,7 +451,7 @@ static int decode_splits(const g4a_cfg* cfg, int n_seq, int max_key_len) {
 }
 
 struct WsLayout {
-    size_t tickets, ml, o, total;
+    size_t ml, o, total;
 };
 
 static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_splits) {
@@ -452,8 +459,7 @@ static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_splits) {
     const size_t G = cfg->n_q_heads / cfg->n_kv_heads;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout L;
-    L.tickets = 0;
-    L.ml = al(pairs * 4);
+    L.ml = 0;
     L.o = L.ml + al(pairs * max_splits * G * sizeof(float2));
     L.total = L.o + pairs * max_splits * G * cfg->head_dim * sizeof(float);
     return L;
@@ -472,6 +478,16 @@ static decode_fn pick_g(int G, bool f32) {
         case 2: return pick_kv<HD, 2>(f32);
         case 4: return pick_kv<HD, 4>(f32);
         case 8: return pick_kv<HD, 8>(f32);
+    }
+    return nullptr;
+}
+template <int HD>
+static decode_fn pick_merge(int G) {
+    switch (G) {
+        case 1: return decode_merge_kernel<HD, 1>;
+        case 2: return decode_merge_kernel<HD, 2>;
+        case 4: return decode_merge_kernel<HD, 4>;
+        case 8: return decode_merge_kernel<HD, 8>;
     }
     return nullptr;
 }
@@ -540,7 +556,6 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     a.seq_stride = seq_stride;
     a.out = out;
     char* w = (char*)ws;
-    a.tickets = (uint32_t*)(w + L.tickets);
     a.part_ml = (float2*)(w + L.ml);
     a.part_o = (float*)(w + L.o);
     a.n_q_heads = (int)cfg->n_q_heads;
@@ -560,5 +575,11 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "decode launch");
+    if (splits > 1) {
+        decode_fn mf = HD == 256 ? pick_merge<256>(G) : pick_merge<512>(G);
+        hipLaunchKernelGGL(mf, dim3(G * HD / 64, cfg->n_kv_heads, n_seq), dim3(256), 0, (hipStream_t)stream, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_error(e, "decode merge launch");
+    }
     return G4A_OK;
 }

@@ -49,9 +49,9 @@ __global__ __launch_bounds__(HD / 2) void kv_write_kernel(KvArgs a) {
         sv += red[1][w];
     }
     if (a.k_gain) {
-        const float den = sqrtf(sk / (float)HD + a.eps);
-        k0 = k0 / den * a.k_gain[t];
-        k1 = k1 / den * a.k_gain[t + HALF];
+        const float rs = 1.0f / sqrtf(sk / (float)HD + a.eps);  // kvnorm's k * rmsk * knorm
+        k0 = k0 * rs * a.k_gain[t];
+        k1 = k1 * rs * a.k_gain[t + HALF];
     }
     if (a.rcos) {
         const float c = a.rcos[(size_t)s * HALF + t], sn = a.rsin[(size_t)s * HALF + t];
@@ -60,9 +60,9 @@ __global__ __launch_bounds__(HD / 2) void kv_write_kernel(KvArgs a) {
         k1 = x1 * c + x0 * sn;
     }
     if (a.v_norm) {
-        const float den = sqrtf(sv / (float)HD + a.eps);
-        v0 = v0 / den;
-        v1 = v1 / den;
+        const float rs = 1.0f / sqrtf(sv / (float)HD + a.eps);
+        v0 = v0 * rs;
+        v1 = v1 * rs;
     }
     const size_t crow = ((size_t)(a.start_pos + s) * a.n_kv_heads + kh) * HD;
     CT* kc = reinterpret_cast<CT*>(a.kc) + crow;

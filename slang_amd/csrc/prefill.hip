@@ -181,18 +181,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
                 sacc[kt][i] = sv;
                 mt = fmaxf(mt, sv);
             }
-        mt = fmaxf(mt, xor_shfl(mt, 16));
-        mt = fmaxf(mt, xor_shfl(mt, 32));
+        mt = max32(max16(mt));
         const float m_new = fmaxf(m_run, mt);
         const float base = (m_new == kNegInf) ? 0.0f : m_new;
-        const float corr = exp2f(m_run - base);
+        const float corr = fexp2(m_run - base);
         float ps = 0.0f;
         half8 pf[NU];
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = exp2f(sacc[kt][i] - base);
+                const float p = fexp2(sacc[kt][i] - base);
                 ps += p;
                 pf[kt >> 1][(kt & 1) * 4 + i] = (half_t)p;
             }
@@ -216,14 +215,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 
     // ---- epilogue: row sum over the 4 lane groups, normalise, srq, store
     float l_tot = l_run;
-    l_tot += xor_shfl(l_tot, 16);
-    l_tot += xor_shfl(l_tot, 32);
+    l_tot = add32(add16(l_tot));
+    const float inv_l = 1.0f / l_tot;
     if (!col_ok) return;
     OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + h) * HD;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_elem(orow + 16 * dt + 4 * g + i, srq(oacc[dt][i] / l_tot, a.out_q));
+        for (int i = 0; i < 4; ++i) store_elem(orow + 16 * dt + 4 * g + i, srq(oacc[dt][i] * inv_l, a.out_q));
 }
 
 typedef void (*prefill_fn)(PrefillArgs);

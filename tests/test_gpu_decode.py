@@ -183,9 +183,10 @@ def test_mask_leak_marker(T, window):
     np.testing.assert_allclose(got, 1.0, atol=1e-5)
 
 
-def test_tickets_reset_and_deterministic():
-    """Every call leaves its ticket counters at zero (kernels_dsl.py:1714-1715,
-    tests/test_kernels_dsl_parity.py:780) and repeats bit-identically."""
+def test_deterministic_and_workspace_reuse():
+    """Repeated calls are bit-identical, also when the workspace holds stale partials from a
+    different call (the reference re-zeroes its ticket per call, kernels_dsl.py:1714-1715;
+    this build keeps no state in the workspace between calls)."""
     T = 4096
     q, qg, k, v, c, s = config2_inputs(T, 1e6, seed=3)
     ws = sa.DecodeWorkspace(DEV)
@@ -193,10 +194,12 @@ def test_tickets_reset_and_deterministic():
     args = (t(q), t(k), t(v), [T], cfg)
     kw = dict(q_gain=t(qg), rope_cos=t(c[None]), rope_sin=t(s[None]), workspace=ws)
     a = sa.decode(*args, **kw).clone()
+    ws.buf.fill_(0x7f)                      # garbage partials
     b = sa.decode(*args, **kw).clone()
+    sa.decode(t(q), t(k), t(v), [1000], cfg, workspace=ws)   # a different split plan in between
+    c2 = sa.decode(*args, **kw).clone()
     torch.cuda.synchronize()
-    assert torch.equal(a, b)
-    assert int(ws.buf[:256].count_nonzero()) == 0, "ticket counters not reset"
+    assert torch.equal(a, b) and torch.equal(a, c2)
     assert int(a.count_nonzero()) > 0
 
 
