@@ -13,11 +13,12 @@
 // the 4 waves owns 16 columns. Scores are computed transposed, S^T = K . Q^T
 // (A = K tile from LDS, B = Q^T held in registers), which leaves every lane with 4
 // keys of ONE query column -- exactly the B-operand layout the P.V product needs
-// when it is also computed transposed, O^T = V^T . P^T (A = V^T from LDS, staged
-// transposed at load time). Scores stay f32 in the MFMA accumulators; P is rounded
-// to f16 only as the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last]
-// are skipped; boundary tiles are masked per element. Work-groups are launched
-// longest-causal-row first.
+// when it is also computed transposed, O^T = V^T . P^T. V stays row-major in LDS and
+// its transposed A operand comes from ds_read_tr16_b64. K/V tiles are double
+// buffered in LDS: the next tile's global loads are in flight while the current one
+// is computed. Scores stay f32 in the MFMA accumulators; P is rounded to f16 only as
+// the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last] are skipped;
+// boundary tiles are masked per element. Work-groups are launched longest-causal-row first.
 #include "common.hpp"
 
 namespace g4a {
@@ -34,19 +35,33 @@ struct PrefillArgs {
     float scale_log2, eps, out_q;
 };
 
+#ifndef G4A_PREFILL_KT256
+#define G4A_PREFILL_KT256 64
+#endif
 template <int HD>
 struct PrefillShape {
-    static constexpr int KT = HD == 512 ? 32 : 64;  // keys per LDS tile
+    static constexpr int KT = HD == 512 ? 32 : G4A_PREFILL_KT256;  // keys per LDS tile
     static constexpr int KSTEPS = HD / 32;           // MFMA k-steps of the score product
     static constexpr int NKT = KT / 16;              // 16-key sub-tiles of S^T
     static constexpr int NU = KT / 32;               // 32-key k-steps of the P.V product
     static constexpr int NDT = HD / 16;              // 16-dim tiles of O^T
-    static constexpr int KS = HD + 8;                // K tile row stride (halves), 16 B pad
-    static constexpr int VS = KT + 8;                // V^T row stride (halves)
+    static constexpr int KS = HD + 8;                // K row stride (halves): A reads conflict-free
+    static constexpr int VS = HD + 16;               // V row stride (halves): transpose reads conflict-free
+    static constexpr int CH = HD / 8;                // 16 B chunks per row
+    static constexpr int PER = KT * CH / 256;        // chunks of K (and of V) per thread per tile
+    static constexpr int STAGE = KT * KS + KT * VS;  // halves per pipeline stage
 };
 
 __device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 4 halves of a row-major LDS tile transposed across each 16-lane group: lane n of the
+// group receives element n%4 of the 8-byte chunks supplied by lanes n/4 + 4j (j < 4).
+__device__ __forceinline__ half4 lds_tr16(const half_t* p) {
+    typedef short short4_ __attribute__((ext_vector_type(4)));
+    const short4_ t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_*)(p));
+    return __builtin_bit_cast(half4, t);
 }
 
 // qprep_b (kernels_dsl.py:1837-1873): q RMSNorm*gain + RoPE for S*nH rows, stored f16.
@@ -81,8 +96,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     constexpr int KS = Sh::KS, VS = Sh::VS;
     constexpr int BQ = 64 / G;
 
-    __shared__ __attribute__((aligned(16))) half_t Ks[KT * KS];
-    __shared__ __attribute__((aligned(16))) half_t Vt[HD * VS];
+    constexpr int CH = Sh::CH, PER = Sh::PER;
+    __shared__ __attribute__((aligned(16))) half_t stage[2 * Sh::STAGE];  // [buf]{K[KT][KS], V[KT][VS]}
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -130,31 +145,38 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
     float m_run = kNegInf, l_run = 0.0f;
 
-    for (int t0 = (wg_lo / KT) * KT; t0 < kv_hi; t0 += KT) {
-        __syncthreads();  // previous tile fully consumed
-        // K tile, row-major [key][dim] with a 16 B row pad
-        for (int idx = tid; idx < KT * (HD / 8); idx += 256) {
-            const int row = idx / (HD / 8), ch = idx % (HD / 8);
-            const int key = t0 + row;
-            half8 v = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            if (key < T_total) v = load8h(kcb + (size_t)key * rstride + 8 * ch);
-            *reinterpret_cast<half8*>(&Ks[row * KS + 8 * ch]) = v;
-        }
-        // V tile, transposed [dim][key]: 4 keys x 8 dims per unit
-        for (int idx = tid; idx < (KT / 4) * (HD / 8); idx += 256) {
-            const int jg = idx % (KT / 4), dg = idx / (KT / 4);
-            half8 v[4];
+    // ---- K/V tile staging: thread chunk r covers row (tid + 256r) / CH, chunk (tid + 256r) % CH
+    half8 kst[PER], vst[PER];
+    auto load_tile = [&](int t0) {
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int key = t0 + 4 * jg + kk;
-                v[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-                if (key < T_total) v[kk] = load8h(vcb + (size_t)key * rstride + 8 * dg);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                *reinterpret_cast<half4*>(&Vt[(8 * dg + i) * VS + 4 * jg]) = half4{v[0][i], v[1][i], v[2][i], v[3][i]};
+        for (int r = 0; r < PER; ++r) {
+            const int idx = tid + 256 * r, row = idx / CH, ch = idx % CH;
+            const int key = min(t0 + row, T_total - 1);  // rows past the prompt are masked
+            kst[r] = load8h(kcb + (size_t)key * rstride + 8 * ch);
+            vst[r] = load8h(vcb + (size_t)key * rstride + 8 * ch);
         }
-        __syncthreads();
+    };
+    auto store_tile = [&](int buf) {
+        half_t* Kb = stage + buf * Sh::STAGE;
+        half_t* Vb = Kb + KT * KS;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int idx = tid + 256 * r, row = idx / CH, ch = idx % CH;
+            *reinterpret_cast<half8*>(&Kb[row * KS + 8 * ch]) = kst[r];
+            *reinterpret_cast<half8*>(&Vb[row * VS + 8 * ch]) = vst[r];
+        }
+    };
+
+    const int t_first = (wg_lo / KT) * KT;
+    const int ntiles = (kv_hi - t_first + KT - 1) / KT;  // >= 1: kv_hi > wg_lo
+    load_tile(t_first);
+    store_tile(0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int t0 = t_first + it * KT, buf = it & 1;
+        if (it + 1 < ntiles) load_tile(t0 + KT);  // in flight during this tile's math
+        const half_t* Kb = stage + buf * Sh::STAGE;
+        const half_t* Vb = Kb + KT * KS;
 
         // S^T = K . Q^T : sacc[kt][i] = score(key t0+16kt+4g+i, column n)
         float4v sacc[NKT];
@@ -163,7 +185,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             float4v c4 = float4v{0, 0, 0, 0};
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
-                const half8 av = *reinterpret_cast<const half8*>(&Ks[(16 * kt + n) * KS + 32 * s + 8 * g]);
+                const half8 av = *reinterpret_cast<const half8*>(&Kb[(16 * kt + n) * KS + 32 * s + 8 * g]);
                 c4 = mfma16(av, qf[s], c4);
                 if constexpr (HILO) c4 = mfma16(av, ql[s], c4);
             }
@@ -197,20 +219,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             }
         l_run = l_run * corr + ps;
         m_run = m_new;
+        if (__any(corr != 1.0f)) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
+            for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
+        }
 
-        // O^T += V^T . P^T
+        // O^T += V^T . P^T; lane n of group g supplies V[32u + 4g + n/4 (+16)][16dt + 4(n%4)..]
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+        for (int u = 0; u < NU; ++u) {
+            const half_t* v0 = Vb + (32 * u + 4 * g + (n >> 2)) * VS + 4 * (n & 3);
 #pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const half_t* vr = &Vt[(16 * dt + n) * VS + 32 * u + 4 * g];
-                const half4 lo4 = *reinterpret_cast<const half4*>(vr);
-                const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
+            for (int dt = 0; dt < NDT; ++dt) {
+                const half4 lo4 = lds_tr16(v0 + 16 * dt);
+                const half4 hi4 = lds_tr16(v0 + 16 * VS + 16 * dt);
                 const half8 av = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 oacc[dt] = mfma16(av, pf[u], oacc[dt]);
             }
+        }
+        if (it + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
     }
 
     // ---- epilogue: row sum over the 4 lane groups, normalise, srq, store
