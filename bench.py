@@ -29,14 +29,31 @@ F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, published
 NH, KVH, HD = 8, 2, 256
 
 
+EAGER = False                 # --eager: time plain back-to-back launches instead of a HIP graph
+
+
 def graph_time_ms(fn_list, steps, warmup):
-    """Capture `steps` calls (cycling fn_list) in one HIP graph; return mean ms per call."""
+    """Capture `steps` calls (cycling fn_list) in one HIP graph; return mean ms per call.
+
+    With --eager the same calls are launched one by one on the stream (for profilers
+    that count per dispatch); the figure then includes host launch gaps.
+    """
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for i in range(max(warmup, 1)):
             fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
+    if EAGER:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for i in range(steps):
+                fn_list[i % len(fn_list)]()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / steps
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for i in range(steps):
@@ -116,6 +133,97 @@ def batched_decode_case(sa, steps, warmup, gen):
     return ms, int(2 * lens.sum()) * KVH * HD * 2, int(lens.sum())
 
 
+def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
+    """35 layers (4 sliding(512) then 1 global, repeated), prefill of S
+    tokens then `steps` decode steps against the growing f16 caches, one cache per layer.
+
+    Each layer's prefill is kv_write(S rows) + prefill; each decode step per layer is
+    kv_write(1 row) + decode. Both phases are timed as whole-stack HIP graphs. q and
+    the raw k/v rows are N(0,1) (the projections that would produce them are not part
+    of the attention path). Returns per-phase totals and per-layer-type figures.
+    """
+    T = S + steps
+    kinds = ["global" if (i % 5) == 4 else "sliding" for i in range(n_layers)]
+    theta = {"global": 1e6, "sliding": 1e4}
+    win = {"global": 0, "sliding": 512}
+    tabs = {k: sa.rope_tables(np.arange(T), HD, theta[k]) for k in theta}
+    cfgs = {k: sa.AttnConfig(NH, KVH, HD, win[k]) for k in theta}
+    kvcfg = sa.AttnConfig(KVH, KVH, HD)
+    qg = 1 + 0.1 * torch.randn(HD, device="cuda", generator=gen)
+    kg = 1 + 0.1 * torch.randn(HD, device="cuda", generator=gen)
+    qp = torch.randn(S, NH, HD, device="cuda", generator=gen)
+    kp = torch.randn(S, KVH, HD, device="cuda", generator=gen).half()
+    vp = torch.randn(S, KVH, HD, device="cuda", generator=gen).half()
+    qd = torch.randn(NH, HD, device="cuda", generator=gen)
+    kd = torch.randn(steps, KVH, HD, device="cuda", generator=gen)
+    vd = torch.randn(steps, KVH, HD, device="cuda", generator=gen)
+    caches = [(torch.zeros(T, KVH, HD, device="cuda", dtype=torch.float16),
+               torch.zeros(T, KVH, HD, device="cuda", dtype=torch.float16)) for _ in range(n_layers)]
+    outp = torch.empty(S, NH, HD, device="cuda", dtype=torch.float16)
+    outd = torch.empty(1, NH, HD, device="cuda")
+    kl = torch.arange(S + 1, T + 1, dtype=torch.int32, device="cuda")
+    ws = sa.DecodeWorkspace("cuda")
+
+    def prefill_layer(i):
+        kc, vc = caches[i]
+        c, sn = tabs[kinds[i]]
+        sa.kv_write(kp, vp, kc, vc, 0, kvcfg, k_gain=kg, rope_cos=c, rope_sin=sn)
+        sa.prefill(qp, kc, vc, 0, cfgs[kinds[i]], q_gain=qg, rope_cos=c, rope_sin=sn, out=outp)
+
+    def decode_layer(i, t):
+        kc, vc = caches[i]
+        c, sn = tabs[kinds[i]]
+        p = S + t
+        sa.kv_write(kd[t:t + 1], vd[t:t + 1], kc, vc, p, kvcfg, k_gain=kg,
+                    rope_cos=c[p:p + 1], rope_sin=sn[p:p + 1])
+        sa.decode(qd, kc, vc, kl[t:t + 1], cfgs[kinds[i]], q_gain=qg, rope_cos=c[p:p + 1],
+                  rope_sin=sn[p:p + 1], out=outd, workspace=ws)
+
+    pre_ms = graph_time_ms([lambda: [prefill_layer(i) for i in range(n_layers)]], 1, 1)
+    dec_ms = graph_time_ms([lambda: [decode_layer(i, t) for t in range(steps) for i in range(n_layers)]], 1, 0)
+    # per-layer-type figures: one layer of each kind (the same calls, graphs of their own)
+    per = {}
+    for kind, li in (("global", 4), ("sliding", 0)):
+        pm = graph_time_ms([lambda li=li: prefill_layer(li)], 4, 1)
+        dm = graph_time_ms([lambda li=li: [decode_layer(li, t) for t in range(steps)]], 1, 0) / steps
+        pairs = sum(min(p + 1, win[kind]) if win[kind] else p + 1 for p in range(S))
+        dbytes = sum(2 * (min(S + t + 1, win[kind]) if win[kind] else S + t + 1) * KVH * HD * 2
+                     for t in range(steps)) / steps
+        per[kind] = {"prefill_us": round(pm * 1e3, 2),
+                     "prefill_TFLOP/s": round(4 * HD * NH * pairs / (pm * 1e-3) / 1e12, 2),
+                     "decode_step_us": round(dm * 1e3, 3),
+                     "decode_GB/s": round(dbytes / (dm * 1e-3) / 1e9, 2)}
+    return {"layers": n_layers, "S": S, "decode_steps": steps,
+            "prefill_ms_35_layers": round(pre_ms, 3),
+            "decode_ms_per_step_35_layers": round(dec_ms / steps, 4),
+            "per_layer": per,
+            "note": "prefill per layer = kv_write(S) + prefill; decode per layer-step = kv_write(1) + decode"}
+
+
+def copy_calibration(steps):
+    """A plain elementwise kernel of known traffic (torch.neg over 256 MiB f16: 256 MiB read,
+    256 MiB written per launch) for scaling FETCH_SIZE / WRITE_SIZE counter readings."""
+    n = 128 << 20
+    src = torch.randn(n, device="cuda").half()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": "torch.neg f16", "read_bytes": 2 * n, "write_bytes": 2 * n,
+                      "launches": steps}), flush=True)
+
+
+def load_traffic():
+    """HBM bytes per decode call from the committed PMC summary (profiles/traffic.json), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("decode_2g", {}).get("bytes_per_call")
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(case, seconds):
     """The numpy oracle (oracle/attention.py) on this host for the headline decode call."""
     import oracle.attention as O
@@ -159,7 +267,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 35-layer config 5 stack")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch calls one by one instead of replaying a HIP graph (for profilers)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a known-size copy kernel (counter calibration) and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config 3 prefill rows (for profiling the prefill kernel)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured mode)", file=sys.stderr)
@@ -167,7 +284,17 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import slang_amd as sa
 
+    if args.copy_calibration:
+        copy_calibration(max(args.steps, 1))
+        return
     gen = torch.Generator(device="cuda").manual_seed(2024)
+    if args.prefill_only:
+        out = {}
+        for tag, win, th in (("prefill_3g", 0, 1e6), ("prefill_3s", 512, 1e4)):
+            msp, fl = prefill_case(sa, 1024, win, th, args.steps, args.warmup, gen)
+            out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
+        print(json.dumps(out), flush=True)
+        return
     ms, nbytes, case = decode_case(sa, 4096, 0, 1e6, args.steps, args.warmup, 64, gen)
     gbs = nbytes / (ms * 1e-3) / 1e9
     rec = {
@@ -179,7 +306,8 @@ def main():
                                "KV 4096 f16 cache, q/k RMSNorm+RoPE theta 1e6, 64 rotated caches",
                    "accumulate": "f32", "kv_bytes_per_call": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                     "kernels": "decode_kernel + decode_merge_kernel (one g4a_decode call)"},
     }
     if not args.only_headline:
         sec = {}
@@ -195,6 +323,8 @@ def main():
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
                            "hbm_frac": round(nb4 / ms4 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb4,
                            "sum_kv_len": toks}
+        if not args.no_stack:
+            sec["stack_5"] = stack_case(sa, gen)
         rec["secondary"] = sec
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds)
