@@ -280,17 +280,22 @@ def kvnorm_b(kraw, vraw, k_norm, cosT, sinT, kc, vc, p, *, S, head_dim, n_kv_hea
              rope_sin=sinT.view(-1, half)[start:start + S], k_in_q=ks, v_in_q=vs)
 
 
-def attn_prefill(q, q_norm, cosT, sinT, kc, vc, out, params, *, head_dim, out_q=0.0):
+def attn_prefill(q, q_norm, cosT, sinT, kc, vc, out, params, *, head_dim, out_q=0.0, q_f16=False):
     """attn_prefill (kernels_dsl.py:1950-2098; prefill_gpu.py:347-354): slots [q, q_norm, cosT,
     sinT, k, v, out, params] with params = (startPos, qH, kvH, W, S); cosT/sinT absolute tables
-    [max_pos][hd/2]. `out` may be f32 (attn_prefill's own output) or f16 (attnh)."""
+    [max_pos][hd/2]. `out` may be f32 (attn_prefill's own output) or f16 (attnh).
+
+    The fused kernel keeps the normalised, rotated q in f32 (kernels_dsl.py:2007-2014), so
+    this uses the f32-accurate q mode; q_f16=True rounds q to f16 first, as qprep_b does
+    for the GEMM form."""
     start, qh, kvh, win, S = (int(x) for x in list(params)[:5])
     cfg = AttnConfig(qh, kvh, head_dim, win, 1.0, 1e-6, out_q)
     half = head_dim // 2
     maxseq = kc.numel() // (kvh * head_dim)
     prefill(q.view(S, qh, head_dim), kc.view(maxseq, kvh, head_dim), vc.view(maxseq, kvh, head_dim),
             start, cfg, q_gain=q_norm, rope_cos=cosT.view(-1, half)[start:start + S],
-            rope_sin=sinT.view(-1, half)[start:start + S], out=out.view(S, qh, head_dim))
+            rope_sin=sinT.view(-1, half)[start:start + S], out=out.view(S, qh, head_dim),
+            q_hilo=not q_f16)
     return out
 
 
@@ -310,4 +315,5 @@ def attn_gemm(q, q_norm, cosT, sinT, kc, vc, attnh, *, S, start_pos, n_q_heads, 
     """PrefillGPU._attn_gemm (prefill_gpu.py:259-313): writes attnh f16 [S][nH*hd] =
     f16(srq(softmax(qf16 . kf16^T) . vf16, o_in)) in one fused kernel."""
     return attn_prefill(q, q_norm, cosT, sinT, kc, vc, attnh,
-                        (start_pos, n_q_heads, n_kv_heads, window, S), head_dim=head_dim, out_q=o_in)
+                        (start_pos, n_q_heads, n_kv_heads, window, S), head_dim=head_dim, out_q=o_in,
+                        q_f16=True)

@@ -1,5 +1,5 @@
-// Decode attention for gfx950: split-KV flash decoding with an in-kernel
-// last-arriver merge.
+// Decode attention for gfx950: split-KV flash decoding; the splits' partials are merged
+// by a second kernel.
 //
 // Reference semantics: attn_101 (gemma4_150/kernels_dsl.py:1537-1749) -- q RMSNorm*gain
 // + split-half RoPE (:1593-1615), attended keys [max(0, p+1-W), keyLen) (:1582-1589),

@@ -215,7 +215,13 @@ def test_f32_cache_and_mirror():
                     t(z["k"].astype(np.float32).reshape(-1)), t(z["v"].astype(np.float32).reshape(-1)),
                     out, (start, nH, kvH, 16, S), head_dim=hd)
     torch.cuda.synchronize()
-    contract_close(out.cpu().numpy().reshape(S, nH, hd), z["expected_q16_w16"], "attn_prefill mirror")
+    contract_close(out.cpu().numpy().reshape(S, nH, hd), z["expected_w16"], "attn_prefill mirror")
+    out16 = torch.zeros(S * nH * hd, device=DEV, dtype=torch.float16)
+    sa.attn_gemm(t(z["q"].reshape(-1)), t(z["w"]), t(cosT), t(sinT),
+                 t(z["k"].astype(np.float32).reshape(-1)), t(z["v"].astype(np.float32).reshape(-1)),
+                 out16, S=S, start_pos=start, n_q_heads=nH, n_kv_heads=kvH, head_dim=hd, window=16, o_in=0.0)
+    torch.cuda.synchronize()
+    contract_close(out16.float().cpu().numpy().reshape(S, nH, hd), z["expected_q16_w16"], "attn_gemm mirror")
 
 
 @pytest.mark.parametrize("window", [0, 512])
