@@ -177,7 +177,7 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
         sa.kv_write(kd[t:t + 1], vd[t:t + 1], kc, vc, p, kvcfg, k_gain=kg,
                     rope_cos=c[p:p + 1], rope_sin=sn[p:p + 1])
         sa.decode(qd, kc, vc, kl[t:t + 1], cfgs[kinds[i]], q_gain=qg, rope_cos=c[p:p + 1],
-                  rope_sin=sn[p:p + 1], out=outd, workspace=ws)
+                  rope_sin=sn[p:p + 1], out=outd, workspace=ws, max_key_len=p + 1)
 
     pre_ms = graph_time_ms([lambda: [prefill_layer(i) for i in range(n_layers)]], 1, 1)
     dec_ms = graph_time_ms([lambda: [decode_layer(i, t) for t in range(steps) for i in range(n_layers)]], 1, 0)

@@ -74,7 +74,8 @@ int g4a_version(void);
  *   key_len[s]  int32, device: keys of sequence s (params[1] keyLen); the query
  *               sits at position key_len[s]-1 (params[2] qOffset = pos).
  *               Sequence s attends keys [max(0, key_len-W), key_len) (W = window, 0 = all).
- *   max_key_len host upper bound of key_len[]; sizes the split-KV grid only.
+ *   max_key_len host upper bound of key_len[]; sizes the split-KV grid only (a tight
+ *               bound gives the best split).
  *   q           f32 [n_seq][n_q_heads][head_dim], raw: RMSNorm*q_gain then RoPE
  *               are applied in the kernel as attn_101 does (kernels_dsl.py:1593-1615).
  *   q_gain      f32 [head_dim] or NULL (no q RMSNorm).

@@ -126,14 +126,17 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
     _need(rope_cos, "rope_cos", torch.float32)
     _need(rope_sin, "rope_sin", torch.float32)
     if not torch.is_tensor(key_len):
-        key_len = torch.tensor(np.atleast_1d(np.asarray(key_len, np.int32)), device=q.device)
+        kl = np.atleast_1d(np.asarray(key_len, np.int32))
+        if max_key_len is None and kl.size:
+            max_key_len = int(kl.max())   # exact bound: lets a single sequence start loading early
+        key_len = torch.tensor(kl, device=q.device)
     _need(key_len, "key_len", torch.int32)
     if key_len.numel() != n_seq:
         raise ValueError("key_len must have one entry per sequence")
     if max_key_len is None:
         max_key_len = kc.shape[1]
-    if max_key_len > kc.shape[1]:
-        raise ValueError("max_key_len exceeds the cache length")
+    if not 0 < max_key_len <= kc.shape[1]:
+        raise ValueError("max_key_len must be in [1, cache length]")
     flags = _lib.KV_F32 if kc.dtype == torch.float32 else 0
     c = cfg.c(flags)
     lib = _lib.load()

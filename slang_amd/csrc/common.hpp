@@ -71,6 +71,31 @@ __device__ __forceinline__ float wave_max(float x) {
 // zero, which a softmax weight relative to the running maximum can afford.
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---------------------------------------------------------------- buffer loads
+// Raw buffer resource over [p, p + bytes): a load at a byte offset >= bytes returns zero
+// and touches no memory, so a NULL operand (bytes = 0) and rows past a range need neither
+// a branch nor an index clamp, and every load stays a plain vector-memory op (vmcnt only).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float bload_f32(rsrc_t r, int off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float2 bload_f32x2(rsrc_t r, int off) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ float4v bload_f32x4(rsrc_t r, int off) {
+    return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ half8 bload_h8(rsrc_t r, int off) {
+    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float8v bload_f8(rsrc_t r, int off) {
+    const float4v a = bload_f32x4(r, off), b = bload_f32x4(r, off + 16);
+    return float8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // ---------------------------------------------------------------- numerics
 // Static-range quantisation, identity when s == 0 (gemma4_150/reference.py:30-31).
 // x / s is the IEEE quotient and rintf rounds half to even, as numpy's round does.

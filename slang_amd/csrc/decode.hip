@@ -91,13 +91,13 @@ struct KOp;
 template <>
 struct KOp<half_t> {
     struct raw { half8 h; };
-    static __device__ __forceinline__ raw load(const half_t* p) { return raw{*reinterpret_cast<const half8*>(p)}; }
+    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_h8(r, off)}; }
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16x32(k.h, q, c); }
 };
 template <>
 struct KOp<float> {
     struct raw { float8v f; };
-    static __device__ __forceinline__ raw load(const float* p) { return raw{load8(p)}; }
+    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_f8(r, off)}; }
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) {
         const half8 hi = __builtin_convertvector(k.f, half8);
         const half8 lo = __builtin_convertvector(k.f - __builtin_convertvector(hi, float8v), half8);
@@ -110,13 +110,13 @@ struct VOp;
 template <>
 struct VOp<half_t> {
     typedef half8 raw;
-    static __device__ __forceinline__ half8 load(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+    static __device__ __forceinline__ half8 load(rsrc_t r, int off) { return bload_h8(r, off); }
     static __device__ __forceinline__ half8 h(half8 v) { return v; }
 };
 template <>
 struct VOp<float> {
     typedef float8v raw;
-    static __device__ __forceinline__ float8v load(const float* p) { return load8(p); }
+    static __device__ __forceinline__ float8v load(rsrc_t r, int off) { return bload_f8(r, off); }
     static __device__ __forceinline__ half8 h(float8v v) { return __builtin_convertvector(v, half8); }
 };
 
@@ -127,24 +127,36 @@ __device__ __forceinline__ float dpp_row_shl(float x) {
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + N, 0xF, 0xF, false));
 }
 
-// Keys attended by sequence b and how they are split: every kernel of a call derives the
-// same plan from key_len[b]. Active keys [lo, lo+active); split c covers
-// [lo + c*chunk, min(lo + (c+1)*chunk, hi)), c < n_act.
+// Keys attended by sequence b and how they are split: active keys [lo, hi), split c covers
+// [lo + c*chunk, min(lo + (c+1)*chunk, hi)); split c is live when c*chunk < hi - lo. No
+// division on the common path: the host's chunk fits max_splits splits of max_key_len keys;
+// only a key_len above max_key_len widens the chunk so the live splits still fit.
 struct SplitPlan {
-    int lo, hi, active, chunk, n_act;
+    int lo, hi, active, chunk;
 };
 __device__ __forceinline__ SplitPlan split_plan(const DecodeArgs& a, int b) {
     SplitPlan p;
     p.hi = a.key_len[b];
     p.lo = (a.window > 0 && p.hi > a.window) ? p.hi - a.window : 0;
     p.active = p.hi - p.lo;
-    p.chunk = a.chunk;  // keys per split (multiple of 16), chosen on the host
-    p.n_act = p.active > 0 ? (p.active + p.chunk - 1) / p.chunk : 0;
-    if (p.n_act > a.max_splits) {  // a key_len above the host's max_key_len: widen the splits
+    p.chunk = a.chunk;
+    if (p.active > a.max_splits * a.chunk)
         p.chunk = (((p.active + a.max_splits - 1) / a.max_splits) + 15) & ~15;
-        p.n_act = (p.active + p.chunk - 1) / p.chunk;
-    }
     return p;
+}
+
+// QP consecutive f32 (QP = 2 or 4) from a buffer
+template <int QP>
+__device__ __forceinline__ void bload_q(rsrc_t r, int off, float (&x)[QP]) {
+    if constexpr (QP == 2) {
+        const float2 v = bload_f32x2(r, off);
+        x[0] = v.x;
+        x[1] = v.y;
+    } else {
+        const float4v v = bload_f32x4(r, off);
+#pragma unroll
+        for (int e = 0; e < QP; ++e) x[e] = v[e];
+    }
 }
 
 template <int HD, int G, typename KVT>
@@ -152,6 +164,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     using Sh = DecodeShape<HD, G>;
     constexpr int KSTEPS = Sh::KSTEPS, NDT = Sh::NDT, VLANES = Sh::VLANES, VROWS = Sh::VROWS;
     constexpr int VLOADS = Sh::VLOADS, VSTR = Sh::VSTR, QSTR = Sh::QSTR;
+    constexpr int ESZ = (int)sizeof(KVT);
     using KO = KOp<KVT>;
     using VO = VOp<KVT>;
     typedef typename KO::raw kraw_t;
@@ -163,95 +176,101 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     half_t* sV = reinterpret_cast<half_t*>(arena);
     float* lds = reinterpret_cast<float*>(arena);
     __shared__ float lds_m[4][G], lds_l[4][G];
-    __shared__ float s_M[G], s_L[G], s_W[4][G];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     const int n = lane & 15, g = lane >> 4;
     const int ci = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pair = b * a.n_kv_heads + kh;
-
-    // ---- q operand loads first: they depend on nothing but the sequence and kv head
-    constexpr int QP = HD / 128;  // elements per lane in each half of a head row
-    const int d0 = QP * lane;     // this lane: dims d0.. and d0+HD/2..
-    float qx[2][QP], qgv[2][QP], qcv[QP], qsv[QP];
-    {
-        const float* qb = a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
-        const float* gp = a.q_gain ? a.q_gain : kOnes;
-        const float* cp = a.rcos ? a.rcos + (size_t)b * (HD / 2) : kOnes;
-        const float* sp = a.rsin ? a.rsin + (size_t)b * (HD / 2) : kZeros;
-        const int hh = wave < G ? wave : 0;
-#pragma unroll
-        for (int e = 0; e < QP; ++e) {
-            qx[0][e] = qb[hh * HD + d0 + e];
-            qx[1][e] = qb[hh * HD + HD / 2 + d0 + e];
-            qgv[0][e] = gp[d0 + e];
-            qgv[1][e] = gp[HD / 2 + d0 + e];
-            qcv[e] = cp[d0 + e];
-            qsv[e] = sp[d0 + e];
-        }
-    }
-
-    // ---- attended keys and this workgroup's split
-    const SplitPlan sp = split_plan(a, b);
     float* outp = a.out + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
-    if (sp.active <= 0) {  // no keys: defined output of zeros
-        if (ci == 0)
-            for (int e = tid; e < G * HD; e += 256) outp[e] = 0.0f;
+    const SplitPlan sp = split_plan(a, b);  // scalar load of key_len, issued first
+
+    // ---- q operand loads: they depend on nothing but the sequence and kv head.
+    // Wave w prepares heads w, w+4 (a head >= G reads past the q range: zeros, no traffic).
+    constexpr int QP = HD / 128;          // elements per lane in each half of a head row
+    constexpr int NQH = (G + 3) / 4;      // heads per wave
+    const int d0 = QP * lane;             // this lane: dims d0.. and d0+HD/2..
+    const rsrc_t rq = make_rsrc(a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD, G * HD * 4);
+    const rsrc_t rg = make_rsrc(a.q_gain, a.q_gain ? HD * 4 : 0);
+    const rsrc_t rc = make_rsrc(a.rcos ? a.rcos + (size_t)b * (HD / 2) : nullptr, a.rcos ? HD * 2 : 0);
+    const rsrc_t rs = make_rsrc(a.rsin ? a.rsin + (size_t)b * (HD / 2) : nullptr, a.rsin ? HD * 2 : 0);
+    float qx[NQH][2][QP], qgv[2][QP], qcv[QP], qsv[QP];
+#pragma unroll
+    for (int j = 0; j < NQH; ++j) {
+        bload_q<QP>(rq, ((wave + 4 * j) * HD + d0) * 4, qx[j][0]);
+        bload_q<QP>(rq, ((wave + 4 * j) * HD + HD / 2 + d0) * 4, qx[j][1]);
+    }
+    bload_q<QP>(rg, d0 * 4, qgv[0]);
+    bload_q<QP>(rg, (HD / 2 + d0) * 4, qgv[1]);
+    bload_q<QP>(rc, d0 * 4, qcv);
+    bload_q<QP>(rs, d0 * 4, qsv);
+
+    // ---- attended keys and this workgroup's split. With one split slot (no merge kernel)
+    // this workgroup writes `out`; otherwise every slot gets a partial, and a slot past the
+    // live splits a weightless (m = -inf, l = 0) marker, so the merge needs no key count.
+    const bool single = a.max_splits == 1;
+    if (ci * sp.chunk >= sp.active) {
+        if (single) {
+            for (int e = tid; e < G * HD; e += 256) outp[e] = 0.0f;  // no keys: zeros
+        } else if (tid < G) {
+            a.part_ml[((size_t)pair * a.max_splits + ci) * G + tid] = make_float2(kNegInf, 0.0f);
+        }
         return;
     }
-    const int n_act = sp.n_act;
-    if (ci >= n_act) return;
     const int k0 = sp.lo + ci * sp.chunk;
     const int k1 = min(k0 + sp.chunk, sp.hi);
 
-    // ---- block loads: K in the MFMA A layout (lane n,g: key n, dims 32s+8g..), V rows
-    const size_t rstride = (size_t)a.n_kv_heads * HD;
-    const KVT* kbase = reinterpret_cast<const KVT*>(a.kc) + (size_t)b * a.seq_stride + (size_t)kh * HD + 8 * g;
-    const KVT* vbase = reinterpret_cast<const KVT*>(a.vc) + (size_t)b * a.seq_stride + (size_t)kh * HD +
-                       8 * (lane % VLANES);
+    // ---- block loads through buffer resources over rows [k0, k1) of this kv head: rows
+    // past k1 read as zeros without memory traffic, so no index is clamped. K in the MFMA
+    // A layout (lane n,g: key n, dims 32s+8g..), V rows of VLANES lanes.
+    const size_t rstride = (size_t)a.n_kv_heads * HD;  // elements per cache row
+    const int rsb = (int)(rstride * ESZ);               // bytes per cache row
+    const uint32_t range = (uint32_t)(k1 - k0) * (uint32_t)rsb;
+    const size_t row0 = (size_t)b * a.seq_stride + (size_t)k0 * rstride + (size_t)kh * HD;
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const KVT*>(a.kc) + row0, range);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const KVT*>(a.vc) + row0, range);
     const int vrow = lane / VLANES;
+    const int koff = n * rsb + 8 * g * ESZ, voff = vrow * rsb + 8 * (lane % VLANES) * ESZ;
     kraw_t kr[KSTEPS];
     vraw_t vr[VLOADS];
     auto load_block = [&](int blk) {
-        const int kk = min(blk + n, k1 - 1);
+        const int r = (blk - k0) * rsb;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::load(kbase + (size_t)kk * rstride + 32 * s);
+        for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::load(rk, r + koff + 32 * s * ESZ);
 #pragma unroll
-        for (int i = 0; i < VLOADS; ++i) {
-            const int kv = min(blk + VROWS * i + vrow, k1 - 1);
-            vr[i] = VO::load(vbase + (size_t)kv * rstride);
-        }
+        for (int i = 0; i < VLOADS; ++i) vr[i] = VO::load(rv, r + VROWS * i * rsb + voff);
     };
     int blk = k0 + wave * 16;
-    if (blk < k1) load_block(blk);  // in flight during the q prologue
+    if (blk < k1) load_block(blk);  // in flight during the q prologue (wave-uniform branch)
 
-    // ---- q prologue: wave w prepares head w (and w+4): RMSNorm*gain, RoPE, scale*log2 e,
-    // split into f16 high/low rows of the B operand, staged in LDS.
-#pragma unroll
-    for (int hh = wave; hh < G; hh += 4) {
-        float x[2][QP];
-        if (hh != wave) {  // G = 8: second head of this wave
-            const float* qb = a.q + ((size_t)b * a.n_q_heads + (size_t)kh * G + hh) * HD;
-#pragma unroll
-            for (int e = 0; e < QP; ++e) {
-                qx[0][e] = qb[d0 + e];
-                qx[1][e] = qb[HD / 2 + d0 + e];
-            }
-        }
+    // ---- q prologue: RMSNorm*gain, RoPE, scale*log2 e, split into f16 high/low rows of
+    // the B operand, staged in LDS.
+    if (!a.rcos) {
 #pragma unroll
         for (int e = 0; e < QP; ++e) {
-            x[0][e] = qx[0][e];
-            x[1][e] = qx[1][e];
+            qcv[e] = 1.0f;
+            qsv[e] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NQH; ++j) {
+        const int hh = wave + 4 * j;
+        if (hh >= G) break;
+        float x[2][QP];
+#pragma unroll
+        for (int e = 0; e < QP; ++e) {
+            x[0][e] = qx[j][0][e];
+            x[1][e] = qx[j][1][e];
         }
         if (a.q_gain) {
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < QP; ++e) ss += x[0][e] * x[0][e] + x[1][e] * x[1][e];
-            const float rs = 1.0f / sqrtf(wave_sum(ss) / (float)HD + a.eps);  // attn_101's q * nscale * w
+            const float rsq = 1.0f / sqrtf(wave_sum(ss) / (float)HD + a.eps);  // attn_101's q * nscale * w
 #pragma unroll
             for (int e = 0; e < QP; ++e) {
-                x[0][e] = x[0][e] * rs * qgv[0][e];
-                x[1][e] = x[1][e] * rs * qgv[1][e];
+                x[0][e] = x[0][e] * rsq * qgv[0][e];
+                x[1][e] = x[1][e] * rsq * qgv[1][e];
             }
         }
 #pragma unroll
@@ -282,12 +301,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
 
     for (; blk < k1; blk += 64) {
-#pragma unroll
-        for (int i = 0; i < VLOADS; ++i)
-            *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
         float4v c4 = float4v{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
+#pragma unroll
+        for (int i = 0; i < VLOADS; ++i)
+            *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
         if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during softmax and P.V
         float sc[4], mloc = kNegInf;
 #pragma unroll
@@ -308,116 +327,109 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             pb[i] = (half_t)p;
         }
         const float corr = fexp2(m_run - m_use);
-        l_run = l_run * corr + ps;
-        m_run = m_new;
-        if (__any(corr != 1.0f)) {
+        // the first block of a wave starts from zero accumulators: nothing to rescale
+        if (blk != k0 + wave * 16 && __any(corr != 1.0f)) {
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
         }
+        l_run = l_run * corr + ps;
+        m_run = m_new;
         // O^T += V^T . P^T : lane n of group g supplies V[key 4g + n/4][16dt + 4(n%4) ..]
         const half_t* vrd = myV + (4 * g + (n >> 2)) * VSTR + 4 * (n & 3);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma16x16(lds_read_tr16(vrd + 16 * dt), pb, oacc[dt]);
     }
 
-    // ---- wave partial: column sums, then the head columns to LDS
+    // ---- workgroup merge of the wave partials through LDS: one barrier, then every thread
+    // owns 4 consecutive outputs of one head and weighs the 4 waves itself.
     l_run = add32(add16(l_run));
     __syncthreads();  // every wave is done with its V block: the arena takes the partials
     if (n < G) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) lds[(wave * G + n) * HD + 16 * dt + 4 * g + i] = oacc[dt][i];
+            *reinterpret_cast<float4v*>(&lds[(wave * G + n) * HD + 16 * dt + 4 * g]) = oacc[dt];
         if (g == 0) {
             lds_m[wave][n] = m_run;
             lds_l[wave][n] = l_run;
         }
     }
     __syncthreads();
-    if (tid < G) {
-        float M = kNegInf;
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, lds_m[w][tid]);
-        float L = 0.0f;
-        for (int w = 0; w < 4; ++w) {
-            const float wt = fexp2(lds_m[w][tid] - M);
-            s_W[w][tid] = wt;
-            L += lds_l[w][tid] * wt;
-        }
-        s_M[tid] = M;
-        s_L[tid] = L;
-    }
-    __syncthreads();
-
-    const bool single = (n_act == 1);
-    float* po = a.part_o + ((size_t)pair * a.max_splits + ci) * (G * HD);
-    for (int e = tid; e < G * HD; e += 256) {
+    for (int e = 4 * tid; e < G * HD; e += 1024) {
         const int hh = e / HD;
-        float o = 0.0f;
+        float mw[4], M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) o += lds[w * G * HD + e] * s_W[w][hh];
-        if (single)
-            outp[e] = srq(o * (1.0f / s_L[hh]), a.out_q);
-        else
-            po[e] = o;
+        for (int w = 0; w < 4; ++w) {
+            mw[w] = lds_m[w][hh];
+            M = fmaxf(M, mw[w]);
+        }
+        float L = 0.0f;
+        float4v o = float4v{0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float wt = mw[w] == kNegInf ? 0.0f : fexp2(mw[w] - M);
+            L += lds_l[w][hh] * wt;
+            o += *reinterpret_cast<const float4v*>(&lds[w * G * HD + e]) * wt;
+        }
+        if (single) {
+            const float inv = 1.0f / L;
+            float4v r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = srq(o[i] * inv, a.out_q);
+            *reinterpret_cast<float4v*>(outp + e) = r;
+        } else {
+            *reinterpret_cast<float4v*>(a.part_o + ((size_t)pair * a.max_splits + ci) * (G * HD) + e) = o;
+            if (e % HD == 0) a.part_ml[((size_t)pair * a.max_splits + ci) * G + hh] = make_float2(M, L);
+        }
     }
-    if (single) return;
-    if (tid < G) a.part_ml[((size_t)pair * a.max_splits + ci) * G + tid] = make_float2(s_M[tid], s_L[tid]);
 }
 
 // Merge of the split partials: out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max_c m_c
 // (the flash-decoding identity attn_101 applies in its last chunk, kernels_dsl.py:1717-1749).
-// One workgroup per (64 output dims, kv head, sequence): thread (split group sg, dim d) loads
-// splits c = sg, sg+4, ... of its output element in one batch of up to 16 (loads are
-// unconditional: the index is clamped and padded splits weigh 0), then the four split groups
-// are summed through LDS. Sequences whose keys fit one split were finished by decode_kernel.
-template <int HD, int G>
+// One workgroup per (64 output dims, kv head, sequence). It needs no key count: every one
+// of the max_splits slots holds a partial or a weightless marker, so all loads are issued
+// at entry. Thread (split group sg, dim d) reads splits sg, sg+4, .. of its output element
+// (NB batches of 64; slots past max_splits read as zeros through the buffer range), thread
+// t reads (m, l) of split t. A slot of weight 0 is dropped by a select, never multiplied
+// in: a marker slot's o holds whatever an earlier call left there.
+template <int HD, int G, int NB>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-    constexpr int E = G * HD;
+    constexpr int E = G * HD, NU = 16 * NB;
     __shared__ float wts[256];
     __shared__ float red[4][64];
-    __shared__ float s_red[4], s_L;
+    __shared__ float s_red[4], s_red2[4];
     const int tid = threadIdx.x, lane = tid & 63, sg = tid >> 6;
     const int e = blockIdx.x * 64 + lane, hh = (blockIdx.x * 64) / HD;
     const int kh = blockIdx.y, b = blockIdx.z, pair = b * a.n_kv_heads + kh;
-    const SplitPlan sp = split_plan(a, b);
-    const int n_act = sp.n_act;
-    if (n_act <= 1) return;
-    const float* po = a.part_o + (size_t)pair * a.max_splits * E + e;
-    const float2* ml = a.part_ml + (size_t)pair * a.max_splits * G + hh;
-    float v[16];
+    const int S = a.max_splits;
+    const rsrc_t ro = make_rsrc(a.part_o + (size_t)pair * S * E, (uint32_t)S * E * 4);
+    const rsrc_t rml = make_rsrc(a.part_ml + (size_t)pair * S * G, (uint32_t)S * G * 8);
+    float v[NU];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(sg + 4 * u, n_act - 1) * E];
-    // weights of every split for this head
-    const float2 mlt = ml[(size_t)min(tid, n_act - 1) * G];
-    float mloc = tid < n_act ? mlt.x : kNegInf;
-    mloc = wave_max(mloc);
+    for (int u = 0; u < NU; ++u) v[u] = bload_f32(ro, ((sg + 4 * u) * E + e) * 4);
+    const float2 mlt = bload_f32x2(rml, (tid * G + hh) * 8);
+    const float mt = tid < S ? mlt.x : kNegInf;
+    const float mloc = wave_max(mt);
     if (lane == 0) s_red[sg] = mloc;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float w = tid < n_act ? fexp2(mlt.x - M) : 0.0f;
+    const float w = mt == kNegInf ? 0.0f : fexp2(mt - M);
     wts[tid] = w;
-    const float lw = wave_sum(w * (tid < n_act ? mlt.y : 0.0f));
+    const float lw = wave_sum(w == 0.0f ? 0.0f : w * mlt.y);
+    if (lane == 0) s_red2[sg] = lw;
     __syncthreads();
-    if (lane == 0) s_red[sg] = lw;
-    __syncthreads();
-    if (tid == 0) s_L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
     float o = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) o = fmaf(wts[min(sg + 4 * u, 255)] * (sg + 4 * u < n_act ? 1.0f : 0.0f), v[u], o);
-    for (int c0 = 64; c0 < n_act; c0 += 64) {  // more than 64 splits: further batches
-#pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(c0 + sg + 4 * u, n_act - 1) * E];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int c = c0 + sg + 4 * u;
-            o = fmaf(c < n_act ? wts[c] : 0.0f, v[u], o);
-        }
+    for (int u = 0; u < NU; ++u) {
+        const float wc = wts[sg + 4 * u];
+        o = wc != 0.0f ? fmaf(wc, v[u], o) : o;
     }
     red[sg][lane] = o;
     __syncthreads();
     if (sg == 0) {
+        const float L = (s_red2[0] + s_red2[1]) + (s_red2[2] + s_red2[3]);
         const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-        a.out[((size_t)b * a.n_q_heads + (size_t)kh * G) * HD + e] = srq(t * (1.0f / s_L), a.out_q);
+        // L = 0 only when the sequence attends no key: defined output of zeros
+        a.out[((size_t)b * a.n_q_heads + (size_t)kh * G) * HD + e] = L > 0.0f ? srq(t * (1.0f / L), a.out_q) : 0.0f;
     }
 }
 
@@ -428,16 +440,19 @@ static int env_int(const char* name, int dflt) {
 }
 
 // Keys per split: spread the worst-case work (every sequence at max_key_len) over about
-// G4A_DECODE_TARGET_WGS workgroups, but never below G4A_DECODE_MIN_CHUNK keys, so the
-// partial (G*hd floats) stays small next to the K/V it summarises.
+// G4A_DECODE_TARGET_WGS workgroups, never below G4A_DECODE_MIN_CHUNK keys; a chunk of 64 keys
+// (every wave of the workgroup busy) is preferred as long as it still yields 128 or more
+// workgroups. At most 256 splits per sequence, chunk a multiple of the 16-key block.
 static int decode_chunk(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     const long pairs = (long)n_seq * cfg->n_kv_heads;
     long max_active = max_key_len;
     if (cfg->window > 0 && (long)cfg->window < max_active) max_active = cfg->window;
-    const long target = env_int("G4A_DECODE_TARGET_WGS", 1024);
-    long min_chunk = env_int("G4A_DECODE_MIN_CHUNK", 32);
-    long chunk = (max_active * pairs + target - 1) / target;
+    const long target = env_int("G4A_DECODE_TARGET_WGS", 512);
+    const long min_chunk = env_int("G4A_DECODE_MIN_CHUNK", 16);
+    const long kp = max_active * pairs;
+    long chunk = (kp + target - 1) / target;
     if (chunk < min_chunk) chunk = min_chunk;
+    if (chunk < 64 && kp >= 128L * 64) chunk = 64;
     if ((max_active + chunk - 1) / chunk > 256) chunk = (max_active + 255) / 256;
     return (int)((chunk + 15) & ~15L);
 }
@@ -481,13 +496,19 @@ static decode_fn pick_g(int G, bool f32) {
     }
     return nullptr;
 }
+template <int HD, int G>
+static decode_fn pick_merge_nb(int splits) {
+    if (splits <= 64) return decode_merge_kernel<HD, G, 1>;
+    if (splits <= 128) return decode_merge_kernel<HD, G, 2>;
+    return decode_merge_kernel<HD, G, 4>;
+}
 template <int HD>
-static decode_fn pick_merge(int G) {
+static decode_fn pick_merge(int G, int splits) {
     switch (G) {
-        case 1: return decode_merge_kernel<HD, 1>;
-        case 2: return decode_merge_kernel<HD, 2>;
-        case 4: return decode_merge_kernel<HD, 4>;
-        case 8: return decode_merge_kernel<HD, 8>;
+        case 1: return pick_merge_nb<HD, 1>(splits);
+        case 2: return pick_merge_nb<HD, 2>(splits);
+        case 4: return pick_merge_nb<HD, 4>(splits);
+        case 8: return pick_merge_nb<HD, 8>(splits);
     }
     return nullptr;
 }
@@ -563,6 +584,10 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     a.window = (int)cfg->window;
     a.max_splits = splits;
     a.chunk = decode_chunk(cfg, n_seq, max_key_len);
+    if ((int64_t)(a.chunk + 64) * cfg->n_kv_heads * HD * (int64_t)esz > 0x7fffffff) {
+        set_error("keys per split too large for 32-bit buffer offsets");
+        return G4A_EINVAL;
+    }
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;
@@ -576,7 +601,7 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "decode launch");
     if (splits > 1) {
-        decode_fn mf = HD == 256 ? pick_merge<256>(G) : pick_merge<512>(G);
+        decode_fn mf = HD == 256 ? pick_merge<256>(G, splits) : pick_merge<512>(G, splits);
         hipLaunchKernelGGL(mf, dim3(G * HD / 64, cfg->n_kv_heads, n_seq), dim3(256), 0, (hipStream_t)stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return hip_error(e, "decode merge launch");

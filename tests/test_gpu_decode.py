@@ -203,6 +203,27 @@ def test_deterministic_and_workspace_reuse():
     assert int(a.count_nonzero()) > 0
 
 
+def test_stale_nan_workspace_and_empty_sequence():
+    """Split slots past a sequence's live splits carry weightless (m = -inf, l = 0) markers:
+    stale NaN partials left in the workspace must not leak into the merge, and a sequence
+    with no keys gives zeros (the grid is sized for max_key_len = the cache length)."""
+    B, nH, kvH, hd, T = 3, 8, 2, 256, 4096
+    lens = np.array([T, 100, 0], np.int32)
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((B, nH, hd)).astype(np.float32)
+    k = rng.standard_normal((B, T, kvH, hd)).astype(np.float16)
+    v = rng.standard_normal((B, T, kvH, hd)).astype(np.float16)
+    ws = sa.DecodeWorkspace(DEV)
+    ws.get(1 << 24).fill_(0xFF)             # every f32 partial reads as NaN
+    out = sa.decode(t(q), t(k), t(v), t(lens), sa.AttnConfig(nH, kvH, hd), workspace=ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for b in range(2):
+        ref = O.decode_attention(q[b], k[b, :lens[b]], v[b, :lens[b]], int(lens[b]), kvH)
+        contract_close(got[b], ref, f"seq {b} len {lens[b]}")
+    assert np.array_equal(got[2], np.zeros_like(got[2]))
+
+
 def test_attn_101_mirror_matches_decode():
     """The reference-slot drop-in (params = (1, keyLen, pos, qH, kvH, W, 0, 0))."""
     z = gold("attn101.npz")
