@@ -35,9 +35,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+# per-file additions: the prefill kernels keep their MFMA accumulators in VGPRs, so the
+# online-softmax rescale of the 128 accumulator registers does not make the compiler copy
+# them between register files on every tile
+FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *CXXFLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *CXXFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     p = subprocess.run(cmd, capture_output=True, text=True)

@@ -163,7 +163,7 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss += x[s][i] * x[s][i];
+            for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[s][i], x[s][i], ss);
         ss = add32(add16(ss));
         const float rs = 1.0f / sqrtf(ss / (float)HD + eps);  // x * rs * w, as the reference kernels
 #pragma unroll
@@ -176,8 +176,8 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
-            x[s][i] = x0 * cv[s][i] - x1 * sv[s][i];
-            x[s + KSTEPS / 2][i] = x1 * cv[s][i] + x0 * sv[s][i];
+            x[s][i] = __builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i]));  // explicit fma: every
+            x[s + KSTEPS / 2][i] = __builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]);  // user rounds alike
         }
 }
 

@@ -19,6 +19,8 @@
 // is computed. Scores stay f32 in the MFMA accumulators; P is rounded to f16 only as
 // the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last] are skipped;
 // boundary tiles are masked per element. Work-groups are launched longest-causal-row first.
+#include <stdlib.h>
+
 #include "common.hpp"
 
 namespace g4a {
@@ -252,7 +254,284 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) store_elem(orow + 16 * dt + 4 * g + i, srq(oacc[dt][i] * inv_l, a.out_q));
 }
 
+// ---------------------------------------------------------------- hd 256 / f16 cache path
+// prefill_kernel_w32: the same attention with 32 query columns per wave (128 per workgroup:
+// G heads x 128/G positions) on v_mfma_f32_32x32x16_f16, which halves the LDS bytes each
+// MFMA FLOP costs compared with 16 columns per wave. K/V tiles of 64 keys go straight from
+// HBM into LDS (buffer_load ... lds, 16 B per lane, no staging registers), double buffered,
+// one barrier per tile. LDS rows are 512 B with the 16-byte chunk c of row r stored at
+// chunk position c ^ (r % 32), so the K reads (32 rows, one chunk column) and the
+// transposed V reads spread over all banks. The O^T accumulators (256 dims x 32 columns)
+// live in AGPRs; the running maximum is only moved when a score exceeds it by more than
+// 2^8, so rescaling them is rare and P stays <= 256 in f16.
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int G, typename OUTT>
+__global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
+    constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
+    constexpr int ROWB = HD * 2;      // bytes per LDS tile row
+    constexpr int TILEB = KT * ROWB;  // one K or V tile
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n32 = lane & 31, h = lane >> 5;
+    const int qb = a.n_qblocks - 1 - (int)blockIdx.x;  // longest causal rows first
+    const int kh = blockIdx.y;
+    const int T_total = a.start_pos + a.S;
+
+    // ---- this lane's query column (head hh, position offset pl) and 8-dim half h
+    const int c = 32 * wave + n32;
+    const int hh = c % G, pl = c / G;
+    const int s_raw = qb * BQ + pl;
+    const bool col_ok = s_raw < a.S;
+    const int s_idx = col_ok ? s_raw : a.S - 1;
+    const int pos = a.start_pos + s_idx;
+
+    // ---- q prologue: lane (column, h) holds dims 16s + 8h + i (s < 16, i < 8), the B
+    // operand layout of the 32x32x16 MFMA. The arithmetic, including the order of the
+    // sum of squares, is that of prep_q_column (qprep_kernel), so both round q to the
+    // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
+    half8 qf[16];
+    {
+        // workgroup-uniform resources (a per-lane base would make the compiler loop over
+        // lanes); the row of this lane's column is in the offset
+        const rsrc_t rq = make_rsrc(a.q, (uint32_t)a.S * a.n_q_heads * HD * 4);
+        const rsrc_t rgn = make_rsrc(a.q_gain, a.q_gain ? HD * 4 : 0);
+        const rsrc_t rc = make_rsrc(a.rcos, a.rcos ? (uint32_t)a.S * HD * 2 : 0);
+        const rsrc_t rs = make_rsrc(a.rsin, a.rsin ? (uint32_t)a.S * HD * 2 : 0);
+        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 4, co = s_idx * HD * 2;
+        float x[16][8];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float8v v = bload_f8(rq, qo + (16 * s + 8 * h) * 4);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = v[i];
+        }
+        if (a.q_gain) {
+            float se = 0.0f, so = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    se = __builtin_fmaf(x[2 * s][i], x[2 * s][i], se);
+                    so = __builtin_fmaf(x[2 * s + 1][i], x[2 * s + 1][i], so);
+                }
+            const float ss = add32(se) + add32(so);
+            const float rsq = 1.0f / sqrtf(ss / (float)HD + a.eps);  // x * rs * w, as the reference kernels
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const float8v gv = bload_f8(rgn, (16 * s + 8 * h) * 4);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rsq * gv[i];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            float8v cv = bload_f8(rc, co + (16 * s + 8 * h) * 4), sv = bload_f8(rs, co + (16 * s + 8 * h) * 4);
+            if (!a.rcos) {
+                cv = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+                sv = float8v{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x0 = x[s][i], x1 = x[s + 8][i];
+                x[s][i] = __builtin_fmaf(x0, cv[i], -(x1 * sv[i]));
+                x[s + 8][i] = __builtin_fmaf(x1, cv[i], x0 * sv[i]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+        // q is only ever an MFMA B operand, which may sit in AGPRs: that leaves the VGPRs to
+        // the O^T accumulators, the scores and the LDS operand batches
+#pragma unroll
+        for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+    }
+
+    // ---- key ranges: workgroup [wg_lo, kv_hi), this wave [w_lo, wp1], this column [col_lo, pos]
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, T_total);
+    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
+    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
+    const int wp0 = p0 + (32 * wave) / G;
+    const int wp1 = min(p0 + (32 * wave + 31) / G, T_total - 1);
+    const int w_lo = a.window > 0 ? max(0, wp0 + 1 - a.window) : 0;
+    const int col_lo = a.window > 0 ? pos + 1 - a.window : 0;
+
+    // K/V of this kv head through buffer resources: rows >= kv_hi read as zeros
+    const int rowg = a.n_kv_heads * HD * 2;  // global bytes per cache row
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const half_t*>(a.kc) + (size_t)kh * HD, (uint32_t)kv_hi * rowg);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const half_t*>(a.vc) + (size_t)kh * HD, (uint32_t)kv_hi * rowg);
+    // wave w fills tile rows 16w .. 16w+15, two rows (1 KiB) per instruction
+    auto issue = [&](int t, int buf) {
+        const int kb = wg_lo + t * KT;
+        char* kdst = lds + buf * 2 * TILEB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 16 * wave + 2 * j + h;  // tile row of this lane
+            const int voff = (kb + r) * rowg + 16 * (n32 ^ (r & 31));
+            char* d = kdst + (16 * wave + 2 * j) * ROWB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)d, 16, voff, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(d + TILEB), 16, voff, 0, 0, 0);
+        }
+    };
+
+    float16v oacc[8];  // O^T[32dt + 8(r/4) + 4h + r%4][column]
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[dt] = float16v{};
+    float m_use = kNegInf, l_run = 0.0f;
+    bool started = false;
+
+    // transposed V reads: 16-lane group (h, half16), lane m supplies row 4h + m/4 (+8, +16u),
+    // dims 32dt + 16 half16 + 4(m%4) .. +3
+    const int m16 = lane & 15, half16 = (lane >> 4) & 1;
+    const int vr0 = 4 * h + (m16 >> 2);
+    const int vc0 = 2 * half16 + ((m16 & 3) >> 1);  // chunk within a 32-dim tile
+    const int vb0 = 8 * (m16 & 1);                   // byte within the chunk
+
+    if (n_tiles > 0) issue(0, 0);
+    for (int t = 0; t < n_tiles; ++t) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile t is in LDS
+        __syncthreads();                                    // all parts; tile t-1 fully consumed
+        if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
+        const int kb = wg_lo + t * KT;
+        if (kb > wp1 || kb + KT - 1 < w_lo) continue;  // no key of this tile for this wave
+        const char* K = lds + (t & 1) * 2 * TILEB;
+        const char* V = K + TILEB;
+
+        // S^T = K . Q^T: two 32-key sub-tiles, 16 k-steps of 16 dims; the A operands of a
+        // sub-tile are read in one batch ahead of its MFMAs
+        float16v sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            sacc[kt] = float16v{};
+            const char* krow = K + (32 * kt + n32) * ROWB;
+#pragma unroll
+            for (int s0 = 0; s0 < 16; s0 += 8) {
+                half8 kv[8];
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    kv[s] = *reinterpret_cast<const half8*>(krow + 16 * ((2 * (s0 + s) + h) ^ n32));
+#pragma unroll
+                for (int s = 0; s < 8; ++s) sacc[kt] = mfma32(kv[s], qf[s0 + s], sacc[kt]);
+            }
+        }
+        // keep 4 LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 28; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+
+        // scores of this lane: key kb + 4h + 32kt + 8(r/4) + r%4 of its column, log2 domain;
+        // tiles inside every column's range skip the per-element mask
+        const bool masked = (kb + KT - 1 > wp0) || (a.window > 0 && kb < wp1 + 1 - a.window);
+        if (masked) {
+            const int rel_hi = pos - (kb + 4 * h), rel_lo = col_lo - (kb + 4 * h);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int o = 32 * kt + 8 * (r >> 2) + (r & 3);
+                    sacc[kt][r] = (o <= rel_hi && o >= rel_lo) ? sacc[kt][r] : kNegInf;
+                }
+        }
+        float mloc = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                sacc[kt][r] *= a.scale_log2;
+                mloc = fmaxf(mloc, sacc[kt][r]);
+            }
+        mloc = max32(mloc);  // the column's other half sits in lane ^ 32
+        // move the running max only when a score passes it by more than 2^8
+        const bool bump = mloc > m_use + 8.0f;
+        if (__any(bump)) {
+            const float m_new = bump ? mloc : m_use;
+            const float corr = m_use == kNegInf ? 0.0f : fexp2(m_use - m_new);
+            l_run *= corr;
+            if (started) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) oacc[dt] *= corr;
+            }
+            m_use = m_new;
+        }
+        started = true;
+        const float msub = m_use == kNegInf ? 0.0f : m_use;
+        half8 pb[4];
+        float ps = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float pv = fexp2(sacc[u >> 1][8 * (u & 1) + i] - msub);
+                ps += pv;
+                pb[u][i] = (half_t)pv;
+            }
+        l_run += ps;
+
+        // O^T += V^T . P^T over four 16-key steps; k-slot i < 4 is key 16u + 4h + i,
+        // i >= 4 is key 16u + 8 + 4h + i - 4, matching the S^T accumulator rows in pb
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int ra = 16 * u + vr0, rb = ra + 8;
+            half8 av[8];
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const int ch = 4 * dt + vc0;
+                const half4 lo = lds_tr16(reinterpret_cast<const half_t*>(V + ra * ROWB + 16 * (ch ^ (ra & 31)) + vb0));
+                const half4 hi = lds_tr16(reinterpret_cast<const half_t*>(V + rb * ROWB + 16 * (ch ^ (rb & 31)) + vb0));
+                av[dt] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) oacc[dt] = mfma32(av[dt], pb[u], oacc[dt]);
+        }
+        // transposed V reads kept ahead of the P.V MFMAs, two reads per MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+        for (int i = 0; i < 29; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+
+    // ---- epilogue: column sum over both halves, normalise, srq, store 4 dims at a time
+    const float l_tot = add32(l_run);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (col_ok) {
+        OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 32 * dt + 8 * j + 4 * h;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_elem(orow + d + i, srq(oacc[dt][4 * j + i] * inv, a.out_q));
+            }
+    }
+}
+
+template <int G>
+static void (*pick_w32(bool out32))(PrefillArgs) {
+    return out32 ? prefill_kernel_w32<G, float> : prefill_kernel_w32<G, half_t>;
+}
+
 typedef void (*prefill_fn)(PrefillArgs);
+
+static int getenv_flag(const char* name) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : 0;
+}
 
 template <int HD, int G, typename KVT, typename OUTT>
 static prefill_fn pick_hilo(bool hilo) {
@@ -319,7 +598,19 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     }
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
     const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
-    prefill_fn fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
+    // hd 256 with f16 caches and f16 q: the 32-column kernel; other modes the 16-column one
+    const bool w32 = HD == 256 && !kv32 && !hilo && getenv_flag("G4A_PREFILL_W16") == 0;
+    prefill_fn fn = nullptr;
+    if (w32) {
+        switch (G) {
+            case 1: fn = pick_w32<1>(out32); break;
+            case 2: fn = pick_w32<2>(out32); break;
+            case 4: fn = pick_w32<4>(out32); break;
+            case 8: fn = pick_w32<8>(out32); break;
+        }
+    } else {
+        fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
+    }
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
@@ -337,8 +628,13 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
-    const int BQ = 64 / G;
+    const int BQ = (w32 ? 128 : 64) / G;
     a.n_qblocks = (S + BQ - 1) / BQ;
+    if (w32 && ((int64_t)(start_pos + S) * cfg->n_kv_heads * HD * 2 > 0x7fffffff ||
+                (int64_t)S * cfg->n_q_heads * HD * 4 > 0x7fffffff)) {
+        set_error("q or cache rows beyond 32-bit buffer offsets");
+        return G4A_EINVAL;
+    }
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;
