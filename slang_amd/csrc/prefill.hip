@@ -259,9 +259,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 // G heads x 128/G positions) on v_mfma_f32_32x32x16_f16, which halves the LDS bytes each
 // MFMA FLOP costs compared with 16 columns per wave. K/V tiles of 64 keys go straight from
 // HBM into LDS (buffer_load ... lds, 16 B per lane, no staging registers), double buffered,
-// one barrier per tile. LDS rows are 512 B with the 16-byte chunk c of row r stored at
-// chunk position c ^ (r % 32), so the K reads (32 rows, one chunk column) and the
-// transposed V reads spread over all banks. The O^T accumulators (256 dims x 32 columns)
+// one barrier per tile. LDS rows are 512 B with the 16-byte chunk c of row r stored at a
+// swizzled position: c ^ (r % 32) for K, whose reads take one chunk of 32 consecutive rows,
+// and c ^ vswz(r % 4) for V, whose transposed reads take 2 (16 lanes) or 4 (32 lanes)
+// adjacent chunks of 4 consecutive rows: vswz = {0, 10, 12, 6} puts those rows' 32-byte
+// pairs in distinct 128-byte and their 64-byte quads in distinct 256-byte bank windows. The O^T accumulators (256 dims x 32 columns)
 // live in AGPRs; the running maximum is only moved when a score exceeds it by more than
 // 2^8, so rescaling them is rare and P stays <= 256 in f16.
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -269,6 +271,8 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+
+__device__ __forceinline__ int vswz(int r) { return (0x6CA0 >> (4 * (r & 3))) & 15; }
 
 template <int G, typename OUTT>
 __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
@@ -375,10 +379,11 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int r = 16 * wave + 2 * j + h;  // tile row of this lane
-            const int voff = (kb + r) * rowg + 16 * (n32 ^ (r & 31));
+            const int kvo = (kb + r) * rowg + 16 * (n32 ^ (r & 31));
+            const int vvo = (kb + r) * rowg + 16 * (n32 ^ vswz(r));
             char* d = kdst + (16 * wave + 2 * j) * ROWB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)d, 16, voff, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(d + TILEB), 16, voff, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)d, 16, kvo, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(d + TILEB), 16, vvo, 0, 0, 0);
         }
     };
 
@@ -394,6 +399,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     const int vr0 = 4 * h + (m16 >> 2);
     const int vc0 = 2 * half16 + ((m16 & 3) >> 1);  // chunk within a 32-dim tile
     const int vb0 = 8 * (m16 & 1);                   // byte within the chunk
+    const int vsw = vswz(vr0);                        // rows 16u + vr0 (+8) share r % 4
 
     if (n_tiles > 0) issue(0, 0);
     for (int t = 0; t < n_tiles; ++t) {
@@ -488,8 +494,8 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
                 const int ch = 4 * dt + vc0;
-                const half4 lo = lds_tr16(reinterpret_cast<const half_t*>(V + ra * ROWB + 16 * (ch ^ (ra & 31)) + vb0));
-                const half4 hi = lds_tr16(reinterpret_cast<const half_t*>(V + rb * ROWB + 16 * (ch ^ (rb & 31)) + vb0));
+                const half4 lo = lds_tr16(reinterpret_cast<const half_t*>(V + ra * ROWB + 16 * (ch ^ vsw) + vb0));
+                const half4 hi = lds_tr16(reinterpret_cast<const half_t*>(V + rb * ROWB + 16 * (ch ^ vsw) + vb0));
                 av[dt] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
 #pragma unroll
