@@ -167,8 +167,8 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
     def prefill_layer(i):
         kc, vc = caches[i]
         c, sn = tabs[kinds[i]]
-        sa.kv_write(kp, vp, kc, vc, 0, kvcfg, k_gain=kg, rope_cos=c, rope_sin=sn)
-        sa.prefill(qp, kc, vc, 0, cfgs[kinds[i]], q_gain=qg, rope_cos=c, rope_sin=sn, out=outp)
+        sa.kv_write(kp, vp, kc, vc, 0, kvcfg, k_gain=kg, rope_cos=c[:S], rope_sin=sn[:S])
+        sa.prefill(qp, kc, vc, 0, cfgs[kinds[i]], q_gain=qg, rope_cos=c[:S], rope_sin=sn[:S], out=outp)
 
     def decode_layer(i, t):
         kc, vc = caches[i]
