@@ -111,7 +111,9 @@ def prefill_case(sa, S, window, theta, steps, warmup, gen):
     kc, vc = make_caches(sa, 1, S, theta, gen)[0]
     cfg = sa.AttnConfig(NH, KVH, HD, window)
     out = torch.empty(S, NH, HD, device="cuda", dtype=torch.float16)
-    fn = lambda: sa.prefill(q, kc, vc, 0, cfg, q_gain=qg, rope_cos=cos, rope_sin=sin, out=out)  # noqa: E731
+    ws = sa.DecodeWorkspace("cuda")
+    fn = lambda: sa.prefill(q, kc, vc, 0, cfg, q_gain=qg, rope_cos=cos, rope_sin=sin, out=out,  # noqa: E731
+                            workspace=ws)
     ms = graph_time_ms([fn], steps, warmup)
     pairs = sum(min(p + 1, window) if window else p + 1 for p in range(S))
     flops = 4 * HD * NH * pairs
@@ -168,7 +170,8 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
         kc, vc = caches[i]
         c, sn = tabs[kinds[i]]
         sa.kv_write(kp, vp, kc, vc, 0, kvcfg, k_gain=kg, rope_cos=c[:S], rope_sin=sn[:S])
-        sa.prefill(qp, kc, vc, 0, cfgs[kinds[i]], q_gain=qg, rope_cos=c[:S], rope_sin=sn[:S], out=outp)
+        sa.prefill(qp, kc, vc, 0, cfgs[kinds[i]], q_gain=qg, rope_cos=c[:S], rope_sin=sn[:S], out=outp,
+                   workspace=ws)
 
     def decode_layer(i, t):
         kc, vc = caches[i]

@@ -106,7 +106,11 @@ int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* ke
  *   k_cache/v_cache rows [0, start_pos+S) already written (g4a_kv_write).
  *   out      f16 [S][n_q_heads][head_dim] (attnh), or f32 with G4A_OUT_F32.
  *   Token s attends keys [max(0, p+1-W), p] with p = start_pos+s (kernels_dsl.py:1986-1992).
- *   ws/ws_bytes: g4a_prefill_ws_bytes() bytes (0 in this build: ws may be NULL).
+ *   ws/ws_bytes: workspace of g4a_prefill_ws_bytes() bytes (256-byte aligned) for the
+ *            key split of short prompts: long causal rows are then spread over several
+ *            workgroups and merged by a second kernel on the same stream. It needs no
+ *            initialisation. With ws NULL or smaller, the call runs unsplit (same results
+ *            up to summation order, slower); ws_bytes() is 0 when no split would be used.
  */
 size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos);
 int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q, const float* q_gain,

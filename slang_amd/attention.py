@@ -25,7 +25,7 @@ from . import _lib
 from ._lib import G4ACfg, check
 
 __all__ = [
-    "AttnConfig", "DecodeWorkspace", "decode", "prefill", "qprep", "kv_write", "rope_tables",
+    "AttnConfig", "DecodeWorkspace", "Workspace", "decode", "prefill", "qprep", "kv_write", "rope_tables",
     "attn_101", "kvnorm", "kvnorm_b", "attn_prefill", "attn_gemm", "qprep_b",
 ]
 
@@ -82,7 +82,9 @@ def rope_tables(positions, head_dim: int, theta: float, cutoff: int | None = Non
 
 
 class DecodeWorkspace:
-    """Split-KV partials for ``decode`` (the reference's `partials` buffer, runner.py:367-371).
+    """Split-KV partials for ``decode`` (the reference's `partials` buffer, runner.py:367-371)
+    and for the key split of ``prefill`` on short prompts (the role of PrefillGPU's scores
+    buffer, prefill_gpu.py:229-256).
 
     Grows on demand; needs no initialisation. Calls that may run concurrently
     need separate workspaces.
@@ -96,6 +98,9 @@ class DecodeWorkspace:
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self.buf
+
+
+Workspace = DecodeWorkspace
 
 
 def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
@@ -154,13 +159,15 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
 
 
 def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
-            rope_sin=None, out=None, out_dtype=torch.float16, q_hilo: bool = False):
+            rope_sin=None, out=None, out_dtype=torch.float16, q_hilo: bool = False,
+            workspace: DecodeWorkspace | None = None):
     """Causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
 
     q [S][nH][hd] f32 raw; caches [>= start_pos+S][kvH][hd] f16/f32; rope_cos/sin
     [S][hd/2] rows for those positions. Returns out [S][nH][hd] (f16 by default).
     q_hilo keeps the normalised, rotated q at f32 accuracy (two f16 MFMA operands)
-    instead of rounding it to f16 as qprep_b does.
+    instead of rounding it to f16 as qprep_b does. Short prompts split long causal rows
+    over workgroups through `workspace` (allocated here when not given).
     """
     S = q.shape[0]
     if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
@@ -184,9 +191,11 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None
             (_lib.OUT_F32 if out.dtype == torch.float32 else 0) | (_lib.Q_HILO if q_hilo else 0)
     c = cfg.c(flags)
     lib = _lib.load()
+    ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos))
+    ws = (workspace or DecodeWorkspace(q.device)).get(ws_bytes) if ws_bytes else None
     check(lib.g4a_prefill(ctypes.byref(c), S, int(start_pos), _ptr(q), _ptr(q_gain), _ptr(rope_cos),
-                          _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), None, 0,
-                          ctypes.c_void_p(_stream())))
+                          _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(ws),
+                          0 if ws is None else ws.numel(), ctypes.c_void_p(_stream())))
     return out
 
 

@@ -124,6 +124,17 @@ __device__ __forceinline__ half8 load8h(const float* p) {
 __device__ __forceinline__ void store_elem(half_t* p, float v) { *p = (half_t)v; }
 __device__ __forceinline__ void store_elem(float* p, float v) { *p = v; }
 
+// 4 consecutive outputs (16-byte aligned for f32, 8-byte for f16) in one store
+__device__ __forceinline__ void store4(half_t* p, float4v v) {
+    *reinterpret_cast<half4*>(p) = __builtin_convertvector(v, half4);
+}
+__device__ __forceinline__ void store4(float* p, float4v v) { *reinterpret_cast<float4v*>(p) = v; }
+// srq of 4 values with one test of the step (0 = pass-through)
+__device__ __forceinline__ float4v srq4(float4v x, float s) {
+    if (s == 0.0f) return x;
+    return float4v{srq(x[0], s), srq(x[1], s), srq(x[2], s), srq(x[3], s)};
+}
+
 // Stand-ins for absent operands, so operand loads never sit behind a null test and
 // can all be issued before any arithmetic: gain 1 (used only when a norm is asked for)
 // and the identity rotation cos 1 / sin 0, which leaves x exactly unchanged.

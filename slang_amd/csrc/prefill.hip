@@ -35,6 +35,14 @@ struct PrefillArgs {
     void* out;
     int S, start_pos, n_q_heads, n_kv_heads, window, n_qblocks;
     float scale_log2, eps, out_q;
+    // key split of long causal rows (prefill_kernel_w32): split_tiles = 0 means none;
+    // otherwise a workgroup covers at most split_tiles key tiles of its query block and
+    // blocks with more tiles leave partials for prefill_merge_kernel
+    int split_tiles, max_pieces;
+    const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
+    half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
+                      // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
+    float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
 };
 
 #ifndef G4A_PREFILL_KT256
@@ -284,9 +292,40 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n32 = lane & 31, h = lane >> 5;
-    const int qb = a.n_qblocks - 1 - (int)blockIdx.x;  // longest causal rows first
     const int kh = blockIdx.y;
     const int T_total = a.start_pos + a.S;
+    // key tiles of query block b: [lo(b), hi(b)) in tiles of KT keys
+    auto block_tiles = [&](int b) {
+        const int b0 = a.start_pos + b * BQ;
+        const int hi = min(b0 + BQ, T_total), lo = a.window > 0 ? max(0, b0 + 1 - a.window) : 0;
+        return (hi - lo + KT - 1) / KT;
+    };
+    // ---- this workgroup's query block (longest causal rows first) and, with a key split,
+    // its piece: workgroup i walks the blocks from the longest, each holding
+    // ceil(tiles / split_tiles) pieces (a scalar loop over at most a few hundred blocks)
+    int qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
+    if (a.split_tiles > 0) {
+        int i = blockIdx.x;
+        for (qb = a.n_qblocks - 1; qb > 0; --qb) {
+            const int np = max(1, (block_tiles(qb) + a.split_tiles - 1) / a.split_tiles);
+            if (i < np) break;
+            i -= np;
+        }
+        n_pieces = max(1, (block_tiles(qb) + a.split_tiles - 1) / a.split_tiles);
+        piece = i;
+    }
+
+    // ---- key range of the workgroup [wg_lo, kv_hi) in tiles; with a key split this
+    // workgroup takes tiles [t0, t1) of its query block
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, T_total);
+    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
+    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
+    int t0 = 0, t1 = n_tiles;
+    if (a.split_tiles > 0) {
+        t0 = piece * a.split_tiles;
+        t1 = min(t0 + a.split_tiles, n_tiles);
+    }
 
     // ---- this lane's query column (head hh, position offset pl) and 8-dim half h
     const int c = 32 * wave + n32;
@@ -295,78 +334,6 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     const bool col_ok = s_raw < a.S;
     const int s_idx = col_ok ? s_raw : a.S - 1;
     const int pos = a.start_pos + s_idx;
-
-    // ---- q prologue: lane (column, h) holds dims 16s + 8h + i (s < 16, i < 8), the B
-    // operand layout of the 32x32x16 MFMA. The arithmetic, including the order of the
-    // sum of squares, is that of prep_q_column (qprep_kernel), so both round q to the
-    // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
-    half8 qf[16];
-    {
-        // workgroup-uniform resources (a per-lane base would make the compiler loop over
-        // lanes); the row of this lane's column is in the offset
-        const rsrc_t rq = make_rsrc(a.q, (uint32_t)a.S * a.n_q_heads * HD * 4);
-        const rsrc_t rgn = make_rsrc(a.q_gain, a.q_gain ? HD * 4 : 0);
-        const rsrc_t rc = make_rsrc(a.rcos, a.rcos ? (uint32_t)a.S * HD * 2 : 0);
-        const rsrc_t rs = make_rsrc(a.rsin, a.rsin ? (uint32_t)a.S * HD * 2 : 0);
-        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 4, co = s_idx * HD * 2;
-        float x[16][8];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const float8v v = bload_f8(rq, qo + (16 * s + 8 * h) * 4);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[s][i] = v[i];
-        }
-        if (a.q_gain) {
-            float se = 0.0f, so = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    se = __builtin_fmaf(x[2 * s][i], x[2 * s][i], se);
-                    so = __builtin_fmaf(x[2 * s + 1][i], x[2 * s + 1][i], so);
-                }
-            const float ss = add32(se) + add32(so);
-            const float rsq = 1.0f / sqrtf(ss / (float)HD + a.eps);  // x * rs * w, as the reference kernels
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const float8v gv = bload_f8(rgn, (16 * s + 8 * h) * 4);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rsq * gv[i];
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            float8v cv = bload_f8(rc, co + (16 * s + 8 * h) * 4), sv = bload_f8(rs, co + (16 * s + 8 * h) * 4);
-            if (!a.rcos) {
-                cv = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-                sv = float8v{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x0 = x[s][i], x1 = x[s + 8][i];
-                x[s][i] = __builtin_fmaf(x0, cv[i], -(x1 * sv[i]));
-                x[s + 8][i] = __builtin_fmaf(x1, cv[i], x0 * sv[i]);
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < 16; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
-        // q is only ever an MFMA B operand, which may sit in AGPRs: that leaves the VGPRs to
-        // the O^T accumulators, the scores and the LDS operand batches
-#pragma unroll
-        for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
-    }
-
-    // ---- key ranges: workgroup [wg_lo, kv_hi), this wave [w_lo, wp1], this column [col_lo, pos]
-    const int p0 = a.start_pos + qb * BQ;
-    const int kv_hi = min(p0 + BQ, T_total);
-    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
-    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
-    const int wp0 = p0 + (32 * wave) / G;
-    const int wp1 = min(p0 + (32 * wave + 31) / G, T_total - 1);
-    const int w_lo = a.window > 0 ? max(0, wp0 + 1 - a.window) : 0;
-    const int col_lo = a.window > 0 ? pos + 1 - a.window : 0;
 
     // K/V of this kv head through buffer resources: rows >= kv_hi read as zeros
     const int rowg = a.n_kv_heads * HD * 2;  // global bytes per cache row
@@ -387,6 +354,95 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         }
     };
 
+
+    // ---- q prologue: lane (column, h) holds dims 16s + 8h + i (s < 16, i < 8), the B
+    // operand layout of the 32x32x16 MFMA. The arithmetic, including the order of the
+    // sum of squares, is that of prep_q_column (qprep_kernel), so both round q to the
+    // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
+    half8 qf[16];
+    if (a.q16) {  // q prepared by qprep_kernel for every piece of the call at once
+        const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
+        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 2;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qf[s] = bload_h8(rq, qo + (16 * s + 8 * h) * 2);
+        if (t0 < t1) issue(t0, t0 & 1);
+        if (!col_ok) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+    } else {
+        // workgroup-uniform resources (a per-lane base would make the compiler loop over
+        // lanes); the row of this lane's column is in the offset
+        const rsrc_t rq = make_rsrc(a.q, (uint32_t)a.S * a.n_q_heads * HD * 4);
+        const rsrc_t rgn = make_rsrc(a.q_gain, a.q_gain ? HD * 4 : 0);
+        const rsrc_t rc = make_rsrc(a.rcos, a.rcos ? (uint32_t)a.S * HD * 2 : 0);
+        const rsrc_t rs = make_rsrc(a.rsin, a.rsin ? (uint32_t)a.S * HD * 2 : 0);
+        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 4, co = s_idx * HD * 2;
+        // every operand load first (one memory round trip), then the arithmetic
+        float x[16][8];
+        float8v gv[16], cv[8], sv[8];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float8v v = bload_f8(rq, qo + (16 * s + 8 * h) * 4);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[s][i] = v[i];
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) gv[s] = bload_f8(rgn, (16 * s + 8 * h) * 4);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            cv[s] = bload_f8(rc, co + (16 * s + 8 * h) * 4);
+            sv[s] = bload_f8(rs, co + (16 * s + 8 * h) * 4);
+            if (!a.rcos) {
+                cv[s] = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+                sv[s] = float8v{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        // the first K/V tile is issued behind the q operands (loads complete in order), so
+        // it lands while q is prepared without delaying the q data
+        if (t0 < t1) issue(t0, t0 & 1);
+        if (a.q_gain) {
+            float se = 0.0f, so = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    se = __builtin_fmaf(x[2 * s][i], x[2 * s][i], se);
+                    so = __builtin_fmaf(x[2 * s + 1][i], x[2 * s + 1][i], so);
+                }
+            const float ss = add32(se) + add32(so);
+            const float rsq = 1.0f / sqrtf(ss / (float)HD + a.eps);  // x * rs * w, as the reference kernels
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rsq * gv[s][i];
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x0 = x[s][i], x1 = x[s + 8][i];
+                x[s][i] = __builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i]));
+                x[s + 8][i] = __builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]);
+            }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+        // q is only ever an MFMA B operand, which may sit in AGPRs: that leaves the VGPRs to
+        // the O^T accumulators, the scores and the LDS operand batches
+#pragma unroll
+        for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+    }
+
+    // ---- key ranges: this wave [w_lo, wp1], this column [col_lo, pos]
+    const int wp0 = p0 + (32 * wave) / G;
+    const int wp1 = min(p0 + (32 * wave + 31) / G, T_total - 1);
+    const int w_lo = a.window > 0 ? max(0, wp0 + 1 - a.window) : 0;
+    const int col_lo = a.window > 0 ? pos + 1 - a.window : 0;
+
     float16v oacc[8];  // O^T[32dt + 8(r/4) + 4h + r%4][column]
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) oacc[dt] = float16v{};
@@ -401,11 +457,10 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     const int vb0 = 8 * (m16 & 1);                   // byte within the chunk
     const int vsw = vswz(vr0);                        // rows 16u + vr0 (+8) share r % 4
 
-    if (n_tiles > 0) issue(0, 0);
-    for (int t = 0; t < n_tiles; ++t) {
+    for (int t = t0; t < t1; ++t) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile t is in LDS
         __syncthreads();                                    // all parts; tile t-1 fully consumed
-        if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
+        if (t + 1 < t1) issue(t + 1, (t + 1) & 1);
         const int kb = wg_lo + t * KT;
         if (kb > wp1 || kb + KT - 1 < w_lo) continue;  // no key of this tile for this wave
         const char* K = lds + (t & 1) * 2 * TILEB;
@@ -513,6 +568,21 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 
     // ---- epilogue: column sum over both halves, normalise, srq, store 4 dims at a time
     const float l_tot = add32(l_run);
+    if (n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
+        const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
+        const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        // one 512-byte run per store instruction: [wave][dt][j][lane] half4
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 4 * lane;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
+                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
+                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+        if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
+        return;
+    }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (col_ok) {
         OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD;
@@ -520,10 +590,74 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int d = 32 * dt + 8 * j + 4 * h;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) store_elem(orow + d + i, srq(oacc[dt][4 * j + i] * inv, a.out_q));
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(orow + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
             }
+    }
+}
+
+// Merge of the pieces of split query blocks (the decode merge identity per column): with
+// each piece holding o_p = O_p / l_p, out = sum_p o_p l_p 2^(m_p - M) / sum_p l_p 2^(m_p - M),
+// M = max_p m_p, then srq and the output type. One workgroup per (query block, 32-column
+// wave block, kv head), laid out like the partials: thread (k, lane) owns the lane's
+// 4-dim runs k, k+4, .. (k < 4) of all 32 dims tiles, so every load instruction reads a
+// contiguous 512-byte run. At most 8 pieces.
+template <typename OUTT>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+    constexpr int HD = 256, KT = 64, NCOL = 128, MAXP = 8;
+    const int qb = blockIdx.x, w = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, k0 = tid >> 6;
+    const int c = 32 * w + (lane & 31), h = lane >> 5;
+    const int G = a.n_q_heads / a.n_kv_heads, BQ = NCOL / G;
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, a.start_pos + a.S);
+    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
+    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
+    const int n_pieces = max(1, (n_tiles + a.split_tiles - 1) / a.split_tiles);
+    const int s_idx = qb * BQ + c / G;
+    if (n_pieces <= 1) return;
+    const size_t blk0 = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces;
+    // buffer ranges end at the block's last piece: the loads of absent pieces read zeros,
+    // so all of them issue at once with no branch
+    const rsrc_t rml = make_rsrc(a.part_ml + blk0 * NCOL, (uint32_t)n_pieces * NCOL * 8);
+    const rsrc_t ro = make_rsrc(a.part_o + blk0 * (NCOL * HD) + (size_t)w * (32 * HD), (uint32_t)n_pieces * NCOL * HD * 2);
+    float2 ml[MAXP];
+    half4 ov[MAXP][8];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) ml[p] = bload_f32x2(rml, (p * NCOL + c) * 8);
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)  // run k = k0 + 4i: dims tile k/4, 8-dim group k%4
+            ov[p][i] = __builtin_bit_cast(half4, bload_f32x2(ro, (p * NCOL * HD + (k0 + 4 * i) * 256 + 4 * lane) * 2));
+    float wt[MAXP];
+    float M = kNegInf;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+        if (p >= n_pieces) ml[p] = make_float2(kNegInf, 0.0f);
+        M = fmaxf(M, ml[p].x);
+    }
+    float L = 0.0f;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {  // a piece with no attended key weighs 0
+        wt[p] = ml[p].x == kNegInf ? 0.0f : ml[p].y * fexp2(ml[p].x - M);
+        L += wt[p];
+    }
+    float4v o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        o[i] = float4v{0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < MAXP; ++p) o[i] += __builtin_convertvector(ov[p][i], float4v) * wt[p];
+    }
+    if (s_idx >= a.S) return;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + c % G) * HD;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int k = k0 + 4 * i, d = 32 * (k >> 2) + 8 * (k & 3) + 4 * h;
+        store4(orow + d, srq4(o[i] * inv, a.out_q));
     }
 }
 
@@ -566,19 +700,68 @@ static prefill_fn pick_g(int G, bool kv32, bool out32, bool hilo) {
 
 using namespace g4a;
 
+// Key split for short prompts: when the query blocks alone give fewer than 2 workgroups
+// per CU, long causal rows are cut into pieces of split_tiles key tiles so that about one
+// piece per CU results (G4A_PREFILL_SPLIT_TILES: 0 automatic, -1 never, N tiles per piece).
+struct PrefillSplit {
+    int split_tiles, max_pieces, n_qblocks, total_pieces;
+    size_t o_bytes, ml_bytes, q16_bytes, total;
+};
+static bool use_w32(const g4a_cfg* cfg) {
+    return cfg->head_dim == 256 && !(cfg->flags & (G4A_KV_F32 | G4A_Q_HILO)) && getenv_flag("G4A_PREFILL_W16") == 0;
+}
+static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
+    PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0};
+    if (!use_w32(cfg) || S <= 0 || cfg->n_kv_heads == 0) return p;
+    const int G = (int)(cfg->n_q_heads / cfg->n_kv_heads);
+    if (G < 1 || 128 % G) return p;
+    const int BQ = 128 / G, KT = 64, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
+    p.n_qblocks = (S + BQ - 1) / BQ;
+    const int mode = getenv_flag("G4A_PREFILL_SPLIT_TILES");
+    if (mode < 0 || (mode == 0 && (long)p.n_qblocks * kvH >= 512)) return p;
+    long total = 0;
+    int max_tiles = 0;
+    for (int qb = 0; qb < p.n_qblocks; ++qb) {
+        const int p0 = start_pos + qb * BQ;
+        const int hi = p0 + BQ < start_pos + S ? p0 + BQ : start_pos + S;
+        const int lo = W > 0 && p0 + 1 - W > 0 ? p0 + 1 - W : 0;
+        const int nt = (hi - lo + KT - 1) / KT;
+        total += nt;
+        if (nt > max_tiles) max_tiles = nt;
+    }
+    total *= kvH;
+    int st = mode > 0 ? mode : (int)((total + 255) / 256);
+    if (st < 2) st = 2;
+    if (st < (max_tiles + 7) / 8) st = (max_tiles + 7) / 8;  // the merge takes <= 8 pieces
+    const int pieces = (max_tiles + st - 1) / st;
+    if (pieces <= 1) return p;
+    p.split_tiles = st;
+    p.max_pieces = pieces;
+    p.total_pieces = 0;
+    for (int qb = 0; qb < p.n_qblocks; ++qb) {
+        const int p0 = start_pos + qb * BQ;
+        const int hi = p0 + BQ < start_pos + S ? p0 + BQ : start_pos + S;
+        const int lo = W > 0 && p0 + 1 - W > 0 ? p0 + 1 - W : 0;
+        const int nt = (hi - lo + KT - 1) / KT;
+        p.total_pieces += nt > st ? (nt + st - 1) / st : 1;
+    }
+    const size_t slots = (size_t)kvH * p.n_qblocks * pieces * 128;
+    p.o_bytes = slots * 256 * sizeof(half_t);
+    p.ml_bytes = (slots * sizeof(float2) + 255) & ~(size_t)255;
+    p.q16_bytes = ((size_t)S * cfg->n_q_heads * 256 * sizeof(half_t) + 255) & ~(size_t)255;
+    p.total = p.o_bytes + p.ml_bytes + p.q16_bytes;
+    return p;
+}
+
 extern "C" size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos) {
-    (void)cfg;
-    (void)S;
-    (void)start_pos;
-    return 0;
+    if (!cfg) return 0;
+    return prefill_split(cfg, S, start_pos).total;
 }
 
 extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q,
                            const float* q_gain, const float* rope_cos, const float* rope_sin,
                            const void* k_cache, const void* v_cache, void* out, void* ws,
                            size_t ws_bytes, void* stream) {
-    (void)ws;
-    (void)ws_bytes;
     if (!check_cfg(cfg, true)) return G4A_EINVAL;
     if (S <= 0 || start_pos < 0) {
         set_error("S (%d) must be positive and start_pos (%d) non-negative", S, start_pos);
@@ -605,7 +788,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
     const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
     // hd 256 with f16 caches and f16 q: the 32-column kernel; other modes the 16-column one
-    const bool w32 = HD == 256 && !kv32 && !hilo && getenv_flag("G4A_PREFILL_W16") == 0;
+    const bool w32 = use_w32(cfg);
     prefill_fn fn = nullptr;
     if (w32) {
         switch (G) {
@@ -644,10 +827,38 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;
-    dim3 grid(a.n_qblocks, cfg->n_kv_heads);
+    // key split when a large enough workspace is given (without one the call runs unsplit)
+    const PrefillSplit sp = prefill_split(cfg, S, start_pos);
+    a.split_tiles = 0;
+    a.max_pieces = 1;
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
+    a.q16 = nullptr;
+    if (sp.split_tiles > 0 && ws && ws_bytes >= sp.total && (uintptr_t)ws % 256 == 0) {
+        a.split_tiles = sp.split_tiles;
+        a.max_pieces = sp.max_pieces;
+        a.part_o = (half_t*)ws;
+        a.part_ml = (float2*)((char*)ws + sp.o_bytes);
+        // the pieces of a query block share its q: prepare it once (qprep_b's kernel, whose
+        // f16 values are those of the fused prologue), then every piece loads f16 q
+        half_t* q16 = (half_t*)((char*)ws + sp.o_bytes + sp.ml_bytes);
+        const int rows = S * (int)cfg->n_q_heads;
+        hipLaunchKernelGGL(qprep_kernel<256>, dim3((rows + 63) / 64), dim3(256), 0, (hipStream_t)stream, q, q_gain,
+                           rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads, cfg->eps);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
+        a.q16 = q16;
+    }
+    dim3 grid(a.split_tiles > 0 ? sp.total_pieces : a.n_qblocks, cfg->n_kv_heads);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
+    if (a.split_tiles > 0) {
+        auto mf = out32 ? prefill_merge_kernel<float> : prefill_merge_kernel<half_t>;
+        hipLaunchKernelGGL(mf, dim3(a.n_qblocks, 4, cfg->n_kv_heads), dim3(256), 0, (hipStream_t)stream, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_error(e, "prefill merge launch");
+    }
     return G4A_OK;
 }
 

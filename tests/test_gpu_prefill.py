@@ -225,6 +225,25 @@ def test_f32_cache_and_mirror():
 
 
 @pytest.mark.parametrize("window", [0, 512])
+def test_key_split_matches_unsplit(window, monkeypatch):
+    """Short prompts split long causal rows over workgroups (partials merged by a second
+    kernel). The split result equals the unsplit one up to summation order, for several
+    piece sizes, and both meet the contract against the oracle."""
+    q, qg, k, v, cos, sin = config3_inputs(seed=7)
+    cfg = sa.AttnConfig(8, 2, 256, window)
+    kw = dict(q_gain=qg, rope_cos=cos, rope_sin=sin)
+    q16 = kernel_q16(q, cfg, qg, cos, sin).astype(np.float32)
+    ref = O.prefill_attention(q16, k, v, 0, 2, window=window)
+    outs = {}
+    for mode in ("-1", "0", "2", "5"):
+        monkeypatch.setenv("G4A_PREFILL_SPLIT_TILES", mode)
+        outs[mode] = run(q, k, v, 0, cfg, out_dtype=torch.float32, **kw)
+        contract_close(outs[mode], ref, f"split tiles {mode} W={window}")
+    for mode in ("0", "2", "5"):  # P is rounded to f16 against each piece's own running max
+        contract_close(outs[mode], outs["-1"], f"split tiles {mode} vs unsplit W={window}")
+
+
+@pytest.mark.parametrize("window", [0, 512])
 def test_config5_layer_s8192(window):
     """One layer of config 5's prefill: S = 8192."""
     S, nH, kvH, hd = 8192, 8, 2, 256
