@@ -466,21 +466,24 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         const char* K = lds + (t & 1) * 2 * TILEB;
         const char* V = K + TILEB;
 
-        // S^T = K . Q^T: two 32-key sub-tiles, 16 k-steps of 16 dims; the A operands of a
-        // sub-tile are read in one batch ahead of its MFMAs
-        float16v sacc[2];
+        // S^T = K . Q^T: two 32-key sub-tiles, 16 k-steps of 16 dims. The two accumulator
+        // chains alternate (a chain of dependent MFMAs issues at half rate), and the A
+        // operands are read in batches ahead of their MFMAs.
+        float16v sacc[2] = {float16v{}, float16v{}};
+        const char* krow0 = K + n32 * ROWB;
+        const char* krow1 = K + (32 + n32) * ROWB;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            sacc[kt] = float16v{};
-            const char* krow = K + (32 * kt + n32) * ROWB;
+        for (int s0 = 0; s0 < 16; s0 += 4) {
+            half8 kv0[4], kv1[4];
 #pragma unroll
-            for (int s0 = 0; s0 < 16; s0 += 8) {
-                half8 kv[8];
+            for (int s = 0; s < 4; ++s) {
+                kv0[s] = *reinterpret_cast<const half8*>(krow0 + 16 * ((2 * (s0 + s) + h) ^ n32));
+                kv1[s] = *reinterpret_cast<const half8*>(krow1 + 16 * ((2 * (s0 + s) + h) ^ n32));
+            }
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
-                    kv[s] = *reinterpret_cast<const half8*>(krow + 16 * ((2 * (s0 + s) + h) ^ n32));
-#pragma unroll
-                for (int s = 0; s < 8; ++s) sacc[kt] = mfma32(kv[s], qf[s0 + s], sacc[kt]);
+            for (int s = 0; s < 4; ++s) {
+                sacc[0] = mfma32(kv0[s], qf[s0 + s], sacc[0]);
+                sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
             }
         }
         // keep 4 LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
@@ -505,15 +508,12 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
                     sacc[kt][r] = (o <= rel_hi && o >= rel_lo) ? sacc[kt][r] : kNegInf;
                 }
         }
-        float mloc = kNegInf;
+        float mloc = kNegInf;  // max of the raw scores, scaled once (scale > 0)
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sacc[kt][r] *= a.scale_log2;
-                mloc = fmaxf(mloc, sacc[kt][r]);
-            }
-        mloc = max32(mloc);  // the column's other half sits in lane ^ 32
+            for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[kt][r]);
+        mloc = max32(mloc) * a.scale_log2;  // the column's other half sits in lane ^ 32
         // move the running max only when a score passes it by more than 2^8
         const bool bump = mloc > m_use + 8.0f;
         if (__any(bump)) {
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float pv = fexp2(sacc[u >> 1][8 * (u & 1) + i] - msub);
+                const float pv = fexp2(__builtin_fmaf(sacc[u >> 1][8 * (u & 1) + i], a.scale_log2, -msub));
                 ps += pv;
                 pb[u][i] = (half_t)pv;
             }
