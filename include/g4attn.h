@@ -143,6 +143,50 @@ int g4a_kv_write(const g4a_cfg* cfg, int S, int start_pos, const void* k, const 
                  float k_in_q, float v_in_q, const float* k_gain, const float* rope_cos,
                  const float* rope_sin, void* k_cache, void* v_cache, void* stream);
 
+/*
+ * ---- The q/k/v producer: projections with QAT weights --------------------------------
+ * Packed weights: row o of an [n_out][n_in] matrix is n_in*bits/32 uint32 words; value i
+ * of the row sits at bit 8*(i/(8/bits)) + bits*(i%(8/bits)) of the row's bytes (byte-major,
+ * low bits first) and stands for row_scale[o] * (q - 2^(bits-1)) (dq_f16,
+ * kernels_dsl.py:2101-2138; qkv_70 unpacks the 4-bit case the same way, :1421-1426).
+ */
+/*
+ * Dequantise to f16: out[o][i] = f16(w_scale[o] * (q - 2^(bits-1))), the product in f32.
+ * Replaces dq_f16 (kernels_dsl.py:2101-2138; PrefillGPU._dq, prefill_gpu.py:186-200, slots
+ * [bits, scale(+offset), dst, (n_in, n_out)]). bits 2, 4 or 8; n_in a multiple of 128/bits.
+ * Weights are static: run it once per layer at load, or per call as the reference does.
+ */
+int g4a_dequant(int bits, int n_in, int n_out, const uint32_t* w_bits, const float* w_scale,
+                void* out_f16, void* stream);
+/*
+ * Decode q/k/v projections of one token, 4-bit QAT rows. Replaces qkv_70
+ * (kernels_dsl.py:1384-1480, dispatched at runner.py:408-423 with slots [a, q_bits, k_bits,
+ * v_bits, scales, sum_a, out_q, out_k, out_v, (q_out, k_out, v_out)]):
+ *   out_q[o] = srq(scales[o] * (sum_i q[o][i] a[i] - 8 sum_a), q_out)            o < q_dim
+ *   out_k[o] = srq(scales[q_dim + o] * (... k rows ...), k_out)                   o < kv_dim
+ *   out_v[o] = srq(scales[q_dim + kv_dim + o] * (... v rows ...), v_out)
+ *   a f32 [hidden] (hidden a multiple of 32, <= 4096); sum_a f32 [1] = sum of a, as
+ *   rmssrq_69 leaves it; q_dim, kv_dim multiples of 8. kv_dim 0 = a KV-sharing layer:
+ *   q only, k/v pointers unused (runner.py:416-419).
+ */
+int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, const float* sum_a,
+                 const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
+                 const float* scales, float q_out, float k_out, float v_out, float* out_q,
+                 float* out_k, float* out_v, void* stream);
+/*
+ * Prefill projection out = A . W^T over M tokens. Replaces one srqh_b -> _gemm -> srq_b
+ * sequence of PrefillGPU._layer (prefill_gpu.py:327-342):
+ *   A      f32 [M][K], rounded to f16 as srqh_b does: f16(srq(a, a_in_q)), 0 = convert only
+ *          (kernels_dsl.py:233-242);
+ *   w_f16  f16 [N][K] (g4a_dequant's output, the GEMM's transposed right operand);
+ *   out    f16 [M][N] = f16(sum_k a16 w16) with f32 accumulation, gemm_tiled's result
+ *          (kernels_dsl.py:34-136; the k/v path); or, with out_f32 != 0, f32 [M][N] =
+ *          srq(f32(that f16), out_q) (srq_b, :246-255; the q path).
+ *   N a multiple of 128, K of 32.
+ */
+int g4a_proj_gemm(int M, int N, int K, const float* a, float a_in_q, const void* w_f16,
+                  void* out, int out_f32, float out_q, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,7 @@ EXPORTS = (
     "g4a_decode_ws_bytes", "g4a_decode",
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
+    "g4a_dequant", "g4a_qkv_gemv", "g4a_proj_gemm",
 )
 
 
@@ -84,6 +85,13 @@ def load() -> ctypes.CDLL:
     lib.g4a_kv_write.restype = ctypes.c_int
     lib.g4a_kv_write.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_float,
                                  ctypes.c_float, P, P, P, P, P, P]
+    i, f = ctypes.c_int, ctypes.c_float
+    lib.g4a_dequant.restype = ctypes.c_int
+    lib.g4a_dequant.argtypes = [i, i, i, P, P, P, P]
+    lib.g4a_qkv_gemv.restype = ctypes.c_int
+    lib.g4a_qkv_gemv.argtypes = [i, i, i, P, P, P, P, P, P, f, f, f, P, P, P, P]
+    lib.g4a_proj_gemm.restype = ctypes.c_int
+    lib.g4a_proj_gemm.argtypes = [i, i, i, P, f, P, P, i, f, P]
     _lib = lib
     return lib
 

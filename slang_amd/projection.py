@@ -1,0 +1,137 @@
+"""Host-side q/k/v producer over libg4attn: QAT-weight projections on torch tensors.
+
+Two layers, as in attention.py:
+  * ``dequant`` / ``qkv_gemv`` / ``proj`` / ``prefill_qkv`` -- the library operations
+    with explicit keyword arguments;
+  * ``dq_f16`` / ``qkv_70`` -- drop-ins for the reference dispatches of the same names,
+    with their binding slots in order (gemma4_150/kernels_dsl.py:1384-1480 and
+    :2101-2138; bound at runner.py:408-423 and prefill_gpu.py:186-200).
+
+Packed weights are int32 (or uint32) tensors holding the reference's uint32 words. Every
+call is asynchronous on torch's current stream; nothing is computed on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import check
+from .attention import _need, _ptr, _stream
+
+__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "prefill_qkv", "packed_bits"]
+
+_WORDS = (torch.int32, torch.uint32)
+
+
+def packed_bits(words: torch.Tensor, n_in: int, n_out: int) -> int:
+    """Bit width of a packed [n_out][n_in] matrix, read off the buffer size as
+    PrefillGPU._dq does (prefill_gpu.py:195-196): 2, 4 or 8."""
+    nbits = words.numel() * 32 // (n_in * n_out)
+    if nbits not in (2, 4, 8) or nbits * n_in * n_out != words.numel() * 32:
+        raise ValueError(f"odd width for a [{n_out}x{n_in}] matrix in {words.numel()} words")
+    return nbits
+
+
+def dequant(words, scale, n_in: int, n_out: int, out=None, bits: int | None = None):
+    """f16 [n_out][n_in] = f16(scale[o] * (q - 2^(bits-1))) (dq_f16)."""
+    _need(words, "words", _WORDS)
+    _need(scale, "scale", torch.float32)
+    bits = packed_bits(words, n_in, n_out) if bits is None else bits
+    if scale.numel() < n_out:
+        raise ValueError("scale needs n_out entries")
+    if out is None:
+        out = torch.empty(n_out, n_in, device=words.device, dtype=torch.float16)
+    _need(out, "out", torch.float16)
+    if out.numel() != n_out * n_in:
+        raise ValueError("out must hold n_out*n_in values")
+    check(_lib.load().g4a_dequant(bits, n_in, n_out, _ptr(words), _ptr(scale), _ptr(out), _stream()))
+    return out
+
+
+def dq_f16(bits, scale, out, p, scale_offset: int = 0):
+    """Drop-in for the dq_f16 dispatch: slots [bits, scale(+offset bytes), dst, (n_in, n_out)]
+    (PrefillGPU._dq, prefill_gpu.py:186-200)."""
+    n_in, n_out = int(p[0]), int(p[1])
+    if scale_offset % 4:
+        raise ValueError("scale offset must be a multiple of 4 bytes")
+    sc = scale.view(-1)[scale_offset // 4:]
+    return dequant(bits, sc, n_in, n_out, out=out)
+
+
+def qkv_gemv(a, sum_a, q_bits, scales, q_dim: int, kv_dim: int = 0, k_bits=None, v_bits=None,
+             q_out: float = 0.0, k_out: float = 0.0, v_out: float = 0.0,
+             out_q=None, out_k=None, out_v=None):
+    """Decode q/k/v of one token from 4-bit rows (qkv_70). kv_dim 0: q only (KV-sharing
+    layers). Returns (q, k, v); k and v are None when kv_dim is 0."""
+    hidden = a.numel()
+    _need(a, "a", torch.float32)
+    _need(sum_a, "sum_a", torch.float32)
+    _need(scales, "scales", torch.float32)
+    for t, nm, rows in ((q_bits, "q_bits", q_dim), (k_bits, "k_bits", kv_dim), (v_bits, "v_bits", kv_dim)):
+        if rows:
+            _need(t, nm, _WORDS)
+            if t.numel() * 8 != rows * hidden:
+                raise ValueError(f"{nm} must hold {rows} 4-bit rows of {hidden} values")
+    if scales.numel() < q_dim + 2 * kv_dim:
+        raise ValueError("scales needs q_dim + 2*kv_dim entries")
+    dev = a.device
+    out_q = torch.empty(q_dim, device=dev, dtype=torch.float32) if out_q is None else out_q
+    if kv_dim:
+        out_k = torch.empty(kv_dim, device=dev, dtype=torch.float32) if out_k is None else out_k
+        out_v = torch.empty(kv_dim, device=dev, dtype=torch.float32) if out_v is None else out_v
+    for t, nm, n in ((out_q, "out_q", q_dim), (out_k, "out_k", kv_dim), (out_v, "out_v", kv_dim)):
+        if n:
+            _need(t, nm, torch.float32)
+            if t.numel() < n:
+                raise ValueError(f"{nm} needs {n} entries")
+    check(_lib.load().g4a_qkv_gemv(hidden, q_dim, kv_dim, _ptr(a), _ptr(sum_a), _ptr(q_bits),
+                                   _ptr(k_bits if kv_dim else None), _ptr(v_bits if kv_dim else None),
+                                   _ptr(scales), q_out, k_out, v_out, _ptr(out_q),
+                                   _ptr(out_k if kv_dim else None), _ptr(out_v if kv_dim else None),
+                                   _stream()))
+    return (out_q, out_k, out_v) if kv_dim else (out_q, None, None)
+
+
+def qkv_70(a, q_bits, k_bits, v_bits, scales, sum_a, out_q, out_k, out_v, params, shared=False):
+    """Drop-in for the qkv_70 dispatch with its slots in order (runner.py:416-423):
+    [a, q_bits, k_bits, v_bits, scales, sum_a, out_q, out_k, out_v, (q_out, k_out, v_out, _)].
+    ``shared`` is the KV-sharing layer's q-only dispatch (runner.py:416-419)."""
+    q_dim = out_q.numel()
+    kv_dim = 0 if shared else out_k.numel()
+    qo, ko, vo = (float(x) for x in list(params)[:3])
+    qkv_gemv(a, sum_a, q_bits, scales, q_dim, kv_dim, k_bits=k_bits, v_bits=v_bits,
+             q_out=qo, k_out=ko, v_out=vo, out_q=out_q, out_k=out_k, out_v=out_v)
+
+
+def proj(a, w_f16, a_in_q: float = 0.0, out_f32: bool = False, out_q: float = 0.0, out=None):
+    """out = A . W^T for M tokens: f16(srq(a, a_in_q)) operands, f32 accumulation, f16
+    result (srqh_b -> gemm_tiled), or f32 srq(result, out_q) with out_f32 (-> srq_b).
+
+    a f32 [M][K]; w_f16 f16 [N][K]."""
+    _need(a, "a", torch.float32)
+    _need(w_f16, "w_f16", torch.float16)
+    M, K = a.shape
+    N = w_f16.shape[0]
+    if w_f16.shape[1] != K:
+        raise ValueError(f"w is [{N}][{w_f16.shape[1]}], a has K = {K}")
+    dt = torch.float32 if out_f32 else torch.float16
+    if out is None:
+        out = torch.empty(M, N, device=a.device, dtype=dt)
+    _need(out, "out", dt)
+    if out.numel() != M * N:
+        raise ValueError("out must hold M*N values")
+    check(_lib.load().g4a_proj_gemm(M, N, K, _ptr(a), a_in_q, _ptr(w_f16), _ptr(out),
+                                    1 if out_f32 else 0, out_q, _stream()))
+    return out
+
+
+def prefill_qkv(a, wq_f16, wk_f16=None, wv_f16=None, a_in_q: float = 0.0, q_out: float = 0.0):
+    """The q/k/v block of PrefillGPU._layer (prefill_gpu.py:327-342) over dequantised weights:
+    q = srq_b(gemm(srqh_b(a), wq)) f32 [S][q_dim]; kraw, vraw = gemm(...) f16 [S][kv_dim]
+    (None on KV-sharing layers), ready for kvnorm_b."""
+    q = proj(a, wq_f16, a_in_q, out_f32=True, out_q=q_out)
+    if wk_f16 is None:
+        return q, None, None
+    return q, proj(a, wk_f16, a_in_q), proj(a, wv_f16, a_in_q)

@@ -105,3 +105,28 @@ def test_host_mirror_raises_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.load()
+
+
+def test_projection_argument_errors(lib):
+    f = FAKE
+    # g4a_dequant(bits, n_in, n_out, w_bits, w_scale, out, stream)
+    assert lib.g4a_dequant(3, 256, 4, f, f, f, None) == -2            # width not supported
+    assert lib.g4a_dequant(4, 200, 4, f, f, f, None) == -1            # n_in not a multiple of 32
+    assert lib.g4a_dequant(4, 256, 4, None, f, f, None) == -1
+    assert lib.g4a_dequant(4, 256, 4, ctypes.c_void_p(0x10004), f, f, None) == -1  # misaligned
+    # g4a_qkv_gemv(hidden, q_dim, kv_dim, a, sum_a, qb, kb, vb, scales, qo, ko, vo, oq, ok, ov, stream)
+    g = lambda hidden=1536, qd=2048, kvd=512, kb=f, qo=0.0, **k: lib.g4a_qkv_gemv(
+        hidden, qd, kvd, f, f, f, kb, f, f, qo, 0.0, 0.0, f, f, f, None)
+    assert g(hidden=1530) == -1
+    assert g(hidden=8192) == -1
+    assert g(qd=2044) == -1
+    assert g(kvd=-8) == -1
+    assert g(kb=None) == -1                                           # k rows missing
+    assert g(qo=-1.0) == -1
+    # g4a_proj_gemm(M, N, K, a, a_in_q, w, out, out_f32, out_q, stream)
+    assert lib.g4a_proj_gemm(0, 128, 32, f, 0.0, f, f, 0, 0.0, None) == -1
+    assert lib.g4a_proj_gemm(16, 100, 32, f, 0.0, f, f, 0, 0.0, None) == -1   # N % 128
+    assert lib.g4a_proj_gemm(16, 128, 48, f, 0.0, f, f, 0, 0.0, None) == -1   # K % 32
+    assert lib.g4a_proj_gemm(16, 128, 32, None, 0.0, f, f, 0, 0.0, None) == -1
+    assert lib.g4a_proj_gemm(16, 128, 32, f, -0.5, f, f, 0, 0.0, None) == -1
+    assert b"a_in_q" in lib.g4a_last_error()

@@ -1,0 +1,180 @@
+"""GPU parity of the q/k/v producer (g4a_dequant, g4a_qkv_gemv, g4a_proj_gemm) against the
+projection oracle (oracle/projection.py), through the C ABI.
+
+* dequant: bit-exact (the same f32 product rounded to f16), all widths, including the
+  E2B q matrix [2048][1536];
+* decode GEMV: the reference test's geometries (qd, hd) = (2048, 256) and (4096, 512)
+  (tests/test_kernels_dsl_parity.py:658-700) plus BASELINE's kvH 2 shape (kv_dim 512),
+  the KV-sharing q-only form and a hidden width past 2048; within 2e-3 + 1e-2|ref|
+  unquantised, and on the srq grid within one step with srq scales;
+* prefill GEMM: every f16 result within 2e-3 + 1e-2|ref| of the correctly rounded product,
+  and within one f16 ulp of it wherever |ref| >= 0.25 (below that the f32 accumulation's
+  own error over K = 1536, up to ~2e-5, can exceed an f16 ulp); f32 srq results within one
+  grid step; at S = 1024 and ragged token counts.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.projection as P
+import slang_amd as sa
+from helpers import contract_close, f16_ulp_close, srq_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def words(rng, n):
+    return rng.integers(0, 2 ** 32, size=n, dtype=np.uint64).astype(np.uint32)
+
+
+def dev_words(w):
+    return t(w.view(np.int32))
+
+
+def gemm_f16_close(got, ref, what):
+    got = np.asarray(got, np.float16)
+    err = contract_close(got.astype(np.float32), ref.astype(np.float32), what)
+    big = np.abs(ref.astype(np.float32)) >= 0.25
+    f16_ulp_close(got[big], ref[big], what + " (|ref| >= 0.25)")
+    return err
+
+
+@pytest.mark.parametrize("bits,n_in,n_out", [(2, 256, 64), (4, 256, 64), (8, 256, 64),
+                                             (4, 1536, 2048), (2, 1536, 96)])
+def test_dequant_bit_exact(bits, n_in, n_out):
+    rng = np.random.default_rng(131 + bits)
+    w = words(rng, n_out * n_in * bits // 32)
+    sc = (rng.random(n_out).astype(np.float32) * 0.01 + 0.001)
+    print(f"dequant bits {bits} [{n_out}x{n_in}]", flush=True)
+    got = sa.dequant(dev_words(w), t(sc), n_in, n_out)
+    assert sa.packed_bits(dev_words(w), n_in, n_out) == bits
+    torch.cuda.synchronize()
+    ref = P.dequant_f16(w, sc, n_in, n_out, bits)
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_dq_f16_dropin_scale_offset():
+    """_dq passes the k/v scales as an offset into qkv_scales (prefill_gpu.py:330-333)."""
+    rng = np.random.default_rng(7)
+    w = words(rng, 64 * 256 // 8)
+    sc = rng.random(200).astype(np.float32) + 0.1
+    out = torch.empty(64, 256, device=DEV, dtype=torch.float16)
+    sa.dq_f16(dev_words(w), t(sc), out, (256, 64), scale_offset=128 * 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), P.dequant_f16(w, sc[128:], 256, 64, 4))
+
+
+def gemv_case(seed, hidden, qd, kvd):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal(hidden).astype(np.float32)
+    wpr = hidden // 8
+    qb, kb, vb = words(rng, qd * wpr), words(rng, kvd * wpr), words(rng, kvd * wpr)
+    sc = (rng.random(qd + 2 * kvd).astype(np.float32) * 0.01 + 0.001)
+    suma = np.array([a.sum(dtype=np.float64)], np.float32)
+    return a, suma, qb, kb, vb, sc
+
+
+@pytest.mark.parametrize("hidden,qd,kvd", [(1536, 2048, 256), (1536, 4096, 512), (1536, 2048, 512),
+                                           (2560, 512, 256), (64, 8, 8)])
+@pytest.mark.parametrize("scales", [(0.0, 0.0, 0.0), (0.03125, 0.0234375, 0.0156)])
+def test_qkv_gemv_matches_oracle(hidden, qd, kvd, scales):
+    a, suma, qb, kb, vb, sc = gemv_case(111, hidden, qd, kvd)
+    print(f"qkv_gemv hidden {hidden} q {qd} kv {kvd} scales {scales}", flush=True)
+    got = sa.qkv_gemv(t(a), t(suma), dev_words(qb), t(sc), qd, kvd, k_bits=dev_words(kb),
+                      v_bits=dev_words(vb), q_out=scales[0], k_out=scales[1], v_out=scales[2])
+    torch.cuda.synchronize()
+    raw = P.qkv_gemv(a, suma[0], qb, kb, vb, sc, qd, kvd)  # unquantised
+    for nm, g, r, s in zip("qkv", got, raw, scales):
+        g = g.cpu().numpy()
+        if s == 0.0:
+            contract_close(g, r, f"out_{nm}")
+        else:
+            srq_close(g, r, s, f"out_{nm}")
+        assert np.count_nonzero(g), f"out_{nm} empty"
+
+
+def test_qkv_70_dropin_and_shared_layer():
+    a, suma, qb, kb, vb, sc = gemv_case(5, 1536, 2048, 256)
+    oq = torch.full((2048,), 7.0, device=DEV)
+    ok = torch.full((256,), 7.0, device=DEV)
+    ov = torch.full((256,), 7.0, device=DEV)
+    sa.qkv_70(t(a), dev_words(qb), dev_words(kb), dev_words(vb), t(sc), t(suma), oq, ok, ov,
+              (0.0, 0.0, 0.0, 0.0))
+    torch.cuda.synchronize()
+    rq, rk, rv = P.qkv_gemv(a, suma[0], qb, kb, vb, sc, 2048, 256)
+    contract_close(oq.cpu().numpy(), rq, "q")
+    contract_close(ok.cpu().numpy(), rk, "k")
+    contract_close(ov.cpu().numpy(), rv, "v")
+    # KV-sharing layer: q only, the k/v outputs untouched
+    ok.fill_(7.0)
+    ov.fill_(7.0)
+    oq.zero_()
+    sa.qkv_70(t(a), dev_words(qb), dev_words(qb), dev_words(qb), t(sc), t(suma), oq, ok, ov,
+              (0.0, 0.0, 0.0, 0.0), shared=True)
+    torch.cuda.synchronize()
+    contract_close(oq.cpu().numpy(), rq, "q shared")
+    assert (ok.cpu().numpy() == 7.0).all() and (ov.cpu().numpy() == 7.0).all()
+
+
+def test_qkv_gemv_zero_point_and_one_hot():
+    """Closed forms on the GPU: all values at the zero point give 0; a one-hot input picks
+    out scale * (q - 8) of one column."""
+    hidden, qd = 1536, 64
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal(hidden).astype(np.float32)
+    zp = np.full(qd * hidden // 8, 0x88888888, np.uint32)
+    sc = np.ones(qd, np.float32)
+    q, _, _ = sa.qkv_gemv(t(a), t(np.array([a.sum(dtype=np.float64)], np.float32)), dev_words(zp), t(sc), qd)
+    torch.cuda.synchronize()
+    assert np.abs(q.cpu().numpy()).max() < 1e-3
+    vals = rng.integers(0, 16, size=(qd, hidden))
+    wb = P.pack_values(vals, 4).reshape(-1)
+    sc = rng.random(qd).astype(np.float32) + 0.5
+    for j in (0, 1, 31, 32, 1535):
+        e = np.zeros(hidden, np.float32)
+        e[j] = 1.0
+        q, _, _ = sa.qkv_gemv(t(e), t(np.ones(1, np.float32)), dev_words(wb), t(sc), qd)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(q.cpu().numpy(), sc * (vals[:, j] - 8), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 2048, 1536), (1024, 512, 1536), (200, 256, 1536),
+                                   (1, 128, 32), (129, 384, 96)])
+def test_proj_gemm_matches_oracle(M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    wb = words(rng, N * K // 8)
+    sc = (rng.random(N).astype(np.float32) * 0.01 + 0.02)
+    print(f"proj_gemm M {M} N {N} K {K}", flush=True)
+    w16 = sa.dequant(dev_words(wb), t(sc), K, N)
+    c16 = sa.proj(t(a), w16)
+    cq = sa.proj(t(a), w16, out_f32=True, out_q=0.03125)
+    torch.cuda.synchronize()
+    wref = P.dequant_f16(wb, sc, K, N, 4)
+    ref = P.proj_gemm(a, wref)
+    err = gemm_f16_close(c16.cpu().numpy(), ref, "f16 out")
+    print(f"max abs err {err:.2e}", flush=True)
+    srq_close(cq.cpu().numpy(), ref.astype(np.float32), 0.03125, "q path srq")
+
+
+def test_prefill_qkv_block():
+    """prefill_gpu.py:327-342 at BASELINE's shapes: q f32 srq'd, kraw/vraw f16, with an
+    srqh_b input scale."""
+    S, H, qd, kvd = 1024, 1536, 2048, 512
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((S, H)).astype(np.float32)
+    ws = [(words(rng, n * H // 8), (rng.random(n).astype(np.float32) * 0.01 + 0.02)) for n in (qd, kvd, kvd)]
+    w16 = [sa.dequant(dev_words(w), t(s), H, w.size * 8 // H) for w, s in ws]
+    q, k, v = sa.prefill_qkv(t(a), *w16, a_in_q=0.0625, q_out=0.03125)
+    torch.cuda.synchronize()
+    a_q = P.srq(a, 0.0625)
+    for got, (w, s), nm in ((k, ws[1], "k"), (v, ws[2], "v")):
+        ref = P.proj_gemm(a_q, P.dequant_f16(w, s, H, w.size * 8 // H, 4))
+        gemm_f16_close(got.cpu().numpy(), ref, nm)
+    refq = P.proj_gemm(a_q, P.dequant_f16(ws[0][0], ws[0][1], H, qd, 4))
+    srq_close(q.cpu().numpy(), refq.astype(np.float32), 0.03125, "q")
