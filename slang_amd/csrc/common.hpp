@@ -59,6 +59,17 @@ __device__ __forceinline__ float max32(float x) { const float2 p = pair32(x); re
 
 __device__ __forceinline__ float wave_sum(float x) { return add32(add16(row16_sum(x))); }
 
+// Inclusive prefix sum over the 64 lanes (Hillis-Steele, six lane shifts).
+__device__ __forceinline__ int wave_prefix_sum(int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
     x = fmaxf(x, dpp_ror<8>(x));
     x = fmaxf(x, dpp_ror<4>(x));

@@ -38,7 +38,7 @@ struct PrefillArgs {
     // key split of long causal rows (prefill_kernel_w32): split_tiles = 0 means none;
     // otherwise a workgroup covers at most split_tiles key tiles of its query block and
     // blocks with more tiles leave partials for prefill_merge_kernel
-    int split_tiles, max_pieces;
+    int split_tiles, max_pieces, pieces_per_head;
     const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
     half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
                       // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
                                                     float eps) {
     constexpr int KSTEPS = HD / 32;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + n;
+    const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 16 + n;
     const bool ok = row < rows;
     const int rr = ok ? row : rows - 1;
     const int s_idx = rr / n_q_heads;
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n32 = lane & 31, h = lane >> 5;
-    const int kh = blockIdx.y;
+    int kh = blockIdx.y;
     const int T_total = a.start_pos + a.S;
     // key tiles of query block b: [lo(b), hi(b)) in tiles of KT keys
     auto block_tiles = [&](int b) {
@@ -301,18 +301,37 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         return (hi - lo + KT - 1) / KT;
     };
     // ---- this workgroup's query block (longest causal rows first) and, with a key split,
-    // its piece: workgroup i walks the blocks from the longest, each holding
-    // ceil(tiles / split_tiles) pieces (a scalar loop over at most a few hundred blocks)
+    // its piece. The split grid is 1-D: the work list (kv head, block from the longest,
+    // piece) is cut into 8 contiguous runs, one per XCD (the dispatcher deals workgroup
+    // L to XCD L % 8), so the pieces of a block share one L2 for the block's q rows and
+    // each kv head's K/V is read by as few XCDs as the split allows: every kernel starts
+    // with cold L2s, and the first tiles of all workgroups arrive together. Within its
+    // kv head, piece i is found by counting through the blocks from the longest, each
+    // holding ceil(tiles / split_tiles) pieces: the lanes take 64 blocks at a time (one
+    // division each, in parallel) and a prefix sum over the wave finds the block holding
+    // piece i; a scalar loop over the blocks would cost microseconds of issue slots.
     int qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
     if (a.split_tiles > 0) {
-        int i = blockIdx.x;
-        for (qb = a.n_qblocks - 1; qb > 0; --qb) {
-            const int np = max(1, (block_tiles(qb) + a.split_tiles - 1) / a.split_tiles);
-            if (i < np) break;
-            i -= np;
+        const int N = gridDim.x, L = blockIdx.x, x = L % 8, slot = L / 8;
+        const int per = (N + 7) / 8, r = N - 8 * (per - 1);  // XCDs x < r take per workgroups, the rest per - 1
+        const int v = x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
+        kh = v / a.pieces_per_head;
+        const int i = v - kh * a.pieces_per_head;
+        int base = 0;  // pieces of the blocks before this group of 64
+        for (int k0 = 0; k0 < a.n_qblocks; k0 += 64) {
+            const int b = a.n_qblocks - 1 - (k0 + lane);
+            const int np = b >= 0 ? max(1, (block_tiles(b) + a.split_tiles - 1) / a.split_tiles) : 0;
+            const int incl = wave_prefix_sum(np);
+            const unsigned long long past = __ballot(base + incl > i);  // lanes whose range ends past piece i
+            if (past) {
+                const int L = __builtin_ctzll(past);
+                qb = a.n_qblocks - 1 - (k0 + L);
+                n_pieces = __builtin_amdgcn_readlane(np, L);
+                piece = i - (base + __builtin_amdgcn_readlane(incl, L) - n_pieces);
+                break;
+            }
+            base += __builtin_amdgcn_readlane(incl, 63);
         }
-        n_pieces = max(1, (block_tiles(qb) + a.split_tiles - 1) / a.split_tiles);
-        piece = i;
     }
 
     // ---- key range of the workgroup [wg_lo, kv_hi) in tiles; with a key split this
@@ -361,11 +380,27 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
     half8 qf[16];
     if (a.q16) {  // q prepared by qprep_kernel for every piece of the call at once
+        // Wave w DMAs the f16 q rows of its own 32 columns (two 512-byte rows per
+        // instruction, chunk n32 of a row from logical chunk n32 ^ (row % 32)) into the LDS
+        // stage that tile t0 + 1 takes over later, then reads them back in the B-operand
+        // layout. Whole rows keep every global access a full 1 KiB run.
         const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
-        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 2;
+        char* qs = lds + ((t0 + 1) & 1) * 2 * TILEB;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) qf[s] = bload_h8(rq, qo + (16 * s + 8 * h) * 2);
+        for (int j = 0; j < 16; ++j) {
+            const int r = 32 * wave + 2 * j + h;  // column of the row this lane moves
+            const int qo = ((qb * BQ + r / G) * a.n_q_heads + kh * G + r % G) * ROWB + 16 * (n32 ^ (r & 31));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(qs + (32 * wave + 2 * j) * ROWB),
+                                                     16, qo, 0, 0, 0);
+        }
         if (t0 < t1) issue(t0, t0 & 1);
+        // the 16 q DMAs were issued before tile t0's 16: they are done at vmcnt <= 16
+        if (t0 < t1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const char* qrow = qs + c * ROWB;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage free for tile t0 + 1's DMA
         if (!col_ok) {
 #pragma unroll
             for (int s = 0; s < 16; ++s) qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -831,25 +866,27 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     const PrefillSplit sp = prefill_split(cfg, S, start_pos);
     a.split_tiles = 0;
     a.max_pieces = 1;
+    a.pieces_per_head = 0;
     a.part_o = nullptr;
     a.part_ml = nullptr;
     a.q16 = nullptr;
     if (sp.split_tiles > 0 && ws && ws_bytes >= sp.total && (uintptr_t)ws % 256 == 0) {
         a.split_tiles = sp.split_tiles;
         a.max_pieces = sp.max_pieces;
+        a.pieces_per_head = sp.total_pieces;
         a.part_o = (half_t*)ws;
         a.part_ml = (float2*)((char*)ws + sp.o_bytes);
         // the pieces of a query block share its q: prepare it once (qprep_b's kernel, whose
         // f16 values are those of the fused prologue), then every piece loads f16 q
         half_t* q16 = (half_t*)((char*)ws + sp.o_bytes + sp.ml_bytes);
         const int rows = S * (int)cfg->n_q_heads;
-        hipLaunchKernelGGL(qprep_kernel<256>, dim3((rows + 63) / 64), dim3(256), 0, (hipStream_t)stream, q, q_gain,
+        hipLaunchKernelGGL(qprep_kernel<256>, dim3((rows + 15) / 16), dim3(64), 0, (hipStream_t)stream, q, q_gain,
                            rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads, cfg->eps);
         hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
         a.q16 = q16;
     }
-    dim3 grid(a.split_tiles > 0 ? sp.total_pieces : a.n_qblocks, cfg->n_kv_heads);
+    const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads) : dim3(a.n_qblocks, cfg->n_kv_heads);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
@@ -888,9 +925,10 @@ extern "C" int g4a_qprep(const g4a_cfg* cfg, int S, const float* q, const float*
         set_error("S*n_q_heads too large");
         return G4A_EINVAL;
     }
-    const int blocks = (int)((rows + 63) / 64);
+    // one wave (16 rows) per workgroup spreads even short prompts over every CU
+    const int blocks = (int)((rows + 15) / 16);
     auto fn = HD == 256 ? qprep_kernel<256> : qprep_kernel<512>;
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, (hipStream_t)stream, q, q_gain, rope_cos, rope_sin,
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64), 0, (hipStream_t)stream, q, q_gain, rope_cos, rope_sin,
                        (half_t*)q16, (int)rows, (int)cfg->n_q_heads, cfg->eps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "qprep launch");
