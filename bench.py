@@ -9,7 +9,9 @@ replays a HIP graph of K calls that rotate over 64 distinct KV caches (512 MiB, 
 than the 256 MiB Infinity Cache), so every call streams its cache from HBM.
 `secondary` carries the other BASELINE rows: config 2 sliding (W 512), config 3
 prefill (S 1024, global and W 512, TFLOP/s of 4*hd*nH*attended-pairs), config 4
-(16 sequences, KV ~ U[1024, 32768]). Times come from HIP events on the stream the
+(16 sequences, KV ~ U[1024, 32768]), the q/k/v producer in front of the path (decode
+4-bit GEMV at the config-2 layer shape, prefill projection GEMMs at config 3) and the
+config-5 35-layer stack. Times come from HIP events on the stream the
 kernels run on. `cpu_baseline` is the numpy oracle on this host for the headline
 workload (a bounded sample).
 """
@@ -187,7 +189,7 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
     # per-layer-type figures: one layer of each kind (the same calls, graphs of their own)
     per = {}
     for kind, li in (("global", 4), ("sliding", 0)):
-        pm = graph_time_ms([lambda li=li: prefill_layer(li)], 4, 1)
+        pm = graph_time_ms([lambda li=li: prefill_layer(li)], 16, 2)
         dm = graph_time_ms([lambda li=li: [decode_layer(li, t) for t in range(steps)]], 1, 0) / steps
         pairs = sum(min(p + 1, win[kind]) if win[kind] else p + 1 for p in range(S))
         dbytes = sum(2 * (min(S + t + 1, win[kind]) if win[kind] else S + t + 1) * KVH * HD * 2
@@ -201,6 +203,46 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
             "decode_ms_per_step_35_layers": round(dec_ms / steps, 4),
             "per_layer": per,
             "note": "prefill per layer = kv_write(S) + prefill; decode per layer-step = kv_write(1) + decode"}
+
+
+def qkv_gemv_case(sa, steps, warmup, gen, n_sets=128):
+    """Decode q/k/v projections of one token (qkv_70) at the config-2 layer shape: H 1536,
+    q 8x256, k/v 2x256 rows of 4-bit weights; n_sets distinct weight sets (302 MB, more
+    than the 256 MB Infinity Cache) rotate so every call streams its weights from HBM."""
+    H, qd, kvd = 1536, NH * HD, KVH * HD
+    words = lambda rows: torch.randint(-2**31, 2**31 - 1, (rows * H // 8,), device="cuda",  # noqa: E731
+                                       dtype=torch.int32, generator=gen)
+    sets = [(words(qd), words(kvd), words(kvd)) for _ in range(n_sets)]
+    sc = 0.01 * torch.rand(qd + 2 * kvd, device="cuda", generator=gen)
+    a = torch.randn(H, device="cuda", generator=gen)
+    sa_ = a.sum().reshape(1)
+    oq = torch.empty(qd, device="cuda")
+    ok = torch.empty(kvd, device="cuda")
+    ov = torch.empty(kvd, device="cuda")
+    fns = [lambda w=w: sa.qkv_gemv(a, sa_, w[0], sc, qd, kvd, k_bits=w[1], v_bits=w[2], q_out=0.02,
+                                   k_out=0.02, v_out=0.02, out_q=oq, out_k=ok, out_v=ov) for w in sets]
+    ms = graph_time_ms(fns, steps, warmup)
+    return ms, (qd + 2 * kvd) * H // 2
+
+
+def proj_case(sa, steps, warmup, gen, S=1024):
+    """Prefill q/k/v projections at config 3 (S 1024 tokens, H 1536 -> q 2048, k 512, v 512)
+    on dequantised f16 weights: srqh_b of the input, then the three GEMMs of one layer."""
+    H = 1536
+    a = torch.randn(S, H, device="cuda", generator=gen)
+    wq = (0.02 * torch.randn(NH * HD, H, device="cuda", generator=gen)).half()
+    wk = (0.02 * torch.randn(KVH * HD, H, device="cuda", generator=gen)).half()
+    wv = (0.02 * torch.randn(KVH * HD, H, device="cuda", generator=gen)).half()
+    a16 = torch.empty(S, H, device="cuda", dtype=torch.float16)
+    oq = torch.empty(S, NH * HD, device="cuda")
+    ok = torch.empty(S, KVH * HD, device="cuda", dtype=torch.float16)
+    ov = torch.empty_like(ok)
+
+    def fn():  # prefill_qkv: srqh_b once, then the three GEMMs in one launch
+        sa.srqh(a, 0.05, out=a16)
+        sa.gemm16(a16, [(wq, oq, 0.02), (wk, ok, None), (wv, ov, None)])
+    ms = graph_time_ms([fn], steps, warmup)
+    return ms, 2 * S * H * (NH * HD + 2 * KVH * HD)
 
 
 def copy_calibration(steps):
@@ -326,6 +368,15 @@ def main():
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
                            "hbm_frac": round(nb4 / ms4 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb4,
                            "sum_kv_len": toks}
+        msg, nbg = qkv_gemv_case(sa, args.steps, args.warmup, gen)
+        sec["qkv_gemv_2"] = {"us_per_call": round(msg * 1e3, 3), "GB/s": round(nbg / msg / 1e6, 2),
+                             "hbm_frac": round(nbg / msg / 1e6 / HBM_PEAK_GBS, 4), "weight_bytes": nbg,
+                             "note": "decode q/k/v projections (qkv_70), 4-bit weights, 128 rotated sets"}
+        msp, flp = proj_case(sa, max(8, args.steps // 8), args.warmup, gen)
+        tfp = flp / (msp * 1e-3) / 1e12
+        sec["proj_3"] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(tfp, 2),
+                         "mfma_frac": round(tfp / F16_PEAK_TFLOPS, 4), "flops": flp,
+                         "note": "prefill q/k/v projection GEMMs of one layer at S 1024, f16 weights"}
         if not args.no_stack:
             sec["stack_5"] = stack_case(sa, gen)
         rec["secondary"] = sec

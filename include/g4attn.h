@@ -174,18 +174,29 @@ int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, const float*
                  const float* scales, float q_out, float k_out, float v_out, float* out_q,
                  float* out_k, float* out_v, void* stream);
 /*
- * Prefill projection out = A . W^T over M tokens. Replaces one srqh_b -> _gemm -> srq_b
- * sequence of PrefillGPU._layer (prefill_gpu.py:327-342):
- *   A      f32 [M][K], rounded to f16 as srqh_b does: f16(srq(a, a_in_q)), 0 = convert only
- *          (kernels_dsl.py:233-242);
- *   w_f16  f16 [N][K] (g4a_dequant's output, the GEMM's transposed right operand);
- *   out    f16 [M][N] = f16(sum_k a16 w16) with f32 accumulation, gemm_tiled's result
- *          (kernels_dsl.py:34-136; the k/v path); or, with out_f32 != 0, f32 [M][N] =
- *          srq(f32(that f16), out_q) (srq_b, :246-255; the q path).
- *   N a multiple of 128, K of 32.
+ * srqh_b (kernels_dsl.py:232-242; prefill_gpu.py:286-288, :327-334): out_f16[i] =
+ * f16(srq(a[i], a_in_q)), 0 = convert only. n a multiple of 8. The activation operand of
+ * g4a_gemm16, made once and shared by the q, k and v products of a layer.
  */
-int g4a_proj_gemm(int M, int N, int K, const float* a, float a_in_q, const void* w_f16,
-                  void* out, int out_f32, float out_q, void* stream);
+int g4a_srqh(int n, const float* a, float a_in_q, void* out_f16, void* stream);
+
+/* One product of g4a_gemm16: out = A . w^T, w f16 [n][K] (g4a_dequant's output); out f16
+ * [M][n] = f16(f32-accumulated sum) as gemm_tiled writes it (kernels_dsl.py:34-136), or
+ * with out_f32 != 0 f32 [M][n] = srq(f32(that f16), out_q), srq_b's q path (:246-255). */
+typedef struct {
+    const void* w_f16;
+    void* out;
+    int n;        /* rows of w = output columns, a multiple of 128 */
+    int out_f32;
+    float out_q;
+} g4a_gemm_mat;
+
+/*
+ * Up to three GEMMs sharing the f16 activation A [M][K] in one launch: the q, k and v
+ * projection GEMMs of PrefillGPU._layer (prefill_gpu.py:327-342, each a _gemm on srqh_b's
+ * output) as one dispatch. K a multiple of 64.
+ */
+int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream);
 
 #ifdef __cplusplus
 }

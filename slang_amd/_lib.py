@@ -25,7 +25,7 @@ EXPORTS = (
     "g4a_decode_ws_bytes", "g4a_decode",
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
-    "g4a_dequant", "g4a_qkv_gemv", "g4a_proj_gemm",
+    "g4a_dequant", "g4a_qkv_gemv", "g4a_srqh", "g4a_gemm16",
 )
 
 
@@ -38,6 +38,17 @@ class G4ACfg(ctypes.Structure):
         ("flags", ctypes.c_uint32),
         ("scale", ctypes.c_float),
         ("eps", ctypes.c_float),
+        ("out_q", ctypes.c_float),
+    ]
+
+
+class G4AGemmMat(ctypes.Structure):
+    """struct g4a_gemm_mat: one product of g4a_gemm16."""
+    _fields_ = [
+        ("w_f16", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("n", ctypes.c_int),
+        ("out_f32", ctypes.c_int),
         ("out_q", ctypes.c_float),
     ]
 
@@ -90,8 +101,10 @@ def load() -> ctypes.CDLL:
     lib.g4a_dequant.argtypes = [i, i, i, P, P, P, P]
     lib.g4a_qkv_gemv.restype = ctypes.c_int
     lib.g4a_qkv_gemv.argtypes = [i, i, i, P, P, P, P, P, P, f, f, f, P, P, P, P]
-    lib.g4a_proj_gemm.restype = ctypes.c_int
-    lib.g4a_proj_gemm.argtypes = [i, i, i, P, f, P, P, i, f, P]
+    lib.g4a_srqh.restype = ctypes.c_int
+    lib.g4a_srqh.argtypes = [i, P, f, P, P]
+    lib.g4a_gemm16.restype = ctypes.c_int
+    lib.g4a_gemm16.argtypes = [i, i, P, i, ctypes.POINTER(G4AGemmMat), P]
     _lib = lib
     return lib
 

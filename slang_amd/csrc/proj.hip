@@ -17,9 +17,9 @@
 //  * Prefill is MFMA work. Weights are static, and 288 GB of HBM holds every layer's f16
 //    weights many times over, so dequantisation is its own pass (g4a_dequant, run at load
 //    or per call as the reference does) rather than VALU work repeated inside every GEMM
-//    tile. The GEMM is a K-major ("TN") f16 MFMA GEMM, 32x32x16 tiles, computed transposed
-//    (D^T = W . A^T) so each lane holds 4 consecutive output columns of one token and stores
-//    them in one instruction; srqh_b is fused into the A staging and srq_b into the store.
+//    tile. srqh_b runs once per layer input (g4a_srqh); the q, k and v GEMMs then share
+//    that f16 activation in one grouped launch (g4a_gemm16): K-major ("TN") f16 MFMA tiles
+//    fed by a four-stage LDS pipeline, srq_b fused into the q path's store.
 #include <stdio.h>
 
 #include "common.hpp"
@@ -130,88 +130,114 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
     }
 }
 
-// ---------------------------------------------------------------- prefill projection GEMM
-struct GemmArgs {
-    const float* a;   // [M][K] f32
-    const half_t* w;  // [N][K] f16
-    void* out;        // [M][N] f16, or f32 with out_f32
-    int M, N, K;
-    float a_in_q, out_q;
+// ---------------------------------------------------------------- f16 GEMM (gemm_tiled)
+// srqh_b (kernels_dsl.py:232-242): out = f16(srq(a, s)), 8 values per thread.
+__global__ __launch_bounds__(256) void srqh_kernel(const float* __restrict__ a, float s, half_t* __restrict__ out,
+                                                   int n8) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const float4v x0 = reinterpret_cast<const float4v*>(a)[2 * i];
+    const float4v x1 = reinterpret_cast<const float4v*>(a)[2 * i + 1];
+    half8 h;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h[j] = (half_t)srq(x0[j], s);
+        h[4 + j] = (half_t)srq(x1[j], s);
+    }
+    reinterpret_cast<half8*>(out)[i] = h;
+}
+
+// Grouped f16 GEMM: up to three products out_p = A . W_p^T sharing A (the q, k and v
+// projections of one layer in one launch). Tiles of 128 tokens x 128 outputs, 64-deep k
+// stages DMA'd straight from HBM into LDS (buffer_load ... lds, 1 KiB per wave
+// instruction), four stages in flight so the loads of three stages hide the memory
+// latency behind the MFMAs of the fourth. LDS rows are 128 B (64 halves, 8 chunks of
+// 16 B); chunk c of row r sits at c ^ ((r >> 1) & 7), so the 16 rows of a quarter-wave
+// operand read fall in 16 distinct bank groups. Each wave owns 64 x 64 of the tile as 2x2
+// v_mfma_f32_32x32x16_f16 blocks computed transposed (D^T = W . A^T) so a lane holds 4
+// consecutive outputs of one token and stores them in one instruction.
+struct Gemm16Args {
+    const half_t* a;  // [M][K] f16
+    int M, K, mtiles, n_mats;
+    const half_t* w[3];  // [N_p][K] f16
+    void* out[3];        // [M][N_p] f16, or f32 (srq'd with out_q) when out_f32
+    int n[3], out_f32[3];
+    float out_q[3];
+    int tile_end[3];  // cumulative tiles (n_p / 128) * mtiles
 };
 
-// LDS tile rows are 32 halves (64 B, 4 chunks of 16 B); chunk c of row r sits at position
-// c ^ ((r >> 2) & 3), so the 16 rows one 16-lane quarter of a b128 operand read touches,
-// and the 8 rows x 2 chunks of a staging store, fall in 16 distinct bank groups.
-__device__ __forceinline__ int gswz(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+__device__ __forceinline__ int g16swz(int r) { return (r >> 1) & 7; }
 
-template <bool OUT_F32>
-__global__ __launch_bounds__(256) void proj_gemm_kernel(GemmArgs g) {
-    constexpr int BM = 128, BN = 128, BK = 32, TILE = 128 * 64;  // bytes per LDS operand tile
-    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILE];  // [buffer][W, A]
+__global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
+    constexpr int BM = 128, BN = 128, BK = 64, ROWB = BK * 2, OPB = 128 * ROWB;  // operand tile bytes
+    constexpr int STAGES = 4, STAGEB = 2 * OPB;
+    __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGEB];  // [stage]{W, A}
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int l32 = lane & 31, h = lane >> 5;
 
-    // staging: thread t moves 16 k-values of row t/2 (k half t%2) of both operands
-    const int sr = tid >> 1, skh = tid & 1;
-    const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * g.K * 4);  // rows >= M read as zeros
-    const rsrc_t rw = make_rsrc(g.w, (uint32_t)g.N * g.K * 2);
-    const int a_off = (m0 + sr) * g.K * 4 + 64 * skh;
-    const int w_off = (n0 + sr) * g.K * 2 + 32 * skh;
-    float4v ast[4];
-    u32x4 wst[2];
-    auto stage_load = [&](int k0) {
+    // ---- this workgroup's matrix and tile: tiles of one matrix run m-tile-major, so
+    // neighbouring workgroups share the rows of W they stream
+    int p = 0, t = blockIdx.x;
+    if (t >= g.tile_end[0]) p = t >= g.tile_end[1] ? 2 : 1;
+    if (p > 0) t -= g.tile_end[p - 1];
+    const int ntiles = g.n[p] / BN;
+    const int n0 = (t % ntiles) * BN, m0 = (t / ntiles) * BM;
+    const int K = g.K, nk = K / BK;
+
+    const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * K * 2);  // token rows >= M read as zeros
+    const rsrc_t rw = make_rsrc(g.w[p], (uint32_t)g.n[p] * K * 2);
+    // wave w moves rows 32w .. 32w+31 of both operands, 8 rows (1 KiB) per instruction
+    auto issue = [&](int kt) {
+        char* st = lds + (kt % STAGES) * STAGEB;
+        const int kb = kt * BK * 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ast[i] = bload_f32x4(ra, a_off + 4 * k0 + 16 * i);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) wst[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off + 2 * k0 + 16 * i, 0, 0);
-    };
-    auto stage_store = [&](int buf) {
-        char* wl = lds + buf * 2 * TILE;
-        char* al = wl + TILE;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            half8 hv;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {  // srqh_b: f16(srq(a, a_in_q))
-                hv[j] = (half_t)srq(ast[2 * i][j], g.a_in_q);
-                hv[4 + j] = (half_t)srq(ast[2 * i + 1][j], g.a_in_q);
-            }
-            *reinterpret_cast<half8*>(al + gswz(sr, 2 * skh + i)) = hv;
-            *reinterpret_cast<u32x4*>(wl + gswz(sr, 2 * skh + i)) = wst[i];
+        for (int i = 0; i < 4; ++i) {
+            const int r = 32 * wave + 8 * i + (lane >> 3);
+            const int c = (lane & 7) ^ g16swz(r);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (32 * wave + 8 * i) * ROWB),
+                                                     16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPB + (32 * wave + 8 * i) * ROWB),
+                                                     16, (m0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
     };
 
     float16v acc[2][2] = {{float16v{}, float16v{}}, {float16v{}, float16v{}}};
-    const int nk = g.K / BK;
-    stage_load(0);
-    stage_store(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        if (kt + 1 < nk) stage_load((kt + 1) * BK);
-        const char* wl = lds + (kt & 1) * 2 * TILE;
-        const char* al = wl + TILE;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {  // 16-value k-steps: lane (l32, h) holds k 8h .. 8h+7
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+        // stage kt has landed once at most the 8 instructions of each later stage remain
+        const int later = min(STAGES - 2, nk - 1 - kt);
+        if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave's part of stage kt; stage kt - 1 fully consumed
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+        const char* wl = lds + (kt % STAGES) * STAGEB;
+        const char* al = wl + OPB;
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {  // lane (l32, h) holds k 16s + 8h .. +7
             half8 wo[2], ao[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                wo[b] = *reinterpret_cast<const half8*>(wl + gswz(64 * wn + 32 * b + l32, 2 * s + h));
-                ao[b] = *reinterpret_cast<const half8*>(al + gswz(64 * wm + 32 * b + l32, 2 * s + h));
+                const int rw_ = 64 * wn + 32 * b + l32, ra_ = 64 * wm + 32 * b + l32;
+                wo[b] = *reinterpret_cast<const half8*>(wl + rw_ * ROWB + 16 * ((2 * s + h) ^ g16swz(rw_)));
+                ao[b] = *reinterpret_cast<const half8*>(al + ra_ * ROWB + 16 * ((2 * s + h) ^ g16swz(ra_)));
             }
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = proj_mfma32(wo[nb], ao[mb], acc[nb][mb]);
         }
-        if (kt + 1 < nk) stage_store((kt + 1) & 1);
-        __syncthreads();
     }
 
-    // D^T[n][m]: acc[r] is column n = 8(r/4) + 4h + r%4, token m = l32 of the 32x32 block;
-    // the GEMM result rounds to f16 (gemm_tiled), the q path then applies srq_b
+    // D^T[n][m]: acc[r] is output n = 8(r/4) + 4h + r%4, token m = l32 of the 32x32 block;
+    // the product rounds to f16 (gemm_tiled), the q path then applies srq_b
+    const int N = g.n[p];
+    const bool f32 = g.out_f32[p] != 0;
+    const float oq = g.out_q[p];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
         const int m = m0 + 64 * wm + 32 * mb + l32;
@@ -224,10 +250,10 @@ __global__ __launch_bounds__(256) void proj_gemm_kernel(GemmArgs g) {
                 float4v v;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = (float)(half_t)acc[nb][mb][4 * q + i];
-                if (OUT_F32)
-                    store4(reinterpret_cast<float*>(g.out) + (size_t)m * g.N + n, srq4(v, g.out_q));
+                if (f32)
+                    store4(reinterpret_cast<float*>(g.out[p]) + (size_t)m * N + n, srq4(v, oq));
                 else
-                    store4(reinterpret_cast<half_t*>(g.out) + (size_t)m * g.N + n, v);
+                    store4(reinterpret_cast<half_t*>(g.out[p]) + (size_t)m * N + n, v);
             }
     }
 }
@@ -235,6 +261,71 @@ __global__ __launch_bounds__(256) void proj_gemm_kernel(GemmArgs g) {
 }  // namespace g4a
 
 using namespace g4a;
+
+extern "C" int g4a_srqh(int n, const float* a, float a_in_q, void* out_f16, void* stream) {
+    if (n <= 0 || n % 8) {
+        set_error("n (%d) must be a positive multiple of 8", n);
+        return G4A_EINVAL;
+    }
+    if (!a || !out_f16 || (((uintptr_t)a | (uintptr_t)out_f16) & 15)) {
+        set_error("a and out must be non-NULL and 16-byte aligned");
+        return G4A_EINVAL;
+    }
+    if (!(a_in_q >= 0.0f)) {
+        set_error("a_in_q must be >= 0");
+        return G4A_EINVAL;
+    }
+    const int n8 = n / 8;
+    hipLaunchKernelGGL(srqh_kernel, dim3((n8 + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, a_in_q,
+                       reinterpret_cast<half_t*>(out_f16), n8);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "srqh launch");
+    return G4A_OK;
+}
+
+extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream) {
+    if (M <= 0 || K <= 0 || K % 64) {
+        set_error("M (%d) must be positive and K (%d) a positive multiple of 64", M, K);
+        return G4A_EINVAL;
+    }
+    if (n_mats < 1 || n_mats > 3 || !mats) {
+        set_error("n_mats (%d) must be 1, 2 or 3 with a matrix table", n_mats);
+        return G4A_EINVAL;
+    }
+    if (!a_f16 || ((uintptr_t)a_f16 & 15) || (int64_t)(M + 127) * K * 2 > 0x7fffffff) {
+        set_error("a must be non-NULL, 16-byte aligned and within 32-bit buffer offsets");
+        return G4A_EINVAL;
+    }
+    Gemm16Args g;
+    g.a = reinterpret_cast<const half_t*>(a_f16);
+    g.M = M;
+    g.K = K;
+    g.mtiles = (M + 127) / 128;
+    g.n_mats = n_mats;
+    int tiles = 0;
+    for (int i = 0; i < 3; ++i) {
+        const g4a_gemm_mat* m = i < n_mats ? &mats[i] : nullptr;
+        if (m) {
+            if (m->n <= 0 || m->n % 128 || !m->w_f16 || !m->out || (((uintptr_t)m->w_f16 | (uintptr_t)m->out) & 15) ||
+                (int64_t)m->n * K * 2 > 0x7fffffff || (int64_t)M * m->n > 0x7fffffff || !(m->out_q >= 0.0f)) {
+                set_error("matrix %d: n (%d) a positive multiple of 128, w/out non-NULL and 16-byte aligned, "
+                          "within 32-bit offsets, out_q >= 0", i, m->n);
+                return G4A_EINVAL;
+            }
+            tiles += (m->n / 128) * g.mtiles;
+        }
+        g.w[i] = m ? reinterpret_cast<const half_t*>(m->w_f16) : nullptr;
+        g.out[i] = m ? m->out : nullptr;
+        g.n[i] = m ? m->n : 128;
+        g.out_f32[i] = m ? m->out_f32 : 0;
+        g.out_q[i] = m ? m->out_q : 0.0f;
+        g.tile_end[i] = tiles;
+    }
+    hipLaunchKernelGGL(gemm16_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "gemm16 launch");
+    return G4A_OK;
+}
 
 extern "C" int g4a_dequant(int bits, int n_in, int n_out, const uint32_t* w_bits, const float* w_scale,
                            void* out_f16, void* stream) {
@@ -319,47 +410,5 @@ extern "C" int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, c
         hipLaunchKernelGGL((qkv_gemv_kernel<2, 2>), grid, dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "qkv_gemv launch");
-    return G4A_OK;
-}
-
-extern "C" int g4a_proj_gemm(int M, int N, int K, const float* a, float a_in_q, const void* w_f16,
-                             void* out, int out_f32, float out_q, void* stream) {
-    if (M <= 0 || N <= 0 || K <= 0 || N % 128 || K % 32) {
-        set_error("M (%d) must be positive, N (%d) a multiple of 128 and K (%d) of 32", M, N, K);
-        return G4A_EINVAL;
-    }
-    if ((int64_t)(M + 127) * K * 4 > 0x7fffffff || (int64_t)N * K * 2 > 0x7fffffff ||
-        (int64_t)M * N > 0x7fffffff) {
-        set_error("operands beyond 32-bit buffer offsets");
-        return G4A_EINVAL;
-    }
-    if (!a || !w_f16 || !out) {
-        set_error("a, w and out must be non-NULL");
-        return G4A_EINVAL;
-    }
-    if (((uintptr_t)a | (uintptr_t)w_f16 | (uintptr_t)out) & 15) {
-        set_error("a, w and out must be 16-byte aligned");
-        return G4A_EINVAL;
-    }
-    if (!(a_in_q >= 0.0f) || !(out_q >= 0.0f)) {
-        set_error("a_in_q/out_q must be >= 0");
-        return G4A_EINVAL;
-    }
-    GemmArgs g;
-    g.a = a;
-    g.w = reinterpret_cast<const half_t*>(w_f16);
-    g.out = out;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.a_in_q = a_in_q;
-    g.out_q = out_q;
-    const dim3 grid(N / 128, (M + 127) / 128);
-    if (out_f32)
-        hipLaunchKernelGGL(proj_gemm_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, g);
-    else
-        hipLaunchKernelGGL(proj_gemm_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, g);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_error(e, "proj_gemm launch");
     return G4A_OK;
 }

@@ -1,7 +1,7 @@
 """Host-side q/k/v producer over libg4attn: QAT-weight projections on torch tensors.
 
 Two layers, as in attention.py:
-  * ``dequant`` / ``qkv_gemv`` / ``proj`` / ``prefill_qkv`` -- the library operations
+  * ``dequant`` / ``qkv_gemv`` / ``srqh`` / ``gemm16`` / ``proj`` / ``prefill_qkv`` -- the library operations
     with explicit keyword arguments;
   * ``dq_f16`` / ``qkv_70`` -- drop-ins for the reference dispatches of the same names,
     with their binding slots in order (gemma4_150/kernels_dsl.py:1384-1480 and
@@ -20,7 +20,7 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 
-__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "prefill_qkv", "packed_bits"]
+__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "prefill_qkv", "packed_bits"]
 
 _WORDS = (torch.int32, torch.uint32)
 
@@ -120,18 +120,57 @@ def proj(a, w_f16, a_in_q: float = 0.0, out_f32: bool = False, out_q: float = 0.
     if out is None:
         out = torch.empty(M, N, device=a.device, dtype=dt)
     _need(out, "out", dt)
-    if out.numel() != M * N:
-        raise ValueError("out must hold M*N values")
-    check(_lib.load().g4a_proj_gemm(M, N, K, _ptr(a), a_in_q, _ptr(w_f16), _ptr(out),
-                                    1 if out_f32 else 0, out_q, _stream()))
+    gemm16(srqh(a, a_in_q), [(w_f16, out, out_q if out_f32 else None)])
     return out
+
+
+def srqh(a, a_in_q: float = 0.0, out=None):
+    """srqh_b (kernels_dsl.py:232-242): f16(srq(a, a_in_q)), 0 = convert only."""
+    _need(a, "a", torch.float32)
+    if out is None:
+        out = torch.empty(a.shape, device=a.device, dtype=torch.float16)
+    _need(out, "out", torch.float16)
+    if out.numel() != a.numel():
+        raise ValueError("out must hold as many values as a")
+    check(_lib.load().g4a_srqh(a.numel(), _ptr(a), a_in_q, _ptr(out), _stream()))
+    return out
+
+
+def gemm16(a16, mats):
+    """Up to three products sharing the f16 activation a16 [M][K], one launch (g4a_gemm16).
+
+    mats: sequence of (w_f16 [N][K], out, out_q or None); out f16 [M][N] gets the f16 GEMM
+    result (gemm_tiled), out f32 [M][N] gets srq(f32(f16 result), out_q) (srq_b)."""
+    _need(a16, "a16", torch.float16)
+    M, K = a16.shape
+    if not 1 <= len(mats) <= 3:
+        raise ValueError("gemm16 takes 1 to 3 matrices")
+    tab = (_lib.G4AGemmMat * len(mats))()
+    for i, (w, out, oq) in enumerate(mats):
+        _need(w, "w_f16", torch.float16)
+        _need(out, "out", (torch.float16, torch.float32))
+        if w.dim() != 2 or w.shape[1] != K:
+            raise ValueError(f"w is {tuple(w.shape)}, a16 has K = {K}")
+        if out.numel() != M * w.shape[0]:
+            raise ValueError("out must hold M*N values")
+        tab[i] = _lib.G4AGemmMat(w.data_ptr(), out.data_ptr(), w.shape[0], int(out.dtype == torch.float32),
+                                 float(oq or 0.0))
+    check(_lib.load().g4a_gemm16(M, K, _ptr(a16), len(mats), tab, _stream()))
 
 
 def prefill_qkv(a, wq_f16, wk_f16=None, wv_f16=None, a_in_q: float = 0.0, q_out: float = 0.0):
     """The q/k/v block of PrefillGPU._layer (prefill_gpu.py:327-342) over dequantised weights:
     q = srq_b(gemm(srqh_b(a), wq)) f32 [S][q_dim]; kraw, vraw = gemm(...) f16 [S][kv_dim]
-    (None on KV-sharing layers), ready for kvnorm_b."""
-    q = proj(a, wq_f16, a_in_q, out_f32=True, out_q=q_out)
+    (None on KV-sharing layers), ready for kvnorm_b. srqh_b runs once for the three GEMMs,
+    which run as one launch."""
+    S = a.shape[0]
+    a16 = srqh(a, a_in_q)
+    q = torch.empty(S, wq_f16.shape[0], device=a.device, dtype=torch.float32)
+    mats = [(wq_f16, q, q_out)]
     if wk_f16 is None:
+        gemm16(a16, mats)
         return q, None, None
-    return q, proj(a, wk_f16, a_in_q), proj(a, wv_f16, a_in_q)
+    k = torch.empty(S, wk_f16.shape[0], device=a.device, dtype=torch.float16)
+    v = torch.empty(S, wv_f16.shape[0], device=a.device, dtype=torch.float16)
+    gemm16(a16, mats + [(wk_f16, k, None), (wv_f16, v, None)])
+    return q, k, v

@@ -123,10 +123,26 @@ def test_projection_argument_errors(lib):
     assert g(kvd=-8) == -1
     assert g(kb=None) == -1                                           # k rows missing
     assert g(qo=-1.0) == -1
-    # g4a_proj_gemm(M, N, K, a, a_in_q, w, out, out_f32, out_q, stream)
-    assert lib.g4a_proj_gemm(0, 128, 32, f, 0.0, f, f, 0, 0.0, None) == -1
-    assert lib.g4a_proj_gemm(16, 100, 32, f, 0.0, f, f, 0, 0.0, None) == -1   # N % 128
-    assert lib.g4a_proj_gemm(16, 128, 48, f, 0.0, f, f, 0, 0.0, None) == -1   # K % 32
-    assert lib.g4a_proj_gemm(16, 128, 32, None, 0.0, f, f, 0, 0.0, None) == -1
-    assert lib.g4a_proj_gemm(16, 128, 32, f, -0.5, f, f, 0, 0.0, None) == -1
-    assert b"a_in_q" in lib.g4a_last_error()
+    # g4a_srqh(n, a, a_in_q, out, stream)
+    assert lib.g4a_srqh(12, f, 0.0, f, None) == -1                     # n % 8
+    assert lib.g4a_srqh(16, None, 0.0, f, None) == -1
+    assert lib.g4a_srqh(16, f, -1.0, f, None) == -1
+    # g4a_gemm16(M, K, a16, n_mats, mats, stream)
+    mat = lambda n=128, w=f, out=f, oq=0.0: _lib.G4AGemmMat(w.value if w else None, out.value, n, 0, oq)  # noqa: E731
+    tab = lambda *ms: (_lib.G4AGemmMat * len(ms))(*ms)  # noqa: E731
+    assert lib.g4a_gemm16(16, 96, f, 1, tab(mat()), None) == -1        # K % 64
+    assert lib.g4a_gemm16(0, 128, f, 1, tab(mat()), None) == -1
+    assert lib.g4a_gemm16(16, 128, f, 0, tab(mat()), None) == -1       # no matrix
+    assert lib.g4a_gemm16(16, 128, f, 4, tab(mat(), mat(), mat(), mat()), None) == -1
+    assert lib.g4a_gemm16(16, 128, None, 1, tab(mat()), None) == -1
+    assert lib.g4a_gemm16(16, 128, f, 2, tab(mat(), mat(n=100)), None) == -1   # n % 128
+    assert lib.g4a_gemm16(16, 128, f, 1, tab(mat(w=None)), None) == -1
+    assert lib.g4a_gemm16(16, 128, f, 1, tab(mat(oq=-1.0)), None) == -1
+    assert b"matrix 0" in lib.g4a_last_error()
+
+
+def test_gemm_mat_struct_layout():
+    """struct g4a_gemm_mat: two pointers, two ints, a float (8-byte aligned, 32 bytes)."""
+    assert [f[0] for f in _lib.G4AGemmMat._fields_] == ["w_f16", "out", "n", "out_f32", "out_q"]
+    assert _lib.G4AGemmMat.n.offset == 16 and _lib.G4AGemmMat.out_q.offset == 24
+    assert ctypes.sizeof(_lib.G4AGemmMat) == 32

@@ -1,4 +1,4 @@
-"""GPU parity of the q/k/v producer (g4a_dequant, g4a_qkv_gemv, g4a_proj_gemm) against the
+"""GPU parity of the q/k/v producer (g4a_dequant, g4a_qkv_gemv, g4a_srqh, g4a_gemm16) against the
 projection oracle (oracle/projection.py), through the C ABI.
 
 * dequant: bit-exact (the same f32 product rounded to f16), all widths, including the
@@ -144,7 +144,7 @@ def test_qkv_gemv_zero_point_and_one_hot():
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 2048, 1536), (1024, 512, 1536), (200, 256, 1536),
-                                   (1, 128, 32), (129, 384, 96)])
+                                   (1, 128, 64), (129, 384, 192)])
 def test_proj_gemm_matches_oracle(M, N, K):
     rng = np.random.default_rng(M + N + K)
     a = rng.standard_normal((M, K)).astype(np.float32)
@@ -160,6 +160,33 @@ def test_proj_gemm_matches_oracle(M, N, K):
     err = gemm_f16_close(c16.cpu().numpy(), ref, "f16 out")
     print(f"max abs err {err:.2e}", flush=True)
     srq_close(cq.cpu().numpy(), ref.astype(np.float32), 0.03125, "q path srq")
+
+
+@pytest.mark.parametrize("M,K,ns", [(1024, 1536, (2048, 512, 512)), (200, 1536, (256,)),
+                                    (1, 64, (128, 128)), (129, 192, (384, 128, 256))])
+def test_gemm16_grouped_matches_oracle(M, K, ns):
+    """g4a_gemm16: up to three products over one f16 A in one launch, each f16 (gemm_tiled)
+    or f32 srq'd (srq_b); ragged M (rows past M read as zeros, nothing stored past M)."""
+    rng = np.random.default_rng(M + K + len(ns))
+    print(f"gemm16 M {M} K {K} n {ns}", flush=True)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    a16 = sa.srqh(t(a), 0.0625)
+    ws = [(words(rng, n * K // 8), (rng.random(n).astype(np.float32) * 0.01 + 0.02)) for n in ns]
+    w16 = [sa.dequant(dev_words(w), t(s), K, n) for (w, s), n in zip(ws, ns)]
+    outs = [torch.full((M + 3, n), 7.0, device=DEV, dtype=torch.float32 if i == 0 else torch.float16)
+            for i, n in enumerate(ns)]
+    sa.gemm16(a16, [(w, o[:M], 0.03125 if i == 0 else None) for i, (w, o) in enumerate(zip(w16, outs))])
+    torch.cuda.synchronize()
+    a_q = P.srq(a, 0.0625)
+    np.testing.assert_array_equal(a16.cpu().numpy(), a_q.astype(np.float16))  # srqh_b exactly
+    for i, ((w, s), n, o) in enumerate(zip(ws, ns, outs)):
+        ref = P.proj_gemm(a_q, P.dequant_f16(w, s, K, n, 4))
+        got = o[:M].float().cpu().numpy()
+        if i == 0:
+            srq_close(got, ref.astype(np.float32), 0.03125, f"matrix {i} (q path)")
+        else:
+            gemm_f16_close(got, ref, f"matrix {i}")
+        assert (o[M:] == 7.0).all(), "stores past M"
 
 
 def test_prefill_qkv_block():
