@@ -415,29 +415,78 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         const rsrc_t rc = make_rsrc(a.rcos, a.rcos ? (uint32_t)a.S * HD * 2 : 0);
         const rsrc_t rs = make_rsrc(a.rsin, a.rsin ? (uint32_t)a.S * HD * 2 : 0);
         const int qo = (s_idx * a.n_q_heads + kh * G + hh) * HD * 4, co = s_idx * HD * 2;
-        // every operand load first (one memory round trip), then the arithmetic
+        // The operands every column shares -- the gain, and the RoPE rows of the block's
+        // BQ positions when they fit (G >= 4) -- are DMA'd once into LDS stage 1, which the
+        // second K/V tile takes over after the loop's first barrier; each lane then reads
+        // its slices from LDS. Fetched per lane from memory they would cost 64 KiB of load
+        // traffic and 256 registers per wave. Layout: [gain 1 KiB][cos BQ x 512 B][sin ...].
+        constexpr bool ROPE_LDS = BQ <= 32;
+        char* shr = lds + ((t0 + 1) & 1) * 2 * TILEB;
+        if (wave == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rgn, (__attribute__((address_space(3))) void*)shr, 16, 16 * lane, 0, 0, 0);
+        if constexpr (ROPE_LDS) {
+            // BQ rows of 512 B per table from token row qb * BQ: 1 KiB per wave instruction
+            constexpr int PER_WAVE = (BQ / 2 + 3) / 4;
+#pragma unroll
+            for (int j = 0; j < PER_WAVE; ++j) {
+                const int ins = 4 * j + wave;  // the table's ins-th KiB
+                if (ins < BQ / 2) {
+                    const int go = (qb * BQ * 512) + 1024 * ins + 16 * lane;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rc, (__attribute__((address_space(3))) void*)(shr + 1024 + 1024 * ins), 16, go, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rs, (__attribute__((address_space(3))) void*)(shr + 1024 + BQ * 512 + 1024 * ins), 16, go, 0, 0, 0);
+                }
+            }
+        }
+        // every remaining operand load first (one memory round trip), then the arithmetic
         float x[16][8];
-        float8v gv[16], cv[8], sv[8];
+        float8v cv[8], sv[8];
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const float8v v = bload_f8(rq, qo + (16 * s + 8 * h) * 4);
 #pragma unroll
             for (int i = 0; i < 8; ++i) x[s][i] = v[i];
         }
+        if constexpr (!ROPE_LDS) {
 #pragma unroll
-        for (int s = 0; s < 16; ++s) gv[s] = bload_f8(rgn, (16 * s + 8 * h) * 4);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            cv[s] = bload_f8(rc, co + (16 * s + 8 * h) * 4);
-            sv[s] = bload_f8(rs, co + (16 * s + 8 * h) * 4);
-            if (!a.rcos) {
-                cv[s] = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-                sv[s] = float8v{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < 8; ++s) {
+                cv[s] = bload_f8(rc, co + (16 * s + 8 * h) * 4);
+                sv[s] = bload_f8(rs, co + (16 * s + 8 * h) * 4);
             }
         }
         // the first K/V tile is issued behind the q operands (loads complete in order), so
         // it lands while q is prepared without delaying the q data
         if (t0 < t1) issue(t0, t0 & 1);
+        if (t0 < t1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // all but tile t0's 16
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave's share of the LDS operands
+        const float* gl = reinterpret_cast<const float*>(shr) + 8 * h;
+        auto gain8 = [&](int s) {
+            const float4v g0 = *reinterpret_cast<const float4v*>(gl + 16 * s);
+            const float4v g1 = *reinterpret_cast<const float4v*>(gl + 16 * s + 4);
+            return float8v{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+        };
+        if constexpr (ROPE_LDS) {
+            const float* cl = reinterpret_cast<const float*>(shr + 1024) + pl * 128 + 8 * h;
+            const float* sl = cl + BQ * 128;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const float4v c0 = *reinterpret_cast<const float4v*>(cl + 16 * s);
+                const float4v c1 = *reinterpret_cast<const float4v*>(cl + 16 * s + 4);
+                const float4v s0 = *reinterpret_cast<const float4v*>(sl + 16 * s);
+                const float4v s1 = *reinterpret_cast<const float4v*>(sl + 16 * s + 4);
+                cv[s] = float8v{c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+                sv[s] = float8v{s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+            }
+        }
+        if (!a.rcos) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                cv[s] = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+                sv[s] = float8v{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            }
+        }
         if (a.q_gain) {
             float se = 0.0f, so = 0.0f;
 #pragma unroll
@@ -450,9 +499,11 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
             const float ss = add32(se) + add32(so);
             const float rsq = 1.0f / sqrtf(ss / (float)HD + a.eps);  // x * rs * w, as the reference kernels
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
+            for (int s = 0; s < 16; ++s) {
+                const float8v gv = gain8(s);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rsq * gv[s][i];
+                for (int i = 0; i < 8; ++i) x[s][i] = x[s][i] * rsq * gv[i];
+            }
         }
 #pragma unroll
         for (int s = 0; s < 8; ++s)

@@ -21,6 +21,7 @@
 //    that f16 activation in one grouped launch (g4a_gemm16): K-major ("TN") f16 MFMA tiles
 //    fed by a four-stage LDS pipeline, srq_b fused into the q path's store.
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "common.hpp"
 
@@ -166,11 +167,17 @@ struct Gemm16Args {
     int tile_end[3];  // cumulative tiles (n_p / 128) * mtiles
 };
 
-__device__ __forceinline__ int g16swz(int r) { return (r >> 1) & 7; }
-
+template <int BK>
 __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
-    constexpr int BM = 128, BN = 128, BK = 64, ROWB = BK * 2, OPB = 128 * ROWB;  // operand tile bytes
+    constexpr int BM = 128, BN = 128, ROWB = BK * 2, OPB = 128 * ROWB;  // operand tile bytes
     constexpr int STAGES = 4, STAGEB = 2 * OPB;
+    constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;           // rows per 1 KiB wave instruction
+    constexpr int IPO = 32 / RPI;           // instructions per operand and wave per stage
+    constexpr int IPS = 2 * IPO;            // ... per stage (W and A)
+    // chunk c of row r sits at c ^ swz(r): the rows sharing a 256-byte bank window get
+    // distinct chunks, so a quarter-wave operand read touches 16 distinct bank groups
+    auto swz = [](int r) { return (r / (256 / ROWB)) % CPR; };
     __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGEB];  // [stage]{W, A}
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -188,17 +195,17 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
 
     const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * K * 2);  // token rows >= M read as zeros
     const rsrc_t rw = make_rsrc(g.w[p], (uint32_t)g.n[p] * K * 2);
-    // wave w moves rows 32w .. 32w+31 of both operands, 8 rows (1 KiB) per instruction
+    // wave w moves rows 32w .. 32w+31 of both operands, RPI rows (1 KiB) per instruction
     auto issue = [&](int kt) {
         char* st = lds + (kt % STAGES) * STAGEB;
         const int kb = kt * BK * 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 32 * wave + 8 * i + (lane >> 3);
-            const int c = (lane & 7) ^ g16swz(r);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (32 * wave + 8 * i) * ROWB),
+        for (int i = 0; i < IPO; ++i) {
+            const int r = 32 * wave + RPI * i + lane / CPR;
+            const int c = (lane % CPR) ^ swz(r);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (32 * wave + RPI * i) * ROWB),
                                                      16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPB + (32 * wave + 8 * i) * ROWB),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPB + (32 * wave + RPI * i) * ROWB),
                                                      16, (m0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
     };
@@ -208,28 +215,34 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < nk) issue(s);
     for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed once at most the 8 instructions of each later stage remain
+        // stage kt has landed once at most the IPS instructions of each later stage remain
         const int later = min(STAGES - 2, nk - 1 - kt);
-        if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        if (later >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPS) : "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // every wave's part of stage kt; stage kt - 1 fully consumed
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
         const char* wl = lds + (kt % STAGES) * STAGEB;
         const char* al = wl + OPB;
-#pragma unroll
-        for (int s = 0; s < BK / 16; ++s) {  // lane (l32, h) holds k 16s + 8h .. +7
-            half8 wo[2], ao[2];
+        // lane (l32, h) holds k 16s + 8h .. +7 of k-step s; the operands of step s + 1 are
+        // read while the MFMAs of step s run (one wave per SIMD hides no LDS latency itself)
+        half8 wo[2][2], ao[2][2];
+        auto rd = [&](int s, half8 (&w)[2], half8 (&x)[2]) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const int rw_ = 64 * wn + 32 * b + l32, ra_ = 64 * wm + 32 * b + l32;
-                wo[b] = *reinterpret_cast<const half8*>(wl + rw_ * ROWB + 16 * ((2 * s + h) ^ g16swz(rw_)));
-                ao[b] = *reinterpret_cast<const half8*>(al + ra_ * ROWB + 16 * ((2 * s + h) ^ g16swz(ra_)));
+                w[b] = *reinterpret_cast<const half8*>(wl + rw_ * ROWB + 16 * ((2 * s + h) ^ swz(rw_)));
+                x[b] = *reinterpret_cast<const half8*>(al + ra_ * ROWB + 16 * ((2 * s + h) ^ swz(ra_)));
             }
+        };
+        rd(0, wo[0], ao[0]);
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            if (s + 1 < BK / 16) rd(s + 1, wo[(s + 1) & 1], ao[(s + 1) & 1]);
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = proj_mfma32(wo[nb], ao[mb], acc[nb][mb]);
+                for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = proj_mfma32(wo[s & 1][nb], ao[s & 1][mb], acc[nb][mb]);
         }
     }
 
@@ -321,7 +334,11 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
         g.out_q[i] = m ? m->out_q : 0.0f;
         g.tile_end[i] = tiles;
     }
-    hipLaunchKernelGGL(gemm16_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    const char* bkv = getenv("G4A_GEMM_BK");
+    if (bkv && atoi(bkv) == 32)
+        hipLaunchKernelGGL(gemm16_kernel<32>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    else
+        hipLaunchKernelGGL(gemm16_kernel<64>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "gemm16 launch");
     return G4A_OK;
