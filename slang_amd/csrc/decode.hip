@@ -9,6 +9,8 @@
 // MI355X design (not the reference's):
 //  * One workgroup per (key split, kv head, sequence) carries ALL G query heads of its
 //    GQA group, so each K/V row leaves HBM once. The 4 waves take 16-key blocks in turn.
+//    A batch of several sequences runs as one work list of equal-length splits over all
+//    of them (see list_chunk), so ragged lengths do not leave long splits running alone.
 //  * Both products on the matrix cores, transposed so that no data moves between them:
 //    S^T = K . Q^T (v_mfma_f32_16x16x32_f16; A = 16 keys straight from HBM, B = the query
 //    rows, f16 high parts in rows 0..G-1 and low parts in rows G..2G-1, so high + low
@@ -22,7 +24,8 @@
 //    registers and V sits in LDS, the next block's loads reuse both register sets.
 //  * Rows past the split end are clamped to the last valid row (loaded, then masked),
 //    so every load is unconditional.
-//  * Waves merge through LDS. Splits merge in a second, wide kernel (decode_merge_kernel):
+//  * Waves merge through LDS. Splits merge in a second, wide kernel (decode_merge_kernel,
+//    decode_merge_list_kernel for a work list):
 //    the kernel boundary publishes the partials, so no workgroup pays a cache-writeback
 //    fence or a ticket round trip, and the merge of one (sequence, kv head) is spread over
 //    HD/16 workgroups whose threads load all of their splits in one batch. (A last-arriver
@@ -47,10 +50,13 @@ struct DecodeArgs {
     const void* vc;
     int64_t seq_stride;
     float* out;
-    float2* part_ml;    // [pairs][max_splits][G] (m, l)
-    float* part_o;      // [pairs][max_splits][G][HD]
+    float2* part_ml;    // [slots][G] (m, l); slot = pair * max_splits + split, or the unit
+    float* part_o;      // [slots][G][HD]
     int n_q_heads, n_kv_heads, window, max_splits, chunk;
     float scale_log2, eps, out_q;
+    // work list (several sequences): list_target > 0 spreads all active keys over about
+    // list_target units of equal length (>= chunk keys, <= chunk_cap), one workgroup each
+    int n_seq, list_target, chunk_cap, list_units;  // list_units: the grid, units past it never run
 };
 
 template <int HD, int G>
@@ -145,6 +151,76 @@ __device__ __forceinline__ SplitPlan split_plan(const DecodeArgs& a, int b) {
     return p;
 }
 
+// ---- work list over several sequences. Per-sequence splits leave the grid as ragged as
+// the batch: at 16 sequences of 1K..32K keys, 2048-key splits give ~340 live workgroups of
+// unequal length on 256 CUs, and the short ones finish early while the long ones cannot
+// keep enough bytes in flight. Instead every workgroup computes one plan from key_len:
+// chunk = ceil(sum of active keys x kvH / list_target) (a multiple of 16), sequence b gets
+// ceil(active_b / chunk) splits per kv head, and the units (sequence, kv head, split) are
+// numbered in that order, unit L on workgroup L. The host sizes the grid to
+// list_target + pairs, which bounds the unit count, and list_target to what stays
+// resident, so all units run at once and end together.
+__device__ __forceinline__ int active_keys(const DecodeArgs& a, int T) {
+    return T <= 0 ? 0 : (a.window > 0 && T > a.window) ? a.window : T;
+}
+__device__ __forceinline__ int ceil_div(int x, int d) { return x / d + (x % d != 0); }
+
+// chunk of the plan; act0 returns this lane's sequence of the first 64 (its active keys),
+// so a batch of up to 64 sequences reads key_len once
+__device__ __forceinline__ int list_chunk(const DecodeArgs& a, int& act0) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long tot = 0;
+    act0 = 0;
+    for (int s0 = 0; s0 < a.n_seq; s0 += 64) {
+        const int s = s0 + lane;
+        const int act = s < a.n_seq ? active_keys(a, a.key_len[s]) : 0;
+        if (s0 == 0) act0 = act;
+        tot += (unsigned)act;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) tot += __shfl_xor(tot, d);
+    unsigned long long c = (tot * (unsigned)a.n_kv_heads + a.list_target - 1) / (unsigned)a.list_target;
+    c = (c + 15) & ~15ull;
+    c = c < (unsigned)a.chunk ? (unsigned)a.chunk : c;
+    c = c > (unsigned)a.chunk_cap ? (unsigned)a.chunk_cap : c;
+    return __builtin_amdgcn_readfirstlane((int)c);
+}
+
+__device__ __forceinline__ int list_active(const DecodeArgs& a, int s0, int act0, int n) {
+    const int s = s0 + (threadIdx.x & 63);
+    return s0 == 0 ? (s < n ? act0 : 0) : (s < n ? active_keys(a, a.key_len[s]) : 0);
+}
+
+struct ListUnit {
+    int b, kh, ci, splits;
+};
+// the unit of workgroup L (b = -1: past the last unit)
+__device__ __forceinline__ ListUnit list_unit(const DecodeArgs& a, int chunk, int act0, int L) {
+    int base = 0;  // units of the sequences before this group of 64
+    for (int s0 = 0; s0 < a.n_seq; s0 += 64) {
+        const int sp = ceil_div(list_active(a, s0, act0, a.n_seq), chunk);
+        const int incl = wave_prefix_sum(sp * a.n_kv_heads);
+        const unsigned long long past = __ballot(base + incl > L);
+        if (past) {
+            const int j = __builtin_ctzll(past);
+            const int splits = __builtin_amdgcn_readlane(sp, j);
+            const int r = L - (base + __builtin_amdgcn_readlane(incl, j) - splits * a.n_kv_heads);
+            return ListUnit{s0 + j, r / splits, r % splits, splits};
+        }
+        base += __builtin_amdgcn_readlane(incl, 63);
+    }
+    return ListUnit{-1, 0, 0, 0};
+}
+// first unit of sequence b and its splits per kv head
+__device__ __forceinline__ int list_first(const DecodeArgs& a, int chunk, int act0, int b, int& splits) {
+    int base = 0;
+    for (int s0 = 0; s0 < b; s0 += 64)
+        base += __builtin_amdgcn_readlane(wave_prefix_sum(ceil_div(list_active(a, s0, act0, b), chunk)), 63);
+    const int act_b = b < 64 ? __builtin_amdgcn_readlane(act0, b) : active_keys(a, a.key_len[b]);
+    splits = __builtin_amdgcn_readfirstlane(ceil_div(act_b, chunk));
+    return base * a.n_kv_heads;
+}
+
 // QP consecutive f32 (QP = 2 or 4) from a buffer
 template <int QP>
 __device__ __forceinline__ void bload_q(rsrc_t r, int off, float (&x)[QP]) {
@@ -180,10 +256,26 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     const int n = lane & 15, g = lane >> 4;
-    const int ci = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-    const int pair = b * a.n_kv_heads + kh;
+    int ci, kh, b;
+    SplitPlan sp;
+    size_t slot;  // partial slot of this workgroup
+    if (a.list_target > 0) {
+        int act0;
+        const int chunk = list_chunk(a, act0);
+        const ListUnit u = list_unit(a, chunk, act0, blockIdx.x);
+        if (u.b < 0) return;  // past the last unit
+        b = u.b, kh = u.kh, ci = u.ci;
+        sp.hi = a.key_len[b];
+        sp.lo = (a.window > 0 && sp.hi > a.window) ? sp.hi - a.window : 0;
+        sp.active = sp.hi - sp.lo;
+        sp.chunk = chunk;
+        slot = blockIdx.x;
+    } else {
+        ci = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+        sp = split_plan(a, b);  // scalar load of key_len, issued first
+        slot = (size_t)(b * a.n_kv_heads + kh) * a.max_splits + ci;
+    }
     float* outp = a.out + ((size_t)b * a.n_q_heads + (size_t)kh * G) * HD;
-    const SplitPlan sp = split_plan(a, b);  // scalar load of key_len, issued first
 
     // ---- q operand loads: they depend on nothing but the sequence and kv head.
     // Wave w prepares heads w, w+4 (a head >= G reads past the q range: zeros, no traffic).
@@ -213,7 +305,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         if (single) {
             for (int e = tid; e < G * HD; e += 256) outp[e] = 0.0f;  // no keys: zeros
         } else if (tid < G) {
-            a.part_ml[((size_t)pair * a.max_splits + ci) * G + tid] = make_float2(kNegInf, 0.0f);
+            a.part_ml[slot * G + tid] = make_float2(kNegInf, 0.0f);
         }
         return;
     }
@@ -377,8 +469,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) r[i] = srq(o[i] * inv, a.out_q);
             *reinterpret_cast<float4v*>(outp + e) = r;
         } else {
-            *reinterpret_cast<float4v*>(a.part_o + ((size_t)pair * a.max_splits + ci) * (G * HD) + e) = o;
-            if (e % HD == 0) a.part_ml[((size_t)pair * a.max_splits + ci) * G + hh] = make_float2(M, L);
+            *reinterpret_cast<float4v*>(a.part_o + slot * (G * HD) + e) = o;
+            if (e % HD == 0) a.part_ml[slot * G + hh] = make_float2(M, L);
         }
     }
 }
@@ -433,6 +525,67 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     }
 }
 
+// The same merge over a work list: the splits of (sequence b, kv head kh) are the units
+// [first, first + splits) of the plan, every one written by this call. Thread (sg, dim e)
+// folds splits sg, sg+4, .. into a running (m, l, o) eight loads at a time; the four
+// split groups are combined through LDS.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
+    constexpr int E = G * HD;
+    __shared__ float sm[4][64], sl[4][64], so[4][64];
+    const int tid = threadIdx.x, lane = tid & 63, sg = tid >> 6;
+    const int e = blockIdx.x * 64 + lane, hh = (blockIdx.x * 64) / HD;
+    const int kh = blockIdx.y, b = blockIdx.z;
+    int act0, splits;
+    const int chunk = list_chunk(a, act0);
+    const int u0 = list_first(a, chunk, act0, b, splits) + kh * splits;
+    // only with a chunk held at chunk_cap could units fall past the grid (key lengths no
+    // cache in device memory can hold): their slots were never written
+    if (u0 + splits > a.list_units) splits = max(0, a.list_units - u0);
+    float M = kNegInf, Ls = 0.0f, O = 0.0f;
+    for (int s0 = sg; s0 < splits; s0 += 32) {
+        float2 ml[8];
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int s = s0 + 4 * j;
+            const size_t u = (size_t)u0 + (s < splits ? s : s0);
+            ml[j] = a.part_ml[u * G + hh];
+            o[j] = a.part_o[u * E + e];
+            if (s >= splits) ml[j].x = kNegInf;
+        }
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bm = fmaxf(bm, ml[j].x);
+        const float c = M == kNegInf ? 0.0f : fexp2(M - bm);  // bm is finite: split s0 is live
+        Ls *= c;
+        O *= c;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float w = ml[j].x == kNegInf ? 0.0f : fexp2(ml[j].x - bm);
+            Ls = w != 0.0f ? fmaf(w, ml[j].y, Ls) : Ls;
+            O = w != 0.0f ? fmaf(w, o[j], O) : O;
+        }
+        M = bm;
+    }
+    sm[sg][lane] = M;
+    sl[sg][lane] = Ls;
+    so[sg][lane] = O;
+    __syncthreads();
+    if (sg == 0) {
+        const float Mx = fmaxf(fmaxf(sm[0][lane], sm[1][lane]), fmaxf(sm[2][lane], sm[3][lane]));
+        float L = 0.0f, t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float w = sm[k][lane] == kNegInf ? 0.0f : fexp2(sm[k][lane] - Mx);
+            L = w != 0.0f ? fmaf(w, sl[k][lane], L) : L;
+            t = w != 0.0f ? fmaf(w, so[k][lane], t) : t;
+        }
+        // L = 0 only when the sequence attends no key: defined output of zeros
+        a.out[((size_t)b * a.n_q_heads + (size_t)kh * G) * HD + e] = L > 0.0f ? srq(t * (1.0f / L), a.out_q) : 0.0f;
+    }
+}
+
 // ---------------------------------------------------------------- host side
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
@@ -465,18 +618,39 @@ static int decode_splits(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     return (int)(s < 1 ? 1 : s);
 }
 
+// The work list (several sequences whose longest needs more than one split): units are
+// spread over what stays resident at once -- two 4-wave workgroups per CU on the 256 CUs
+// for the hd-256 f16 kernel (its registers allow two waves per SIMD), one otherwise -- less
+// one unit per pair, the most the per-pair rounding up can add.
+struct ListPlan {
+    int target, grid;
+};
+static ListPlan list_plan(const g4a_cfg* cfg, int n_seq, int max_key_len) {
+    ListPlan p{0, 0};
+    if (n_seq <= 1 || decode_splits(cfg, n_seq, max_key_len) <= 1) return p;
+    const bool f32 = (cfg->flags & G4A_KV_F32) != 0;
+    const int resident = env_int("G4A_DECODE_RESIDENT", cfg->head_dim == 256 && !f32 ? 512 : 256);
+    const long pairs = (long)n_seq * cfg->n_kv_heads;
+    p.target = resident - pairs > resident / 2 ? (int)(resident - pairs) : resident / 2;
+    p.grid = (int)(p.target + pairs);
+    return p;
+}
+
 struct WsLayout {
     size_t ml, o, total;
 };
 
-static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_splits) {
-    const size_t pairs = (size_t)n_seq * cfg->n_kv_heads;
+// partial slots: max_splits per pair, or one per work-list unit
+static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_key_len) {
+    const ListPlan lp = list_plan(cfg, n_seq, max_key_len);
+    const size_t slots = lp.grid > 0 ? (size_t)lp.grid
+                                     : (size_t)n_seq * cfg->n_kv_heads * decode_splits(cfg, n_seq, max_key_len);
     const size_t G = cfg->n_q_heads / cfg->n_kv_heads;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout L;
     L.ml = 0;
-    L.o = L.ml + al(pairs * max_splits * G * sizeof(float2));
-    L.total = L.o + pairs * max_splits * G * cfg->head_dim * sizeof(float);
+    L.o = L.ml + al(slots * G * sizeof(float2));
+    L.total = L.o + slots * G * cfg->head_dim * sizeof(float);
     return L;
 }
 
@@ -503,6 +677,16 @@ static decode_fn pick_merge_nb(int splits) {
     return decode_merge_kernel<HD, G, 4>;
 }
 template <int HD>
+static decode_fn pick_merge_list(int G) {
+    switch (G) {
+        case 1: return decode_merge_list_kernel<HD, 1>;
+        case 2: return decode_merge_list_kernel<HD, 2>;
+        case 4: return decode_merge_list_kernel<HD, 4>;
+        case 8: return decode_merge_list_kernel<HD, 8>;
+    }
+    return nullptr;
+}
+template <int HD>
 static decode_fn pick_merge(int G, int splits) {
     switch (G) {
         case 1: return pick_merge_nb<HD, 1>(splits);
@@ -519,7 +703,7 @@ using namespace g4a;
 
 extern "C" size_t g4a_decode_ws_bytes(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     if (!check_cfg(cfg, true) || n_seq <= 0 || max_key_len <= 0) return 0;
-    return ws_layout(cfg, n_seq, decode_splits(cfg, n_seq, max_key_len)).total;
+    return ws_layout(cfg, n_seq, max_key_len).total;
 }
 
 extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
@@ -557,7 +741,8 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
         return G4A_EINVAL;
     }
     const int splits = decode_splits(cfg, n_seq, max_key_len);
-    const WsLayout L = ws_layout(cfg, n_seq, splits);
+    const ListPlan lp = list_plan(cfg, n_seq, max_key_len);
+    const WsLayout L = ws_layout(cfg, n_seq, max_key_len);
     if (!ws || ws_bytes < L.total || ((uintptr_t)ws % 256)) {
         set_error("decode workspace needs %zu bytes (256-byte aligned), got %zu", L.total, ws_bytes);
         return G4A_EWORKSPACE;
@@ -582,11 +767,28 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
-    a.max_splits = splits;
-    a.chunk = decode_chunk(cfg, n_seq, max_key_len);
-    if ((int64_t)(a.chunk + 64) * cfg->n_kv_heads * HD * (int64_t)esz > 0x7fffffff) {
-        set_error("keys per split too large for 32-bit buffer offsets");
-        return G4A_EINVAL;
+    const int64_t row_bytes = (int64_t)cfg->n_kv_heads * HD * (int64_t)esz;
+    a.n_seq = n_seq;
+    a.list_target = lp.target;
+    a.list_units = lp.grid;
+    if (lp.grid > 0) {
+        // work list: units of at least 64 keys (every wave of a workgroup busy); a unit's
+        // byte offsets stay within 32 bits
+        a.max_splits = 0;
+        a.chunk = 64;
+        a.chunk_cap = (int)(((0x7fffffff / row_bytes) - 64) & ~15LL);
+        if (a.chunk_cap < a.chunk) {
+            set_error("cache rows too large for 32-bit buffer offsets");
+            return G4A_EINVAL;
+        }
+    } else {
+        a.max_splits = splits;
+        a.chunk = decode_chunk(cfg, n_seq, max_key_len);
+        a.chunk_cap = 0;
+        if ((int64_t)(a.chunk + 64) * row_bytes > 0x7fffffff) {
+            set_error("keys per split too large for 32-bit buffer offsets");
+            return G4A_EINVAL;
+        }
     }
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
@@ -596,12 +798,13 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
         set_error("no decode kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
     }
-    dim3 grid(splits, cfg->n_kv_heads, n_seq);
+    const dim3 grid = lp.grid > 0 ? dim3(lp.grid) : dim3(splits, cfg->n_kv_heads, n_seq);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "decode launch");
-    if (splits > 1) {
-        decode_fn mf = HD == 256 ? pick_merge<256>(G, splits) : pick_merge<512>(G, splits);
+    if (lp.grid > 0 || splits > 1) {
+        decode_fn mf = lp.grid > 0 ? (HD == 256 ? pick_merge_list<256>(G) : pick_merge_list<512>(G))
+                                   : (HD == 256 ? pick_merge<256>(G, splits) : pick_merge<512>(G, splits));
         hipLaunchKernelGGL(mf, dim3(G * HD / 64, cfg->n_kv_heads, n_seq), dim3(256), 0, (hipStream_t)stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return hip_error(e, "decode merge launch");

@@ -151,6 +151,49 @@ def test_ragged_batch_with_window():
     contract_close(got, ref, "ragged batch")
 
 
+@pytest.mark.parametrize("B,nH,kvH,hd,kv_dtype,window", [
+    (80, 8, 2, 256, np.float16, 0),     # more than 64 sequences: the plan's multi-group passes
+    (80, 8, 2, 256, np.float16, 96),
+    (70, 4, 1, 512, np.float16, 0),     # hd 512: one resident workgroup per CU
+    (67, 4, 2, 256, np.float32, 0),     # f32 caches
+])
+def test_work_list_many_ragged_sequences(B, nH, kvH, hd, kv_dtype, window):
+    """Several sequences run as one work list of equal-length units over all of them
+    (sequence, kv head, split in order). Lengths include 0 (no unit, zero output), 1, and
+    one sequence far longer than the rest, which takes most of the units."""
+    rng = np.random.default_rng(B + hd)
+    lens = rng.integers(0, 300, size=B).astype(np.int32)
+    lens[:4] = [0, 1, 2900, 16]
+    Tmax = int(lens.max())
+    q = rng.standard_normal((B, nH, hd)).astype(np.float32)
+    k = rng.standard_normal((B, Tmax, kvH, hd)).astype(kv_dtype)
+    v = rng.standard_normal((B, Tmax, kvH, hd)).astype(kv_dtype)
+    got = run(q, k, v, t(lens), sa.AttnConfig(nH, kvH, hd, window))
+    for b in range(B):
+        L = int(lens[b])
+        if L == 0:
+            assert np.array_equal(got[b], np.zeros_like(got[b])), f"seq {b} has no keys"
+            continue
+        ref = O.decode_attention(q[b], k[b, :L].astype(np.float32), v[b, :L].astype(np.float32), L, kvH,
+                                 window=window)
+        contract_close(got[b], ref, f"seq {b} len {L}")
+
+
+def test_work_list_skewed_pair():
+    """Two sequences, one 64x longer: the long one is cut into many units, the short one
+    into one, and the merge finds each sequence's units."""
+    lens = np.array([8192, 128], np.int32)
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((2, 8, 256)).astype(np.float32)
+    k = rng.standard_normal((2, 8192, 2, 256)).astype(np.float16)
+    v = rng.standard_normal((2, 8192, 2, 256)).astype(np.float16)
+    got = run(q, k, v, t(lens), sa.AttnConfig(8, 2, 256))
+    for b in range(2):
+        L = int(lens[b])
+        ref = O.decode_attention(q[b], k[b, :L].astype(np.float32), v[b, :L].astype(np.float32), L, 2)
+        contract_close(got[b], ref, f"seq {b} len {L}")
+
+
 @pytest.mark.parametrize("T", [1, 63, 64, 65, 255, 256, 257, 511])
 @pytest.mark.parametrize("dw", [None, -1, 0, 1])
 def test_mask_set_exact(T, dw):
