@@ -36,7 +36,7 @@ extern "C" {
 /* cfg.flags */
 #define G4A_KV_F32    0x1u /* caches hold f32 (the reference's own cache type); default f16 */
 #define G4A_IN_F16    0x2u /* g4a_kv_write: k/v inputs are f16 (kvnorm_b); default f32 (kvnorm) */
-#define G4A_NO_V_NORM 0x4u /* g4a_kv_write: store v as given instead of RMSNorm(v) */
+#define G4A_NO_V_NORM 0x4u /* g4a_kv_write, g4a_decode_kv: store v as given instead of RMSNorm(v) */
 #define G4A_OUT_F32   0x8u /* g4a_prefill: f32 output (attn_prefill's "out"); default f16 (attnh) */
 #define G4A_Q_HILO    0x10u /* g4a_prefill: keep q at f32 accuracy (f16 hi + lo MFMA operands),
                                as attn_prefill's f32 q (kernels_dsl.py:2007-2014); default rounds
@@ -92,6 +92,24 @@ int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* ke
                const float* q, const float* q_gain, const float* rope_cos, const float* rope_sin,
                const void* k_cache, const void* v_cache, int64_t seq_stride, float* out,
                void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Decode step with its KV write fused in: the kvnorm dispatch (kernels_dsl.py:573-618,
+ * bound at runner.py:424-429) and the attn_101 dispatch that follows it
+ * (runner.py:430-441) as one call. For every sequence s with key_len[s] > 0 the raw rows
+ * k_new/v_new [n_seq][n_kv_heads][head_dim] (f32, the q/k/v projection's output) are
+ * prepared exactly as g4a_kv_write prepares them (srq with k_in_q / v_in_q, k RMSNorm *
+ * k_gain then RoPE with the sequence's rope_cos/rope_sin row -- the query's position --,
+ * v RMSNorm unless G4A_NO_V_NORM) and stored at row key_len[s]-1 of the caches; the
+ * attention then includes that row. The workgroup whose split holds the new key writes
+ * it, so the row costs no extra kernel. Other arguments, the workspace and the result
+ * are those of g4a_decode; the caches are written, so they are not const here.
+ */
+int g4a_decode_kv(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                  const float* q, const float* q_gain, const float* rope_cos, const float* rope_sin,
+                  const float* k_new, const float* v_new, float k_in_q, float v_in_q,
+                  const float* k_gain, void* k_cache, void* v_cache, int64_t seq_stride, float* out,
+                  void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Batched causal prefill attention for S tokens at positions start_pos..start_pos+S-1.

@@ -105,12 +105,17 @@ Workspace = DecodeWorkspace
 
 def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
            rope_sin=None, out=None, workspace: DecodeWorkspace | None = None,
-           max_key_len: int | None = None):
+           max_key_len: int | None = None, k_new=None, v_new=None, k_gain=None,
+           k_in_q: float = 0.0, v_in_q: float = 0.0):
     """Decode attention for n_seq sequences (one query each).
 
     q [n_seq][nH][hd] (or [nH][hd]) f32; caches [n_seq][max_seq][kvH][hd] (or
     [max_seq][kvH][hd]) f16/f32; key_len int32 device tensor [n_seq] or python ints;
     rope_cos/sin [n_seq][hd/2] (or [hd/2]) rows for each query position.
+    With k_new/v_new (f32 [n_seq][kvH][hd], or [kvH][hd]) the step's KV write is fused
+    in (g4a_decode_kv): those raw rows are prepared as kv_write prepares them (srq with
+    k_in_q/v_in_q, k RMSNorm*k_gain + RoPE with the query's rope row, v RMSNorm) and
+    stored at row key_len-1 before being attended.
     Returns out f32 shaped like q.
     """
     single = q.dim() == 2
@@ -152,9 +157,23 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
     if out is None:
         out = torch.empty_like(q3)
     _need(out, "out", torch.float32)
-    check(lib.g4a_decode(ctypes.byref(c), n_seq, max_key_len, _ptr(key_len), _ptr(q3), _ptr(q_gain),
-                         _ptr(rope_cos), _ptr(rope_sin), _ptr(kc), _ptr(vc),
-                         kc.stride(0), _ptr(out), _ptr(ws), ws.numel(), ctypes.c_void_p(_stream())))
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is None:
+        check(lib.g4a_decode(ctypes.byref(c), n_seq, max_key_len, _ptr(key_len), _ptr(q3), _ptr(q_gain),
+                             _ptr(rope_cos), _ptr(rope_sin), _ptr(kc), _ptr(vc),
+                             kc.stride(0), _ptr(out), _ptr(ws), ws.numel(), ctypes.c_void_p(_stream())))
+    else:
+        rows = (n_seq, cfg.n_kv_heads, cfg.head_dim)
+        for name, x in (("k_new", k_new), ("v_new", v_new)):
+            _need(x, name, torch.float32)
+            if x.numel() != n_seq * cfg.n_kv_heads * cfg.head_dim:
+                raise ValueError(f"{name} must hold {rows} f32 rows")
+        _need(k_gain, "k_gain", torch.float32)
+        check(lib.g4a_decode_kv(ctypes.byref(c), n_seq, max_key_len, _ptr(key_len), _ptr(q3), _ptr(q_gain),
+                                _ptr(rope_cos), _ptr(rope_sin), _ptr(k_new), _ptr(v_new), float(k_in_q),
+                                float(v_in_q), _ptr(k_gain), _ptr(kc), _ptr(vc), kc.stride(0), _ptr(out),
+                                _ptr(ws), ws.numel(), ctypes.c_void_p(_stream())))
     return out[0] if single and out.dim() == 3 else out
 
 

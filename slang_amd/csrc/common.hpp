@@ -203,4 +203,46 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
         }
 }
 
+// One RoPE pair (d, d + hd/2) of a new k and v row, per thread t = d < hd/2 of the first
+// hd/128 waves (kvnorm, kernels_dsl.py:573-618; kvnorm_b, :1789-1834): k <- RoPE(RMSNorm(k)
+// * gain), v <- RMSNorm(v) without scale. The sums of squares run per wave then over the
+// waves in order through `red` (2 x hd/128 floats of LDS), so g4a_kv_write and the fused
+// decode write identical rows. Every wave of the workgroup must call it (one barrier);
+// threads t >= hd/2 pass zeros and ignore the result.
+template <int HD>
+__device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, float& v1, const float* k_gain,
+                                             const float* rcos, const float* rsin, bool v_norm, float eps,
+                                             float* red, int t) {
+    constexpr int HALF = HD / 2, NW = HALF / 64;
+    const float sk_w = wave_sum(k0 * k0 + k1 * k1), sv_w = wave_sum(v0 * v0 + v1 * v1);
+    if (t < HALF && (t & 63) == 0) {
+        red[t >> 6] = sk_w;
+        red[NW + (t >> 6)] = sv_w;
+    }
+    __syncthreads();
+    if (t >= HALF) return;
+    float sk = 0.0f, sv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        sk += red[w];
+        sv += red[NW + w];
+    }
+    if (k_gain) {
+        const float rs = 1.0f / sqrtf(sk / (float)HD + eps);  // kvnorm's k * rmsk * knorm
+        k0 = k0 * rs * k_gain[t];
+        k1 = k1 * rs * k_gain[t + HALF];
+    }
+    if (rcos) {
+        const float c = rcos[t], sn = rsin[t];
+        const float x0 = k0, x1 = k1;
+        k0 = x0 * c - x1 * sn;
+        k1 = x1 * c + x0 * sn;
+    }
+    if (v_norm) {
+        const float rs = 1.0f / sqrtf(sv / (float)HD + eps);
+        v0 = v0 * rs;
+        v1 = v1 * rs;
+    }
+}
+
 }  // namespace g4a

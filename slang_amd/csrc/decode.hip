@@ -57,6 +57,16 @@ struct DecodeArgs {
     // work list (several sequences): list_target > 0 spreads all active keys over about
     // list_target units of equal length (>= chunk keys, <= chunk_cap), one workgroup each
     int n_seq, list_target, chunk_cap, list_units;  // list_units: the grid, units past it never run
+    // fused KV write (g4a_decode_kv): k_new != NULL gives each sequence's raw k/v row
+    // [n_seq][kvH][HD] for position key_len - 1, prepared and stored by the workgroup
+    // whose split holds that key
+    const float* k_new;
+    const float* v_new;
+    const float* k_gain;
+    void* kc_out;
+    void* vc_out;
+    float k_in_q, v_in_q;
+    int v_norm;
 };
 
 template <int HD, int G>
@@ -98,12 +108,17 @@ template <>
 struct KOp<half_t> {
     struct raw { half8 h; };
     static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_h8(r, off)}; }
+    static __device__ __forceinline__ raw lds(const half_t* p) { return raw{*reinterpret_cast<const half8*>(p)}; }
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16x32(k.h, q, c); }
 };
 template <>
 struct KOp<float> {
     struct raw { float8v f; };
     static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_f8(r, off)}; }
+    static __device__ __forceinline__ raw lds(const float* p) {
+        const float4v a = *reinterpret_cast<const float4v*>(p), b = *reinterpret_cast<const float4v*>(p + 4);
+        return raw{float8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}};
+    }
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) {
         const half8 hi = __builtin_convertvector(k.f, half8);
         const half8 lo = __builtin_convertvector(k.f - __builtin_convertvector(hi, float8v), half8);
@@ -235,8 +250,11 @@ __device__ __forceinline__ void bload_q(rsrc_t r, int off, float (&x)[QP]) {
     }
 }
 
+// hd 256 with f16 caches fits two waves per SIMD (two workgroups per CU, which the work
+// list's resident count assumes); the attribute holds the allocator to that.
 template <int HD, int G, typename KVT>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 && sizeof(KVT) == 2 ? 2 : 1)))
+void decode_kernel(DecodeArgs a) {
     using Sh = DecodeShape<HD, G>;
     constexpr int KSTEPS = Sh::KSTEPS, NDT = Sh::NDT, VLANES = Sh::VLANES, VROWS = Sh::VROWS;
     constexpr int VLOADS = Sh::VLOADS, VSTR = Sh::VSTR, QSTR = Sh::QSTR;
@@ -252,6 +270,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     half_t* sV = reinterpret_cast<half_t*>(arena);
     float* lds = reinterpret_cast<float*>(arena);
     __shared__ float lds_m[4][G], lds_l[4][G];
+    __shared__ __attribute__((aligned(16))) KVT sKn[HD], sVn[HD];  // fused KV write: the new row
+    __shared__ float kv_red[2 * (HD / 128)];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -311,6 +331,20 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     }
     const int k0 = sp.lo + ci * sp.chunk;
     const int k1 = min(k0 + sp.chunk, sp.hi);
+
+    // ---- fused KV write: this workgroup's split holds the new key p = key_len - 1; its raw
+    // k/v loads go out before the first block's, the row is prepared with the q prologue
+    constexpr int HALF = HD / 2;
+    const int p_new = sp.hi - 1;
+    const bool owns_new = a.k_new != nullptr && p_new >= k0 && p_new < k1;  // workgroup-uniform
+    float nk0 = 0.0f, nk1 = 0.0f, nv0 = 0.0f, nv1 = 0.0f;
+    if (owns_new && tid < HALF) {
+        const size_t ro = ((size_t)b * a.n_kv_heads + kh) * HD;
+        nk0 = srq(a.k_new[ro + tid], a.k_in_q);
+        nk1 = srq(a.k_new[ro + tid + HALF], a.k_in_q);
+        nv0 = srq(a.v_new[ro + tid], a.v_in_q);
+        nv1 = srq(a.v_new[ro + tid + HALF], a.v_in_q);
+    }
 
     // ---- block loads through buffer resources over rows [k0, k1) of this kv head: rows
     // past k1 read as zeros without memory traffic, so no index is clamped. K in the MFMA
@@ -377,6 +411,23 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
             sQ[(G + hh) * QSTR + HD / 2 + d0 + e] = (half_t)(r1 - (float)h1);
         }
     }
+    if (owns_new) {  // every wave takes part (one barrier inside)
+        kv_pair_prep<HD>(nk0, nk1, nv0, nv1, a.k_gain, a.rcos ? a.rcos + (size_t)b * HALF : nullptr,
+                         a.rsin ? a.rsin + (size_t)b * HALF : nullptr, a.v_norm != 0, a.eps, kv_red, tid);
+        if (tid < HALF) {
+            const size_t crow = (size_t)b * a.seq_stride + (size_t)p_new * a.n_kv_heads * HD + (size_t)kh * HD;
+            KVT* kcw = reinterpret_cast<KVT*>(a.kc_out) + crow;
+            KVT* vcw = reinterpret_cast<KVT*>(a.vc_out) + crow;
+            store_elem(kcw + tid, nk0);
+            store_elem(kcw + tid + HALF, nk1);
+            store_elem(vcw + tid, nv0);
+            store_elem(vcw + tid + HALF, nv1);
+            sKn[tid] = (KVT)nk0;
+            sKn[tid + HALF] = (KVT)nk1;
+            sVn[tid] = (KVT)nv0;
+            sVn[tid + HALF] = (KVT)nv1;
+        }
+    }
     __syncthreads();
     half8 qop[KSTEPS];
 #pragma unroll
@@ -393,12 +444,25 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
 
     for (; blk < k1; blk += 64) {
+        // the block holding the new key: its row comes from the prepared copy, whatever
+        // the load (issued before the store) returned
+        const bool patch = owns_new && p_new >= blk && p_new < blk + 16;  // wave-uniform
+        if (patch && n == p_new - blk) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::lds(&sKn[32 * s + 8 * g]);
+        }
         float4v c4 = float4v{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
 #pragma unroll
         for (int i = 0; i < VLOADS; ++i)
             *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
+        if (patch && lane < HD / 8) {  // rounded to f16 as VO::h rounds a loaded row
+            half8 hv;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hv[i] = (half_t)(float)sVn[8 * lane + i];
+            *reinterpret_cast<half8*>(&myV[(p_new - blk) * VSTR + 8 * lane]) = hv;
+        }
         if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during softmax and P.V
         float sc[4], mloc = kNegInf;
 #pragma unroll
@@ -706,10 +770,17 @@ extern "C" size_t g4a_decode_ws_bytes(const g4a_cfg* cfg, int n_seq, int max_key
     return ws_layout(cfg, n_seq, max_key_len).total;
 }
 
-extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
-                          const float* q, const float* q_gain, const float* rope_cos,
-                          const float* rope_sin, const void* k_cache, const void* v_cache,
-                          int64_t seq_stride, float* out, void* ws, size_t ws_bytes, void* stream) {
+struct KvNew {
+    const float* k;
+    const float* v;
+    const float* k_gain;
+    float k_in_q, v_in_q;
+};
+
+static int decode_impl(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                       const float* q, const float* q_gain, const float* rope_cos, const float* rope_sin,
+                       const void* k_cache, const void* v_cache, int64_t seq_stride, float* out, void* ws,
+                       size_t ws_bytes, void* stream, const KvNew* kvn) {
     if (!check_cfg(cfg, true)) return G4A_EINVAL;
     if (n_seq <= 0 || max_key_len <= 0) {
         set_error("n_seq (%d) and max_key_len (%d) must be positive", n_seq, max_key_len);
@@ -793,6 +864,14 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;
+    a.k_new = kvn ? kvn->k : nullptr;
+    a.v_new = kvn ? kvn->v : nullptr;
+    a.k_gain = kvn ? kvn->k_gain : nullptr;
+    a.kc_out = const_cast<void*>(k_cache);
+    a.vc_out = const_cast<void*>(v_cache);
+    a.k_in_q = kvn ? kvn->k_in_q : 0.0f;
+    a.v_in_q = kvn ? kvn->v_in_q : 0.0f;
+    a.v_norm = (cfg->flags & G4A_NO_V_NORM) ? 0 : 1;
     decode_fn fn = HD == 256 ? pick_g<256>(G, f32) : pick_g<512>(G, f32);
     if (!fn) {
         set_error("no decode kernel for group size %d", G);
@@ -810,4 +889,38 @@ extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const 
         if (e != hipSuccess) return hip_error(e, "decode merge launch");
     }
     return G4A_OK;
+}
+
+extern "C" int g4a_decode(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                          const float* q, const float* q_gain, const float* rope_cos,
+                          const float* rope_sin, const void* k_cache, const void* v_cache,
+                          int64_t seq_stride, float* out, void* ws, size_t ws_bytes, void* stream) {
+    return decode_impl(cfg, n_seq, max_key_len, key_len, q, q_gain, rope_cos, rope_sin, k_cache, v_cache,
+                            seq_stride, out, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" int g4a_decode_kv(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                             const float* q, const float* q_gain, const float* rope_cos,
+                             const float* rope_sin, const float* k_new, const float* v_new, float k_in_q,
+                             float v_in_q, const float* k_gain, void* k_cache, void* v_cache,
+                             int64_t seq_stride, float* out, void* ws, size_t ws_bytes, void* stream) {
+    if (!k_new || !v_new) {
+        set_error("k_new and v_new must be non-NULL");
+        return G4A_EINVAL;
+    }
+    if (!(k_in_q >= 0.0f) || !(v_in_q >= 0.0f)) {
+        set_error("k_in_q/v_in_q must be >= 0");
+        return G4A_EINVAL;
+    }
+    if (cfg && (cfg->flags & G4A_IN_F16)) {
+        set_error("g4a_decode_kv takes f32 k/v rows (G4A_IN_F16 not supported)");
+        return G4A_EUNSUPPORTED;
+    }
+    if ((uintptr_t)k_new % 4 || (uintptr_t)v_new % 4 || (k_gain && (uintptr_t)k_gain % 4)) {
+        set_error("k_new, v_new and k_gain must be 4-byte aligned");
+        return G4A_EINVAL;
+    }
+    const KvNew kvn{k_new, v_new, k_gain, k_in_q, v_in_q};
+    return decode_impl(cfg, n_seq, max_key_len, key_len, q, q_gain, rope_cos, rope_sin, k_cache, v_cache,
+                            seq_stride, out, ws, ws_bytes, stream, &kvn);
 }

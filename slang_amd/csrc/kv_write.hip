@@ -27,7 +27,7 @@ __device__ __forceinline__ float ld(const half_t* p) { return (float)*p; }
 template <int HD, typename IT, typename CT>
 __global__ __launch_bounds__(HD / 2) void kv_write_kernel(KvArgs a) {
     constexpr int HALF = HD / 2, NW = HALF / 64;
-    __shared__ float red[2][NW];
+    __shared__ float red[2 * NW];
     const int t = threadIdx.x, s = blockIdx.x, kh = blockIdx.y;
     const size_t row = ((size_t)s * a.n_kv_heads + kh) * HD;
     const IT* kin = reinterpret_cast<const IT*>(a.k) + row;
@@ -35,35 +35,8 @@ __global__ __launch_bounds__(HD / 2) void kv_write_kernel(KvArgs a) {
     float k0 = srq(ld(kin + t), a.k_in_q), k1 = srq(ld(kin + t + HALF), a.k_in_q);
     float v0 = srq(ld(vin + t), a.v_in_q), v1 = srq(ld(vin + t + HALF), a.v_in_q);
 
-    float sk = wave_sum(k0 * k0 + k1 * k1), sv = wave_sum(v0 * v0 + v1 * v1);
-    if ((t & 63) == 0) {
-        red[0][t >> 6] = sk;
-        red[1][t >> 6] = sv;
-    }
-    __syncthreads();
-    sk = 0.0f;
-    sv = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        sk += red[0][w];
-        sv += red[1][w];
-    }
-    if (a.k_gain) {
-        const float rs = 1.0f / sqrtf(sk / (float)HD + a.eps);  // kvnorm's k * rmsk * knorm
-        k0 = k0 * rs * a.k_gain[t];
-        k1 = k1 * rs * a.k_gain[t + HALF];
-    }
-    if (a.rcos) {
-        const float c = a.rcos[(size_t)s * HALF + t], sn = a.rsin[(size_t)s * HALF + t];
-        const float x0 = k0, x1 = k1;
-        k0 = x0 * c - x1 * sn;
-        k1 = x1 * c + x0 * sn;
-    }
-    if (a.v_norm) {
-        const float rs = 1.0f / sqrtf(sv / (float)HD + a.eps);
-        v0 = v0 * rs;
-        v1 = v1 * rs;
-    }
+    kv_pair_prep<HD>(k0, k1, v0, v1, a.k_gain, a.rcos ? a.rcos + (size_t)s * HALF : nullptr,
+                     a.rsin ? a.rsin + (size_t)s * HALF : nullptr, a.v_norm != 0, a.eps, red, t);
     const size_t crow = ((size_t)(a.start_pos + s) * a.n_kv_heads + kh) * HD;
     CT* kc = reinterpret_cast<CT*>(a.kc) + crow;
     CT* vc = reinterpret_cast<CT*>(a.vc) + crow;

@@ -263,7 +263,8 @@ class AttentionStack:
     def decode_layer(self, L: int, pos: int, a: torch.Tensor, sum_a: torch.Tensor, out=None):
         """Layer L's attention for one token at position pos from its normed, srq'd input a
         f32 [H] (and sum_a f32 [1]): qkv_70 -> kvnorm (non-shared layers) -> attn_101.
-        Returns the srq'd attention output f32 [nH][hd] (runner.py:408-441)."""
+        Returns the srq'd attention output f32 [nH][hd] (runner.py:408-441). The KV write of
+        a non-shared layer runs inside the decode call (g4a_decode_kv)."""
         s, man, w = self.man.layers[L], self.man, self.w[L]
         if not 0 <= pos < self.max_seq:
             raise ValueError(f"position {pos} outside the {self.max_seq}-row caches")
@@ -275,12 +276,9 @@ class AttentionStack:
                              k_out=sc.get("k_out", 0.0), v_out=sc.get("v_out", 0.0))
         kc, vc = self.caches(L)
         cos, sin = self._rows(L, pos, pos + 1)
-        if not s.shared:
-            A.kv_write(k.view(1, cfg.n_kv_heads, s.head_dim), v.view(1, cfg.n_kv_heads, s.head_dim), kc, vc,
-                       pos, A.AttnConfig(cfg.n_kv_heads, cfg.n_kv_heads, s.head_dim), k_gain=w["k_norm"],
-                       rope_cos=cos, rope_sin=sin)
+        kv = {} if s.shared else dict(k_new=k, v_new=v, k_gain=w["k_norm"])
         return A.decode(q.view(cfg.n_q_heads, s.head_dim), kc, vc, [pos + 1], cfg, q_gain=w["q_norm"],
-                        rope_cos=cos, rope_sin=sin, out=out, workspace=self.ws, max_key_len=pos + 1)
+                        rope_cos=cos, rope_sin=sin, out=out, workspace=self.ws, max_key_len=pos + 1, **kv)
 
     def _dequant(self, L):
         if L not in self.dq:

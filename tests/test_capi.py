@@ -76,6 +76,25 @@ def test_decode_argument_errors(lib):
     assert b"workspace" in lib.g4a_last_error()
 
 
+def test_decode_kv_argument_errors(lib):
+    """g4a_decode_kv checks its own arguments, then those of g4a_decode."""
+    D = lib.g4a_decode_kv
+
+    def call(c=None, k_new=FAKE, v_new=FAKE, k_in_q=0.0, v_in_q=0.0, **kw):
+        a = dict(n_seq=1, max_key_len=64, key_len=FAKE, q=FAKE, k=FAKE, v=FAKE, ws=FAKE, ws_bytes=1 << 30)
+        a.update(kw)
+        return D(ctypes.byref(c or cfg()), a["n_seq"], a["max_key_len"], a["key_len"], a["q"], None, None, None,
+                 k_new, v_new, k_in_q, v_in_q, None, a["k"], a["v"], 0, FAKE, a["ws"], a["ws_bytes"], None)
+
+    assert call(k_new=None) == -1
+    assert call(v_new=None) == -1
+    assert call(k_in_q=-1.0) == -1
+    assert call(c=cfg(flags=0x2)) == -2                                # f16 raw rows not taken
+    assert call(k_new=ctypes.c_void_p(0x10002)) == -1                   # misaligned
+    assert call(n_seq=0) == -1                                          # g4a_decode's checks
+    assert call(ws_bytes=16) == -3
+
+
 def test_decode_ws_bytes(lib):
     c = cfg()
     small = lib.g4a_decode_ws_bytes(ctypes.byref(c), 1, 64)

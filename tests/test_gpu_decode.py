@@ -284,3 +284,60 @@ def test_attn_101_mirror_matches_decode():
     with pytest.raises(ValueError):
         sa.attn_101(t(z[f"{tag}_q"].reshape(-1)), None, None, None, t(kc.reshape(-1)),
                     t(vc.reshape(-1)), None, out, (1, kl, kl, 8, 1, 0, 0, 0), head_dim=hd)
+
+
+# ---------------------------------------------------------------- fused KV write
+@pytest.mark.parametrize("B,nH,kvH,hd,window,cache,k_in_q", [
+    (1, 8, 2, 256, 0, torch.float16, 0.0),       # config 2 shape, one split per 64 keys
+    (1, 8, 2, 256, 512, torch.float16, 0.02),    # sliding, srq'd inputs
+    (1, 4, 1, 512, 0, torch.float16, 0.0),       # hd 512
+    (1, 8, 2, 256, 0, torch.float32, 0.0),       # f32 caches
+    (5, 8, 2, 256, 0, torch.float16, 0.0),       # a batch: the work list
+    (3, 4, 1, 512, 96, torch.float16, 0.0),
+])
+def test_decode_kv_matches_kv_write_then_decode(B, nH, kvH, hd, window, cache, k_in_q):
+    """g4a_decode_kv writes the same cache rows as g4a_kv_write (shared arithmetic, bit for
+    bit) and returns the same output as g4a_kv_write followed by g4a_decode; both meet the
+    contract against the oracle's kv_write + decode_attention."""
+    rng = np.random.default_rng(B * 100 + hd + window)
+    lens = np.array([rng.integers(1, 3000) for _ in range(B)], np.int32)
+    lens[0] = 2049 if B == 1 else lens[0]
+    Tmax = int(lens.max()) + 3
+    q = t(rng.standard_normal((B, nH, hd)).astype(np.float32))
+    qg = t((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    kg = t((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    kraw = t(rng.standard_normal((B, kvH, hd)).astype(np.float32))
+    vraw = t(rng.standard_normal((B, kvH, hd)).astype(np.float32))
+    c, s = O.rope_tables(lens - 1, hd, 1e4)
+    c, s = t(c), t(s)
+    base_k = torch.from_numpy(rng.standard_normal((B, Tmax, kvH, hd)).astype(np.float32)).to(DEV, cache)
+    base_v = torch.from_numpy(rng.standard_normal((B, Tmax, kvH, hd)).astype(np.float32)).to(DEV, cache)
+    cfg = sa.AttnConfig(nH, kvH, hd, window)
+    kvcfg = sa.AttnConfig(kvH, kvH, hd)
+    # separate: kv_write per sequence at its position, then decode
+    k1, v1 = base_k.clone(), base_v.clone()
+    for b in range(B):
+        p = int(lens[b]) - 1
+        sa.kv_write(kraw[b:b + 1], vraw[b:b + 1], k1[b], v1[b], p, kvcfg, k_gain=kg, rope_cos=c[b:b + 1],
+                    rope_sin=s[b:b + 1], k_in_q=k_in_q, v_in_q=k_in_q)
+    out1 = sa.decode(q, k1, v1, t(lens), cfg, q_gain=qg, rope_cos=c, rope_sin=s)
+    # fused
+    k2, v2 = base_k.clone(), base_v.clone()
+    out2 = sa.decode(q, k2, v2, t(lens), cfg, q_gain=qg, rope_cos=c, rope_sin=s, k_new=kraw, v_new=vraw,
+                     k_gain=kg, k_in_q=k_in_q, v_in_q=k_in_q)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2), "cache rows differ from g4a_kv_write's"
+    assert torch.equal(out1, out2), "fused decode differs from kv_write + decode"
+    # and against the oracle
+    qn, kn, vn = q.cpu().numpy(), k2.float().cpu().numpy(), v2.float().cpu().numpy()
+    cn, sn = c.cpu().numpy(), s.cpu().numpy()
+    got = out2.cpu().numpy()
+    for b in range(B):
+        L = int(lens[b])
+        kref, vref = O.kv_write(kraw[b:b + 1].cpu().numpy(), vraw[b:b + 1].cpu().numpy(), kg.cpu().numpy(),
+                                cn[b:b + 1], sn[b:b + 1], k_in_q=k_in_q, v_in_q=k_in_q,
+                                cache_dtype=np.float32 if cache == torch.float32 else np.float16)
+        contract_close(kn[b, L - 1:L], kref.astype(np.float32), f"seq {b} k row")
+        ref = O.decode_attention(qn[b], kn[b, :L], vn[b, :L], L, kvH, q_gain=qg.cpu().numpy(), cos=cn[b],
+                                 sin=sn[b], window=window)
+        contract_close(got[b], ref, f"seq {b} len {L}")
