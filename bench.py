@@ -329,6 +329,8 @@ def main():
                     help="only run a known-size copy kernel (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config 3 prefill rows (for profiling the prefill kernel)")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only the config 4 batched decode row (for profiling its kernels)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -349,6 +351,11 @@ def main():
             msp, fl = prefill_case(sa, 1024, win, th, args.steps, args.warmup, gen)
             out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
         print(json.dumps(out), flush=True)
+        return
+    if args.batched_only:
+        ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
+        print(json.dumps({"decode_4": {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
+                                       "sum_kv_len": toks}}), flush=True)
         return
     ms, nbytes, case = decode_case(sa, 4096, 0, 1e6, args.steps, args.warmup, 64, gen)
     gbs = nbytes / (ms * 1e-3) / 1e9

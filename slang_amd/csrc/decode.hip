@@ -252,7 +252,10 @@ __device__ __forceinline__ void bload_q(rsrc_t r, int off, float (&x)[QP]) {
 
 // hd 256 with f16 caches fits two waves per SIMD (two workgroups per CU, which the work
 // list's resident count assumes); the attribute holds the allocator to that.
-template <int HD, int G, typename KVT>
+// LIST: the unit comes from the work-list plan (several sequences); KVW: the fused KV write
+// of g4a_decode_kv. Both are template switches so the plain single-sequence kernel carries
+// neither (their code measured 0.2 us on the latency-bound T 4096 call).
+template <int HD, int G, typename KVT, bool LIST, bool KVW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 && sizeof(KVT) == 2 ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
     using Sh = DecodeShape<HD, G>;
@@ -270,7 +273,7 @@ void decode_kernel(DecodeArgs a) {
     half_t* sV = reinterpret_cast<half_t*>(arena);
     float* lds = reinterpret_cast<float*>(arena);
     __shared__ float lds_m[4][G], lds_l[4][G];
-    __shared__ __attribute__((aligned(16))) KVT sKn[HD], sVn[HD];  // fused KV write: the new row
+    __shared__ __attribute__((aligned(16))) KVT sKn[KVW ? HD : 8], sVn[KVW ? HD : 8];  // KVW: the new row
     __shared__ float kv_red[2 * (HD / 128)];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -279,7 +282,7 @@ void decode_kernel(DecodeArgs a) {
     int ci, kh, b;
     SplitPlan sp;
     size_t slot;  // partial slot of this workgroup
-    if (a.list_target > 0) {
+    if constexpr (LIST) {
         int act0;
         const int chunk = list_chunk(a, act0);
         const ListUnit u = list_unit(a, chunk, act0, blockIdx.x);
@@ -336,7 +339,7 @@ void decode_kernel(DecodeArgs a) {
     // k/v loads go out before the first block's, the row is prepared with the q prologue
     constexpr int HALF = HD / 2;
     const int p_new = sp.hi - 1;
-    const bool owns_new = a.k_new != nullptr && p_new >= k0 && p_new < k1;  // workgroup-uniform
+    const bool owns_new = KVW && p_new >= k0 && p_new < k1;  // workgroup-uniform
     float nk0 = 0.0f, nk1 = 0.0f, nv0 = 0.0f, nv1 = 0.0f;
     if (owns_new && tid < HALF) {
         const size_t ro = ((size_t)b * a.n_kv_heads + kh) * HD;
@@ -720,17 +723,22 @@ static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_key_len) {
 
 typedef void (*decode_fn)(DecodeArgs);
 
+template <int HD, int G, typename KVT>
+static decode_fn pick_mode(bool list, bool kvw) {
+    if (list) return kvw ? decode_kernel<HD, G, KVT, true, true> : decode_kernel<HD, G, KVT, true, false>;
+    return kvw ? decode_kernel<HD, G, KVT, false, true> : decode_kernel<HD, G, KVT, false, false>;
+}
 template <int HD, int G>
-static decode_fn pick_kv(bool f32) {
-    return f32 ? decode_kernel<HD, G, float> : decode_kernel<HD, G, half_t>;
+static decode_fn pick_kv(bool f32, bool list, bool kvw) {
+    return f32 ? pick_mode<HD, G, float>(list, kvw) : pick_mode<HD, G, half_t>(list, kvw);
 }
 template <int HD>
-static decode_fn pick_g(int G, bool f32) {
+static decode_fn pick_g(int G, bool f32, bool list, bool kvw) {
     switch (G) {
-        case 1: return pick_kv<HD, 1>(f32);
-        case 2: return pick_kv<HD, 2>(f32);
-        case 4: return pick_kv<HD, 4>(f32);
-        case 8: return pick_kv<HD, 8>(f32);
+        case 1: return pick_kv<HD, 1>(f32, list, kvw);
+        case 2: return pick_kv<HD, 2>(f32, list, kvw);
+        case 4: return pick_kv<HD, 4>(f32, list, kvw);
+        case 8: return pick_kv<HD, 8>(f32, list, kvw);
     }
     return nullptr;
 }
@@ -872,7 +880,8 @@ static int decode_impl(const g4a_cfg* cfg, int n_seq, int max_key_len, const int
     a.k_in_q = kvn ? kvn->k_in_q : 0.0f;
     a.v_in_q = kvn ? kvn->v_in_q : 0.0f;
     a.v_norm = (cfg->flags & G4A_NO_V_NORM) ? 0 : 1;
-    decode_fn fn = HD == 256 ? pick_g<256>(G, f32) : pick_g<512>(G, f32);
+    const bool list = lp.grid > 0, kvw = kvn != nullptr;
+    decode_fn fn = HD == 256 ? pick_g<256>(G, f32, list, kvw) : pick_g<512>(G, f32, list, kvw);
     if (!fn) {
         set_error("no decode kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
