@@ -329,6 +329,8 @@ def main():
                     help="only run a known-size copy kernel (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config 3 prefill rows (for profiling the prefill kernel)")
+    ap.add_argument("--prefill-seq", type=int, default=1024,
+                    help="prompt length of the --prefill-only rows (1024 = config 3, 8192 = config 5's layer)")
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config 4 batched decode row (for profiling its kernels)")
     args = ap.parse_args()
@@ -347,8 +349,9 @@ def main():
     gen = torch.Generator(device="cuda").manual_seed(2024)
     if args.prefill_only:
         out = {}
-        for tag, win, th in (("prefill_3g", 0, 1e6), ("prefill_3s", 512, 1e4)):
-            msp, fl = prefill_case(sa, 1024, win, th, args.steps, args.warmup, gen)
+        cfgn = "3" if args.prefill_seq == 1024 else f"S{args.prefill_seq}"
+        for tag, win, th in ((f"prefill_{cfgn}g", 0, 1e6), (f"prefill_{cfgn}s", 512, 1e4)):
+            msp, fl = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen)
             out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
         print(json.dumps(out), flush=True)
         return

@@ -39,12 +39,21 @@ struct PrefillArgs {
     // otherwise a workgroup covers at most split_tiles key tiles of its query block and
     // blocks with more tiles leave partials for prefill_merge_kernel
     int split_tiles, max_pieces, pieces_per_head;
+    int xcd_runs;  // prefill_kernel_w32 unsplit: 1-D grid, query blocks in contiguous runs per XCD
     const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
     half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
                       // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
     float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
 };
 
+// LDS operand reads issued ahead of their MFMAs in prefill_kernel_w32: score product
+// (one K read per MFMA) and P.V product (two transposed V reads per MFMA)
+#ifndef G4A_QK_AHEAD
+#define G4A_QK_AHEAD 4
+#endif
+#ifndef G4A_PV_AHEAD
+#define G4A_PV_AHEAD 3
+#endif
 #ifndef G4A_PREFILL_KT256
 #define G4A_PREFILL_KT256 64
 #endif
@@ -282,6 +291,14 @@ __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
 
 __device__ __forceinline__ int vswz(int r) { return (0x6CA0 >> (4 * (r & 3))) & 15; }
 
+// Position of workgroup L in a work list cut into 8 contiguous runs, one per XCD (the
+// dispatcher deals workgroup L to XCD L % 8): XCDs x < r take `per` items, the rest per - 1.
+__device__ __forceinline__ int xcd_run_index() {
+    const int N = gridDim.x, L = blockIdx.x, x = L % 8, slot = L / 8;
+    const int per = (N + 7) / 8, r = N - 8 * (per - 1);
+    return x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
+}
+
 template <int G, typename OUTT>
 __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
@@ -311,10 +328,16 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     // division each, in parallel) and a prefix sum over the wave finds the block holding
     // piece i; a scalar loop over the blocks would cost microseconds of issue slots.
     int qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
+    if (a.xcd_runs) {
+        // sliding window, unsplit: a 1-D grid over (kv head, query block) in contiguous runs
+        // per XCD, so neighbouring blocks -- which share most of their window's K/V tiles --
+        // run on one L2 at the same time
+        const int v = xcd_run_index();
+        kh = v / a.n_qblocks;
+        qb = v - kh * a.n_qblocks;
+    }
     if (a.split_tiles > 0) {
-        const int N = gridDim.x, L = blockIdx.x, x = L % 8, slot = L / 8;
-        const int per = (N + 7) / 8, r = N - 8 * (per - 1);  // XCDs x < r take per workgroups, the rest per - 1
-        const int v = x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
+        const int v = xcd_run_index();
         kh = v / a.pieces_per_head;
         const int i = v - kh * a.pieces_per_head;
         int base = 0;  // pieces of the blocks before this group of 64
@@ -572,14 +595,14 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
                 sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
             }
         }
-        // keep 4 LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        // keep G4A_QK_AHEAD LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
+        __builtin_amdgcn_sched_group_barrier(0x100, G4A_QK_AHEAD, 0);
 #pragma unroll
-        for (int i = 0; i < 28; ++i) {
+        for (int i = 0; i < 32 - G4A_QK_AHEAD; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, G4A_QK_AHEAD, 0);
 
         // scores of this lane: key kb + 4h + 32kt + 8(r/4) + r%4 of its column, log2 domain;
         // tiles inside every column's range skip the per-element mask
@@ -642,14 +665,14 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) oacc[dt] = mfma32(av[dt], pb[u], oacc[dt]);
         }
-        // transposed V reads kept ahead of the P.V MFMAs, two reads per MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+        // transposed V reads kept G4A_PV_AHEAD MFMAs ahead of the P.V MFMAs, two reads per MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * G4A_PV_AHEAD, 0);
 #pragma unroll
-        for (int i = 0; i < 29; ++i) {
+        for (int i = 0; i < 32 - G4A_PV_AHEAD; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, G4A_PV_AHEAD, 0);
     }
 
     // ---- epilogue: column sum over both halves, normalise, srq, store 4 dims at a time
@@ -937,7 +960,10 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
         a.q16 = q16;
     }
-    const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads) : dim3(a.n_qblocks, cfg->n_kv_heads);
+    a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0 && getenv_flag("G4A_PREFILL_XCD_RUNS") >= 0;
+    const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
+                      : a.xcd_runs      ? dim3(a.n_qblocks * cfg->n_kv_heads)
+                                        : dim3(a.n_qblocks, cfg->n_kv_heads);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
