@@ -828,6 +828,10 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     p.n_qblocks = (S + BQ - 1) / BQ;
     const int mode = getenv_flag("G4A_PREFILL_SPLIT_TILES");
     if (mode < 0 || (mode == 0 && (long)p.n_qblocks * kvH >= 512)) return p;
+    // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
+    // preparation and merge only while the unsplit grid leaves most CUs idle (S 2048,
+    // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27)
+    if (mode == 0 && W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
     long total = 0;
     int max_tiles = 0;
     for (int qb = 0; qb < p.n_qblocks; ++qb) {
