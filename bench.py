@@ -7,7 +7,8 @@ attention, nH 8 / kvH 2, hd 256, KV length 4096, f16 cache, in GB/s of K+V bytes
 attended (8,388,608 B per call). A step is one decode call; the timed region
 replays a HIP graph of K calls that rotate over 64 distinct KV caches (512 MiB, more
 than the 256 MiB Infinity Cache), so every call streams its cache from HBM.
-`secondary` carries the other BASELINE rows: config 2 sliding (W 512), config 3
+`secondary` carries the other BASELINE rows: config 1 on the GPU (f32 caches, 256
+rotated), config 2 sliding (W 512), config 3
 prefill (S 1024, global and W 512, TFLOP/s of 4*hd*nH*attended-pairs), config 4
 (16 sequences, KV ~ U[1024, 32768]), the q/k/v producer in front of the path (decode
 4-bit GEMV at the config-2 layer shape, prefill projection GEMMs at config 3) and the
@@ -104,6 +105,23 @@ def decode_case(sa, T, window, theta, steps, warmup, n_caches, gen):
     attended = min(T, window) if window else T
     nbytes = 2 * attended * KVH * HD * 2
     return ms, nbytes, (q, qg, cos, sin, caches[0], cfg)
+
+
+def config1_case(sa, steps, warmup, gen, n_caches=256):
+    """BASELINE config 1 on the GPU: nH 4 / kvH 1, hd 256, T 1024, f32 caches (the
+    reference's own cache type), scale 1/16, no norms or RoPE; n_caches rotated 2 MiB caches
+    (512 MiB, beyond the MALL)."""
+    T, nh, kvh, hd = 1024, 4, 1, 256
+    caches = [(torch.randn(T, kvh, hd, device="cuda", generator=gen),
+               torch.randn(T, kvh, hd, device="cuda", generator=gen)) for _ in range(n_caches)]
+    q = torch.randn(nh, hd, device="cuda", generator=gen)
+    kl = torch.tensor([T], dtype=torch.int32, device="cuda")
+    cfg = sa.AttnConfig(nh, kvh, hd, 0, 1.0 / 16)
+    ws = sa.DecodeWorkspace("cuda")
+    out = torch.empty(1, nh, hd, device="cuda")
+    fns = [lambda kc=kc, vc=vc: sa.decode(q, kc, vc, kl, cfg, out=out, workspace=ws) for kc, vc in caches]
+    ms = graph_time_ms(fns, steps, warmup)
+    return ms, 2 * T * kvh * hd * 4
 
 
 def prefill_case(sa, S, window, theta, steps, warmup, gen):
@@ -377,6 +395,10 @@ def main():
     if not args.only_headline:
         sec = {}
         ms2, nb2, _ = decode_case(sa, 4096, 512, 1e4, args.steps, args.warmup, 64, gen)
+        ms1, nb1 = config1_case(sa, args.steps, args.warmup, gen)
+        sec["decode_1"] = {"us_per_call": round(ms1 * 1e3, 3), "GB/s": round(nb1 / ms1 / 1e6, 2),
+                           "hbm_frac": round(nb1 / ms1 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb1,
+                           "note": "config 1 on the GPU: f32 caches, nH 4/kvH 1, T 1024, scale 1/16"}
         sec["decode_2s"] = {"us_per_call": round(ms2 * 1e3, 3), "GB/s": round(nb2 / ms2 / 1e6, 2),
                             "hbm_frac": round(nb2 / ms2 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb2}
         for tag, win, th in (("prefill_3g", 0, 1e6), ("prefill_3s", 512, 1e4)):
