@@ -74,8 +74,11 @@ int g4a_version(void);
  *   key_len[s]  int32, device: keys of sequence s (params[1] keyLen); the query
  *               sits at position key_len[s]-1 (params[2] qOffset = pos).
  *               Sequence s attends keys [max(0, key_len-W), key_len) (W = window, 0 = all).
- *   max_key_len host upper bound of key_len[]; sizes the split-KV grid only (a tight
- *               bound gives the best split).
+ *               NULL: every sequence has exactly max_key_len keys, known on the host as
+ *               the reference's params are (runner.py:290); the kernel then reads no
+ *               length from memory before its first K/V loads.
+ *   max_key_len host upper bound of key_len[] (the exact length when key_len is NULL);
+ *               sizes the split-KV grid (a tight bound gives the best split).
  *   q           f32 [n_seq][n_q_heads][head_dim], raw: RMSNorm*q_gain then RoPE
  *               are applied in the kernel as attn_101 does (kernels_dsl.py:1593-1615).
  *   q_gain      f32 [head_dim] or NULL (no q RMSNorm).

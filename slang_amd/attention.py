@@ -137,12 +137,23 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
     _need(rope_sin, "rope_sin", torch.float32)
     if not torch.is_tensor(key_len):
         kl = np.atleast_1d(np.asarray(key_len, np.int32))
-        if max_key_len is None and kl.size:
-            max_key_len = int(kl.max())   # exact bound: lets a single sequence start loading early
-        key_len = torch.tensor(kl, device=q.device)
-    _need(key_len, "key_len", torch.int32)
-    if key_len.numel() != n_seq:
-        raise ValueError("key_len must have one entry per sequence")
+        if kl.size != n_seq:
+            raise ValueError("key_len must have one entry per sequence")
+        if kl.size and kl.min() == kl.max() and kl[0] > 0:
+            # one host-known length (a batch-1 decode step): no device array, the kernel
+            # takes the length from max_key_len and starts loading without a memory read
+            if not int(kl[0]) <= kc.shape[1]:
+                raise ValueError("key_len beyond the cache length")
+            max_key_len = int(kl[0])
+            key_len = None
+        else:
+            if max_key_len is None and kl.size:
+                max_key_len = int(kl.max())   # exact bound
+            key_len = torch.tensor(kl, device=q.device)
+    if key_len is not None:
+        _need(key_len, "key_len", torch.int32)
+        if key_len.numel() != n_seq:
+            raise ValueError("key_len must have one entry per sequence")
     if max_key_len is None:
         max_key_len = kc.shape[1]
     if not 0 < max_key_len <= kc.shape[1]:

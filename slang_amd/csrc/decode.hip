@@ -57,6 +57,7 @@ struct DecodeArgs {
     // work list (several sequences): list_target > 0 spreads all active keys over about
     // list_target units of equal length (>= chunk keys, <= chunk_cap), one workgroup each
     int n_seq, list_target, chunk_cap, list_units;  // list_units: the grid, units past it never run
+    int fixed_len;  // key_len == NULL: every sequence has fixed_len keys (no device read)
     // fused KV write (g4a_decode_kv): k_new != NULL gives each sequence's raw k/v row
     // [n_seq][kvH][HD] for position key_len - 1, prepared and stored by the workgroup
     // whose split holds that key
@@ -148,6 +149,10 @@ __device__ __forceinline__ float dpp_row_shl(float x) {
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + N, 0xF, 0xF, false));
 }
 
+// keys of sequence s: from the device array, or the host-given length when there is none
+// (a batch-1 decode knows its position on the host, as the reference's params do)
+__device__ __forceinline__ int seq_len(const DecodeArgs& a, int s) { return a.key_len ? a.key_len[s] : a.fixed_len; }
+
 // Keys attended by sequence b and how they are split: active keys [lo, hi), split c covers
 // [lo + c*chunk, min(lo + (c+1)*chunk, hi)); split c is live when c*chunk < hi - lo. No
 // division on the common path: the host's chunk fits max_splits splits of max_key_len keys;
@@ -157,7 +162,7 @@ struct SplitPlan {
 };
 __device__ __forceinline__ SplitPlan split_plan(const DecodeArgs& a, int b) {
     SplitPlan p;
-    p.hi = a.key_len[b];
+    p.hi = seq_len(a, b);
     p.lo = (a.window > 0 && p.hi > a.window) ? p.hi - a.window : 0;
     p.active = p.hi - p.lo;
     p.chunk = a.chunk;
@@ -188,7 +193,7 @@ __device__ __forceinline__ int list_chunk(const DecodeArgs& a, int& act0) {
     act0 = 0;
     for (int s0 = 0; s0 < a.n_seq; s0 += 64) {
         const int s = s0 + lane;
-        const int act = s < a.n_seq ? active_keys(a, a.key_len[s]) : 0;
+        const int act = s < a.n_seq ? active_keys(a, seq_len(a, s)) : 0;
         if (s0 == 0) act0 = act;
         tot += (unsigned)act;
     }
@@ -203,7 +208,7 @@ __device__ __forceinline__ int list_chunk(const DecodeArgs& a, int& act0) {
 
 __device__ __forceinline__ int list_active(const DecodeArgs& a, int s0, int act0, int n) {
     const int s = s0 + (threadIdx.x & 63);
-    return s0 == 0 ? (s < n ? act0 : 0) : (s < n ? active_keys(a, a.key_len[s]) : 0);
+    return s0 == 0 ? (s < n ? act0 : 0) : (s < n ? active_keys(a, seq_len(a, s)) : 0);
 }
 
 struct ListUnit {
@@ -231,7 +236,7 @@ __device__ __forceinline__ int list_first(const DecodeArgs& a, int chunk, int ac
     int base = 0;
     for (int s0 = 0; s0 < b; s0 += 64)
         base += __builtin_amdgcn_readlane(wave_prefix_sum(ceil_div(list_active(a, s0, act0, b), chunk)), 63);
-    const int act_b = b < 64 ? __builtin_amdgcn_readlane(act0, b) : active_keys(a, a.key_len[b]);
+    const int act_b = b < 64 ? __builtin_amdgcn_readlane(act0, b) : active_keys(a, seq_len(a, b));
     splits = __builtin_amdgcn_readfirstlane(ceil_div(act_b, chunk));
     return base * a.n_kv_heads;
 }
@@ -288,7 +293,7 @@ void decode_kernel(DecodeArgs a) {
         const ListUnit u = list_unit(a, chunk, act0, blockIdx.x);
         if (u.b < 0) return;  // past the last unit
         b = u.b, kh = u.kh, ci = u.ci;
-        sp.hi = a.key_len[b];
+        sp.hi = seq_len(a, b);
         sp.lo = (a.window > 0 && sp.hi > a.window) ? sp.hi - a.window : 0;
         sp.active = sp.hi - sp.lo;
         sp.chunk = chunk;
@@ -794,8 +799,8 @@ static int decode_impl(const g4a_cfg* cfg, int n_seq, int max_key_len, const int
         set_error("n_seq (%d) and max_key_len (%d) must be positive", n_seq, max_key_len);
         return G4A_EINVAL;
     }
-    if (!key_len || !q || !k_cache || !v_cache || !out) {
-        set_error("key_len, q, k_cache, v_cache and out must be non-NULL");
+    if (!q || !k_cache || !v_cache || !out) {
+        set_error("q, k_cache, v_cache and out must be non-NULL");
         return G4A_EINVAL;
     }
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) {
@@ -832,6 +837,7 @@ static int decode_impl(const g4a_cfg* cfg, int n_seq, int max_key_len, const int
     }
     DecodeArgs a;
     a.key_len = key_len;
+    a.fixed_len = max_key_len;
     a.q = q;
     a.q_gain = q_gain;
     a.rcos = rope_cos;

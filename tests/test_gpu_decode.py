@@ -341,3 +341,29 @@ def test_decode_kv_matches_kv_write_then_decode(B, nH, kvH, hd, window, cache, k
         ref = O.decode_attention(qn[b], kn[b, :L], vn[b, :L], L, kvH, q_gain=qg.cpu().numpy(), cos=cn[b],
                                  sin=sn[b], window=window)
         contract_close(got[b], ref, f"seq {b} len {L}")
+
+
+@pytest.mark.parametrize("B,window,fused", [(1, 0, False), (1, 512, False), (4, 0, False), (1, 0, True)])
+def test_host_key_len_matches_device_key_len(B, window, fused):
+    """A host-given length (key_len NULL at the C ABI, max_key_len exact) and the same length
+    in a device array give bit-identical outputs (and cache rows, with the fused KV write)."""
+    rng = np.random.default_rng(31 + B + window)
+    T, nH, kvH, hd = 2049, 8, 2, 256
+    q = t(rng.standard_normal((B, nH, hd)).astype(np.float32))
+    qg = t((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    c, s = O.rope_tables([T - 1] * B, hd, 1e4)
+    c, s = t(c), t(s)
+    k = torch.from_numpy(rng.standard_normal((B, T + 7, kvH, hd)).astype(np.float16)).to(DEV)
+    v = torch.from_numpy(rng.standard_normal((B, T + 7, kvH, hd)).astype(np.float16)).to(DEV)
+    cfg = sa.AttnConfig(nH, kvH, hd, window)
+    kw = dict(q_gain=qg, rope_cos=c, rope_sin=s)
+    if fused:
+        kw.update(k_new=t(rng.standard_normal((B, kvH, hd)).astype(np.float32)),
+                  v_new=t(rng.standard_normal((B, kvH, hd)).astype(np.float32)), k_gain=qg)
+    k1, v1, k2, v2 = k.clone(), v.clone(), k.clone(), v.clone()
+    dev_len = torch.full((B,), T, dtype=torch.int32, device=DEV)
+    a = sa.decode(q, k1, v1, dev_len, cfg, max_key_len=T, **kw)  # the same split plan
+    b = sa.decode(q, k2, v2, [T] * B, cfg, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
