@@ -108,14 +108,14 @@ struct KOp;
 template <>
 struct KOp<half_t> {
     struct raw { half8 h; };
-    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_h8(r, off)}; }
+    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_h8_nt(r, off)}; }
     static __device__ __forceinline__ raw lds(const half_t* p) { return raw{*reinterpret_cast<const half8*>(p)}; }
     static __device__ __forceinline__ float4v dot(const raw& k, half8 q, float4v c) { return mfma16x32(k.h, q, c); }
 };
 template <>
 struct KOp<float> {
     struct raw { float8v f; };
-    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_f8(r, off)}; }
+    static __device__ __forceinline__ raw load(rsrc_t r, int off) { return raw{bload_f8_nt(r, off)}; }
     static __device__ __forceinline__ raw lds(const float* p) {
         const float4v a = *reinterpret_cast<const float4v*>(p), b = *reinterpret_cast<const float4v*>(p + 4);
         return raw{float8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}};
@@ -132,13 +132,13 @@ struct VOp;
 template <>
 struct VOp<half_t> {
     typedef half8 raw;
-    static __device__ __forceinline__ half8 load(rsrc_t r, int off) { return bload_h8(r, off); }
+    static __device__ __forceinline__ half8 load(rsrc_t r, int off) { return bload_h8_nt(r, off); }
     static __device__ __forceinline__ half8 h(half8 v) { return v; }
 };
 template <>
 struct VOp<float> {
     typedef float8v raw;
-    static __device__ __forceinline__ float8v load(rsrc_t r, int off) { return bload_f8(r, off); }
+    static __device__ __forceinline__ float8v load(rsrc_t r, int off) { return bload_f8_nt(r, off); }
     static __device__ __forceinline__ half8 h(float8v v) { return __builtin_convertvector(v, half8); }
 };
 

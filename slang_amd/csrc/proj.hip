@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
         for (int j = 0; j < NJ; ++j) {
             const int c = lane + 64 * j;  // chunk of the row; past the row end reads zeros
             const int off = c < row_bytes / 16 ? (r0 + r) * row_bytes + 16 * c : 0x7fffffff;
-            wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+            wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kCpolNT);  // read once: non-temporal
         }
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
