@@ -58,6 +58,7 @@ struct DecodeArgs {
     // list_target units of equal length (>= chunk keys, <= chunk_cap), one workgroup each
     int n_seq, list_target, chunk_cap, list_units;  // list_units: the grid, units past it never run
     int fixed_len;  // key_len == NULL: every sequence has fixed_len keys (no device read)
+    int2* list_tab;  // work list: (first unit, splits) per (sequence, kv head), written by split 0
     // fused KV write (g4a_decode_kv): k_new != NULL gives each sequence's raw k/v row
     // [n_seq][kvH][HD] for position key_len - 1, prepared and stored by the workgroup
     // whose split holds that key
@@ -231,16 +232,6 @@ __device__ __forceinline__ ListUnit list_unit(const DecodeArgs& a, int chunk, in
     }
     return ListUnit{-1, 0, 0, 0};
 }
-// first unit of sequence b and its splits per kv head
-__device__ __forceinline__ int list_first(const DecodeArgs& a, int chunk, int act0, int b, int& splits) {
-    int base = 0;
-    for (int s0 = 0; s0 < b; s0 += 64)
-        base += __builtin_amdgcn_readlane(wave_prefix_sum(ceil_div(list_active(a, s0, act0, b), chunk)), 63);
-    const int act_b = b < 64 ? __builtin_amdgcn_readlane(act0, b) : active_keys(a, seq_len(a, b));
-    splits = __builtin_amdgcn_readfirstlane(ceil_div(act_b, chunk));
-    return base * a.n_kv_heads;
-}
-
 // QP consecutive f32 (QP = 2 or 4) from a buffer
 template <int QP>
 __device__ __forceinline__ void bload_q(rsrc_t r, int off, float (&x)[QP]) {
@@ -293,6 +284,9 @@ void decode_kernel(DecodeArgs a) {
         const ListUnit u = list_unit(a, chunk, act0, blockIdx.x);
         if (u.b < 0) return;  // past the last unit
         b = u.b, kh = u.kh, ci = u.ci;
+        // split 0 of each (sequence, kv head) tells the merge where its units are, so the
+        // merge needs no plan of its own (a pair without keys has no unit and no entry)
+        if (ci == 0 && tid == 0) a.list_tab[b * a.n_kv_heads + kh] = make_int2((int)blockIdx.x, u.splits);
         sp.hi = seq_len(a, b);
         sp.lo = (a.window > 0 && sp.hi > a.window) ? sp.hi - a.window : 0;
         sp.active = sp.hi - sp.lo;
@@ -598,9 +592,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 }
 
 // The same merge over a work list: the splits of (sequence b, kv head kh) are the units
-// [first, first + splits) of the plan, every one written by this call. Thread (sg, dim e)
-// folds splits sg, sg+4, .. into a running (m, l, o) eight loads at a time; the four
-// split groups are combined through LDS.
+// [first, first + splits) that split 0 of the pair recorded in list_tab, every one written
+// by this call. Thread (sg, dim e) folds splits sg, sg+4, .. into a running (m, l, o) eight
+// loads at a time (read once: non-temporal); the four split groups are combined through LDS.
 template <int HD, int G>
 __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
     constexpr int E = G * HD;
@@ -608,9 +602,12 @@ __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, sg = tid >> 6;
     const int e = blockIdx.x * 64 + lane, hh = (blockIdx.x * 64) / HD;
     const int kh = blockIdx.y, b = blockIdx.z;
-    int act0, splits;
-    const int chunk = list_chunk(a, act0);
-    const int u0 = list_first(a, chunk, act0, b, splits) + kh * splits;
+    // the units of this pair, from split 0's entry; a sequence without keys has none (and
+    // its entry is whatever an earlier call left)
+    const int2 ent = a.list_tab[b * a.n_kv_heads + kh];
+    const bool has_keys = active_keys(a, seq_len(a, b)) > 0;
+    const int u0 = ent.x;
+    int splits = has_keys ? ent.y : 0;
     // only with a chunk held at chunk_cap could units fall past the grid (key lengths no
     // cache in device memory can hold): their slots were never written
     if (u0 + splits > a.list_units) splits = max(0, a.list_units - u0);
@@ -622,8 +619,10 @@ __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
         for (int j = 0; j < 8; ++j) {
             const int s = s0 + 4 * j;
             const size_t u = (size_t)u0 + (s < splits ? s : s0);
-            ml[j] = a.part_ml[u * G + hh];
-            o[j] = a.part_o[u * E + e];
+            typedef float f2v __attribute__((ext_vector_type(2)));
+            const f2v mlv = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(&a.part_ml[u * G + hh]));
+            ml[j] = make_float2(mlv[0], mlv[1]);
+            o[j] = __builtin_nontemporal_load(&a.part_o[u * E + e]);
             if (s >= splits) ml[j].x = kNegInf;
         }
         float bm = M;
@@ -709,7 +708,7 @@ static ListPlan list_plan(const g4a_cfg* cfg, int n_seq, int max_key_len) {
 }
 
 struct WsLayout {
-    size_t ml, o, total;
+    size_t ml, o, tab, total;
 };
 
 // partial slots: max_splits per pair, or one per work-list unit
@@ -722,7 +721,8 @@ static WsLayout ws_layout(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     WsLayout L;
     L.ml = 0;
     L.o = L.ml + al(slots * G * sizeof(float2));
-    L.total = L.o + slots * G * cfg->head_dim * sizeof(float);
+    L.tab = L.o + al(slots * G * cfg->head_dim * sizeof(float));
+    L.total = L.tab + (lp.grid > 0 ? (size_t)n_seq * cfg->n_kv_heads * sizeof(int2) : 0);
     return L;
 }
 
@@ -849,6 +849,7 @@ static int decode_impl(const g4a_cfg* cfg, int n_seq, int max_key_len, const int
     char* w = (char*)ws;
     a.part_ml = (float2*)(w + L.ml);
     a.part_o = (float*)(w + L.o);
+    a.list_tab = (int2*)(w + L.tab);
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
