@@ -594,7 +594,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 // The same merge over a work list: the splits of (sequence b, kv head kh) are the units
 // [first, first + splits) that split 0 of the pair recorded in list_tab, every one written
 // by this call. Thread (sg, dim e) folds splits sg, sg+4, .. into a running (m, l, o) eight
-// loads at a time (read once: non-temporal); the four split groups are combined through LDS.
+// loads at a time; the four split groups are combined through LDS. (The partials were just
+// written from other XCDs: non-temporal loads of them measured slower.)
 template <int HD, int G>
 __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
     constexpr int E = G * HD;
@@ -619,10 +620,8 @@ __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
         for (int j = 0; j < 8; ++j) {
             const int s = s0 + 4 * j;
             const size_t u = (size_t)u0 + (s < splits ? s : s0);
-            typedef float f2v __attribute__((ext_vector_type(2)));
-            const f2v mlv = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(&a.part_ml[u * G + hh]));
-            ml[j] = make_float2(mlv[0], mlv[1]);
-            o[j] = __builtin_nontemporal_load(&a.part_o[u * E + e]);
+            ml[j] = a.part_ml[u * G + hh];
+            o[j] = a.part_o[u * E + e];
             if (s >= splits) ml[j].x = kNegInf;
         }
         float bm = M;
