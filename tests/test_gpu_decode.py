@@ -156,6 +156,7 @@ def test_ragged_batch_with_window():
     (80, 8, 2, 256, np.float16, 96),
     (70, 4, 1, 512, np.float16, 0),     # hd 512: one resident workgroup per CU
     (67, 4, 2, 256, np.float32, 0),     # f32 caches
+    (300, 8, 2, 256, np.float16, 0),    # more pairs than resident workgroups: the grid grows
 ])
 def test_work_list_many_ragged_sequences(B, nH, kvH, hd, kv_dtype, window):
     """Several sequences run as one work list of equal-length units over all of them
