@@ -219,6 +219,60 @@ typedef struct {
  */
 int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream);
 
+/*
+ * ---- The rest of a decode step: the decoder layer around the attention block ---------
+ * One token's layer (gemma4_150/reference.py:141-191) is, with x f32 [H]:
+ *   a = srq(rms(x, in_norm), qkv_in)        g4a_rms_norm (out2, sum2)     rmssrq_69
+ *   q/k/v, KV write, attention              g4a_qkv_gemv, g4a_decode_kv   qkv_70, kvnorm, attn_101
+ *   x = x + rms(qlin(attn, o), post_attn)   g4a_qgemv, g4a_rms_norm       oproj_73
+ *   y2 = f16(srq(f16(rms(x, pre_ffn)), gate_in))  g4a_rms_norm (f16_2)
+ *   x = x + rms(qlin(srq(gelu(qlin(y2, gate)) * qlin(y2, up), down_in), down), post_ffn)
+ *                                           g4a_qgemv, g4a_geglu          gateup_74/95, down_75/96
+ *   x = (x + rms(ilin(gelu(ilin(x, plegate)) * ple_in[L], pleproj), post_ple)) * layer_scalar
+ *                                           g4a_qgemv (8-bit), g4a_geglu  plegate_76, pleproj_77
+ * and around the layers (reference.py:114-139, 193-207): the token and per-layer
+ * embedding rows (g4a_embed; embed_00, plegather_01), the per-layer-input projection
+ * (g4a_gemv_f16 + g4a_rms_norm), the final norm, the 2-bit lm_head (g4a_qgemv) and the
+ * softcap + greedy argmax (g4a_softcap_argmax; logits_33, argmax1_34/argmax2_35).
+ */
+/*
+ * Quantised GEMV: out[o] = srq(w_scale[o] * sum_i (q[o][i] - 2^(bits-1)) * srq(x[i], in_q), out_q)
+ * (reference.py:96-101 _qlin; :103-111 _ilin_raw is the bits = 8 case over export.py's
+ * biased codes, :150-156; :200-206 the lm_head with in_q = out_q = 0). Rows are packed as
+ * for g4a_dequant; bits 2, 4 or 8; n_in a multiple of 128/bits. x f32 [n_in], 16-byte
+ * aligned; out f32 [n_out].
+ */
+int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
+              const float* w_scale, float out_q, float* out, void* stream);
+/* Dense f16 GEMV: out[o] = sum_i w[o][i] x[i] in f32 (the per-layer-input projection,
+ * reference.py:136, exported f16 by export.py:95). n_in a multiple of 8. */
+int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* out, void* stream);
+/*
+ * RMSNorm family over n_rows rows of n values (reference.py:38-43 and the sandwich adds
+ * of :170, :183, :191; :133-139 for the per-layer-input context):
+ *   y = x' / sqrt(mean(x'^2) + eps) * w (w NULL: no gain), x' = x * pre
+ *   out = (res + y) * mult (res NULL: 0)
+ *   out2 = srq(out, q2), or with f16_2 f16(srq(f16(out), q2)) (reference.py:153-156);
+ *   sum2[row] = sum of out2 (qkv_70's sum_a). out2 and sum2 may be NULL.
+ * out may alias x or res.
+ */
+int g4a_rms_norm(int n_rows, int n, const float* x, float pre, const float* w, const float* res,
+                 float mult, float eps, float* out, float q2, int f16_2, float* out2, float* sum2,
+                 void* stream);
+/* out[i] = srq(gelu_tanh(a[i]) * b[i], out_q) (reference.py:34-35, :181, :188). */
+int g4a_geglu(int n, const float* a, const float* b, float out_q, float* out, void* stream);
+/*
+ * Embedding row of the token id tok[0] (device memory, so a step can take the previous
+ * step's argmax): out[j] = mult * row_scale[tok * (n/group) + j/group] * (code_j - 2^(bits-1))
+ * from row tok of a packed table of n_rows rows (reference.py:114-121 embed: 2-bit, group
+ * n; :123-131 ple_table: 4-bit, group ple_d). An id outside [0, n_rows) gives zeros.
+ */
+int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok,
+              const float* row_scale, int group, float mult, float* out, void* stream);
+/* logits <- cap * tanh(logits / cap) in place (cap 0: unchanged) and tok[0] = the first
+ * index of the maximum (reference.py:207; runner.py:501-505 argmax on the GPU). */
+int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,159 @@
+"""CPU oracle for the decode step around the attention block (one token, every layer).
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product package (slang_amd/) imports
+this module. It may be imported only by tests/, by __graft_entry__.smoke() and
+by bench.py's cpu_baseline leg, and there only as the checker, never as a
+fallback for the GPU path.
+
+It restates gemma4_150/reference.py's ReferenceSRQ over the exported model format
+(export.py:64-181) instead of the checkpoint:
+
+  * gelu_tanh ........................................ reference.py:34-35
+  * rms_norm (x / sqrt(mean(x^2) + eps) * w) .......... reference.py:38-43
+  * _qlin: srq(W @ srq(x, in_s), out_s), W = (q - 2^(bits-1)) * row_scale
+                                                       reference.py:96-101
+  * _ilin_raw: the same with int8 rows; export.py:150-156 stores them biased by 128,
+    which is the bits = 8 zero point ............... reference.py:103-111
+  * embed (2-bit row * scale[tok] * sqrt(H)) ......... reference.py:114-121
+  * ple_table (4-bit row, one scale per layer slice)  reference.py:123-131
+  * ple_input ((rms(P x * H^-1/2, w) + ple) / sqrt 2)  reference.py:133-139
+  * layer (sandwich norms, MLP with the f16 input rounding of :176-178, PLE block)
+                                                       reference.py:141-191
+  * forward's tail (final norm, 2-bit lm_head, softcap)  reference.py:193-207
+  * lm_head rows from export.py's blocked [24][vocab][4] words  export.py:91-93
+
+The attention block itself is oracle.attention's (q/k/v from oracle.projection).
+`post_attention` and `ple_block` return every intermediate of a layer after its
+attention; the GPU tests check each stage from the GPU's own inputs to that stage with
+the primitives above (SRQ grids make a flipped code in one stage legitimately move every
+later one).
+
+Pinning (tests/test_oracle_decoder.py): gelu_tanh against the erf form of GELU and its
+limits; rms_norm against a float64 loop and its scale invariance; qlin against a
+pure-Python triple loop over unpacked codes, and against the zero-point closed form;
+hand-packed embedding words; the lm_head block order against a row-major re-pack;
+argmax ties.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .attention import srq
+from .projection import unpack_values
+
+EPS = 1e-6
+
+
+def gelu_tanh(v):
+    """reference.py:34-35."""
+    v = np.asarray(v, np.float32)
+    return (0.5 * v * (1.0 + np.tanh(np.float32(0.7978845608028654) * (v + np.float32(0.044715) * v ** 3)))
+            ).astype(np.float32)
+
+
+def rms_norm(x, w=None, eps=EPS):
+    """reference.py:38-43 (w None: rms_norm_noscale); rows over the last axis."""
+    x = np.asarray(x, np.float32)
+    y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(eps))
+    return (y * w if w is not None else y).astype(np.float32)
+
+
+def dequant_rows(words, scale, n_in, bits):
+    """W [n_out][n_in] f32 = (q - 2^(bits-1)) * scale[o] (reference.py:99-100)."""
+    codes = unpack_values(words, n_in, bits).astype(np.float32)
+    return (codes - np.float32(1 << (bits - 1))) * np.asarray(scale, np.float32)[:, None]
+
+
+def qlin(x, words, scale, n_in, bits, in_q=0.0, out_q=0.0):
+    """reference.py:96-101 (_qlin) and :103-111 (_ilin_raw, bits 8 over biased codes)."""
+    W = dequant_rows(words, scale, n_in, bits)
+    return srq(W @ srq(np.asarray(x, np.float32), in_q), out_q).astype(np.float32)
+
+
+def embed_row(table_u8, tok, scale, n, bits, group, mult):
+    """reference.py:114-131: row tok of a packed u8 table -> mult * scale * (code - zp)."""
+    row = np.ascontiguousarray(table_u8[tok]).view(np.uint32)
+    codes = unpack_values(row.reshape(1, -1), n, bits)[0].astype(np.int64)
+    sc = np.asarray(scale, np.float32).reshape(-1)[tok * (n // group) + np.arange(n) // group]
+    return (np.float32(mult) * sc * (codes - (1 << (bits - 1))).astype(np.float32)).astype(np.float32)
+
+
+def lmhead_rows(blk_words):
+    """export.py:91-93 stores lm_head as [24][vocab][4] words; rows are [vocab][96]."""
+    blk = np.asarray(blk_words, np.uint32)
+    nb, vocab, four = blk.shape
+    return np.ascontiguousarray(blk.transpose(1, 0, 2)).reshape(vocab, nb * four)
+
+
+def softcap_argmax(logits, cap):
+    """reference.py:207 softcap, then numpy's argmax (the first maximum)."""
+    z = np.asarray(logits, np.float32)
+    if cap:
+        z = (np.float32(cap) * np.tanh(z / np.float32(cap))).astype(np.float32)
+    return z, int(np.argmax(z))
+
+
+def ple_input(man, tok, x):
+    """reference.py:123-139 for token tok and its embedding x."""
+    c = man.config
+    H, nL, d = int(c["H"]), int(c["nL"]), int(c["ple_d"])
+    ple = embed_row(man.tensor("ple_q"), tok, man.tensor("ple_scale"), nL * d, 4, d,
+                    float(c["ple_scale"])).reshape(nL, d)
+    proj = man.tensor("pl_model_proj").astype(np.float32) @ x
+    ctx = proj.reshape(nL, d) * np.float32(H ** -0.5)
+    ctx = rms_norm(ctx, man.tensor("pl_proj_norm"))
+    return ((ctx + ple) * np.float32(2.0 ** -0.5)).astype(np.float32)
+
+
+def bits_of(man, name, n_out, n_in):
+    """Bit width of a packed [n_out][n_in] matrix from its word count (export.py:59-61)."""
+    return 8 * int(man.tensors[name]["len"]) // (n_out * n_in)
+
+
+def post_attention(man, L, x, attn):
+    """The rest of layer L after its attention output attn (srq'd by o_in), stage by stage
+    (reference.py:167-191). Returns a dict of every intermediate, each from its inputs."""
+    s = man.layers[L]
+    sc, H, inter = s.scales, man.hidden, s.intermediate
+    t = lambda n: man.tensor(f"L{L}.{n}")  # noqa: E731
+    o_w12, pl = t("o_w12"), t("pleproj_w12s")
+    st = {}
+    st["o"] = qlin(attn, t("o_bits"), t("o_scale"), s.q_dim, bits_of(man, f"L{L}.o_bits", H, s.q_dim),
+                   sc["o_in"], sc["o_out"])
+    st["x1"] = (x + rms_norm(st["o"], o_w12[:H])).astype(np.float32)
+    h = rms_norm(st["x1"], o_w12[H:])
+    st["y2"] = srq(h.astype(np.float16).astype(np.float32), sc["gate_in"]).astype(np.float16).astype(np.float32)
+    gb = bits_of(man, f"L{L}.gate_bits", inter, H)
+    st["gate"] = qlin(st["y2"], t("gate_bits"), t("gate_scale"), H, gb, sc["gate_in"], sc["gate_out"])
+    st["up"] = qlin(st["y2"], t("up_bits"), t("up_scale"), H, gb, sc["up_in"], sc["up_out"])
+    st["geglu"] = srq(gelu_tanh(st["gate"]) * st["up"], sc["down_in"]).astype(np.float32)
+    st["down"] = qlin(st["geglu"], t("down_bits"), t("down_scale"), inter,
+                      bits_of(man, f"L{L}.down_bits", H, inter), sc["down_in"], sc["down_out"])
+    st["x2"] = (st["x1"] + rms_norm(st["down"], t("down_nw"))).astype(np.float32)
+    return st
+
+
+def ple_block(man, L, x2, ple_in_L, gate_out=None, g=None, proj=None):
+    """reference.py:185-191; each stage from the given previous stage when supplied."""
+    s = man.layers[L]
+    sc, H = s.scales, man.hidden
+    d = int(man.config["ple_d"])
+    t = lambda n: man.tensor(f"L{L}.{n}")  # noqa: E731
+    pl = t("pleproj_w12s")
+    st = {}
+    st["plegate"] = qlin(x2, t("plegate_codes"), t("plegate_rowscale"), H, 8, sc["plegate_in"], sc["plegate_out"])
+    st["pleg"] = (gelu_tanh(st["plegate"] if gate_out is None else gate_out) * ple_in_L).astype(np.float32)
+    st["pleproj"] = qlin(st["pleg"] if g is None else g, t("pleproj_codes"), t("pleproj_rowscale"), d, 8,
+                         sc["pleproj_in"], sc["pleproj_out"])
+    st["x3"] = ((x2 + rms_norm(st["pleproj"] if proj is None else proj, pl[:H])) * pl[2 * H]).astype(np.float32)
+    return st
+
+
+def final_logits(man, x):
+    """reference.py:200-207 (norm, 2-bit lm_head over the exported blocks, softcap)."""
+    c = man.config
+    H = man.hidden
+    xn = rms_norm(x, man.tensor("final_norm"))
+    rows = lmhead_rows(man.tensor("lmhead_blk"))
+    W = dequant_rows(rows, man.tensor("lmhead_scale"), H, 2)
+    return softcap_argmax(W @ xn, float(c["softcap"]))

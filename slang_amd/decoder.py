@@ -1,0 +1,249 @@
+"""The decode step of the whole decoder on one GPU: embedding rows, every layer (attention
+block, o_proj, MLP, per-layer-embedding block) and the greedy lm_head, over libg4attn.
+
+Reference: gemma4_150/reference.py:114-207 (ReferenceSRQ.embed / ple_input / layer /
+forward) is the arithmetic; gemma4_150/runner.py:373-505 (G4Runner.layer / forward) is
+the resident form this mirrors: weights uploaded once, the hidden state and the next
+token stay on the device, and the argmax's token feeds the next step's embedding rows
+without a host round trip.
+
+Two layers, as in attention.py:
+  * ``qgemv`` / ``gemv_f16`` / ``rms_norm`` / ``geglu`` / ``embed`` / ``softcap_argmax``
+    -- the library operations on torch tensors;
+  * ``DecoderStack`` -- the model: an ``AttentionStack`` for the attention blocks plus the
+    rest of each layer, driven by the manifest (export.py:86-181).
+
+Every call is asynchronous on torch's current stream; nothing is computed on the host.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check
+from .attention import _need, _ptr, _stream
+from .manifest import AttentionStack, Manifest, ManifestError
+from .projection import packed_bits
+
+__all__ = ["qgemv", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax", "DecoderStack", "EPS"]
+
+EPS = 1e-6  # reference.py:27
+_WORDS = (torch.int32, torch.uint32)
+
+
+def qgemv(x, words, scale, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: float = 0.0,
+          bits: int | None = None, out=None):
+    """out[o] = srq(scale[o] * sum_i (q[o][i] - zp) srq(x[i], in_q), out_q) (reference.py:96-111)."""
+    _need(x, "x", torch.float32)
+    _need(words, "words", _WORDS)
+    _need(scale, "scale", torch.float32)
+    bits = bits or packed_bits(words, n_in, n_out)
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
+    check(_lib.load().g4a_qgemv(bits, n_in, n_out, _ptr(x), float(in_q), _ptr(words), _ptr(scale), float(out_q),
+                                _ptr(out), _stream()))
+    return out
+
+
+def gemv_f16(x, w_f16, out=None):
+    """out = w @ x, w f16 [n_out][n_in], f32 accumulation (reference.py:136)."""
+    _need(x, "x", torch.float32)
+    _need(w_f16, "w", torch.float16)
+    n_out, n_in = w_f16.shape
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
+    check(_lib.load().g4a_gemv_f16(n_in, n_out, _ptr(x), _ptr(w_f16), _ptr(out), _stream()))
+    return out
+
+
+def rms_norm(x, w=None, *, res=None, pre: float = 1.0, mult: float = 1.0, eps: float = EPS, out=None,
+             q2: float | None = None, f16_2: bool = False, out2=None, sum2=None):
+    """Rows of x [.., n]: out = (res + rms(x * pre) * w) * mult; optional out2 = srq(out, q2)
+    (f16_2: f16(srq(f16(out), q2))) and sum2 = sum of out2 per row (reference.py:38-43)."""
+    _need(x, "x", torch.float32)
+    n = x.shape[-1]
+    rows = x.numel() // n
+    if out is None:
+        out = torch.empty_like(x)
+    if q2 is not None and out2 is None:
+        out2 = torch.empty_like(x)
+    lib = _lib.load()
+    check(lib.g4a_rms_norm(rows, n, _ptr(x), float(pre), _ptr(w) if w is not None else None,
+                           _ptr(res) if res is not None else None, float(mult), float(eps), _ptr(out),
+                           float(q2 or 0.0), int(f16_2), _ptr(out2) if out2 is not None else None,
+                           _ptr(sum2) if sum2 is not None else None, _stream()))
+    return (out, out2) if out2 is not None else out
+
+
+def geglu(a, b, out_q: float = 0.0, out=None):
+    """out = srq(gelu_tanh(a) * b, out_q) (reference.py:34-35, :181, :188)."""
+    _need(a, "a", torch.float32)
+    _need(b, "b", torch.float32)
+    if out is None:
+        out = torch.empty_like(a)
+    check(_lib.load().g4a_geglu(a.numel(), _ptr(a), _ptr(b), float(out_q), _ptr(out), _stream()))
+    return out
+
+
+def embed(table_u8, tok, row_scale, n: int, bits: int, group: int, mult: float, out=None):
+    """Row tok[0] (device int32) of a packed table: mult * scale * (code - zp) (reference.py:114-131)."""
+    _need(table_u8, "table", torch.uint8)
+    _need(tok, "tok", torch.int32)
+    _need(row_scale, "row_scale", torch.float32)
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=table_u8.device)
+    check(_lib.load().g4a_embed(bits, n, _ptr(table_u8), table_u8.shape[0], _ptr(tok), _ptr(row_scale), group,
+                                float(mult), _ptr(out), _stream()))
+    return out
+
+
+def softcap_argmax(logits, cap: float, tok=None):
+    """logits <- cap * tanh(logits / cap) in place; tok[0] = first argmax (reference.py:207)."""
+    _need(logits, "logits", torch.float32)
+    if tok is None:
+        tok = torch.empty(1, dtype=torch.int32, device=logits.device)
+    check(_lib.load().g4a_softcap_argmax(logits.numel(), _ptr(logits), float(cap), _ptr(tok), _stream()))
+    return tok
+
+
+def lmhead_rows(blk: np.ndarray) -> np.ndarray:
+    """export.py:91-93 writes the lm_head as [H/64][vocab][4] words (one 16-byte block of
+    every row after another); the GEMV reads whole rows, [vocab][H/16] words."""
+    nb, vocab, four = blk.shape
+    return np.ascontiguousarray(blk.transpose(1, 0, 2)).reshape(vocab, nb * four)
+
+
+class DecoderStack:
+    """Every layer of the exported model for one token per step (reference.py:141-207).
+
+    Holds an AttentionStack (caches, q/k/v weights) and uploads the rest once: embedding
+    and per-layer-embedding tables, lm_head rows, o_proj, MLP and per-layer-embedding
+    linears and the norms. ``step(pos)`` runs the token in ``self.tok`` (device int32 [1])
+    at position pos and leaves the argmax in ``self.tok`` and the soft-capped logits in
+    ``self.logits``, so consecutive steps never touch the host.
+    """
+
+    def __init__(self, man: Manifest, max_seq: int, device="cuda"):
+        self.man = man
+        self.device = device
+        need = ["embed_q", "embed_scale", "ple_q", "ple_scale", "lmhead_blk", "lmhead_scale", "pl_model_proj",
+                "final_norm", "pl_proj_norm"]
+        for L in range(len(man.layers)):
+            need += [f"L{L}.{n}" for n in ("in_norm", "o_bits", "o_scale", "o_w12", "down_nw", "pleproj_w12s",
+                                           "gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits",
+                                           "down_scale", "plegate_codes", "plegate_rowscale", "pleproj_codes",
+                                           "pleproj_rowscale")]
+        missing = [n for n in need if n not in man.tensors]
+        if missing:
+            raise ManifestError(f"the decoder needs tensors the manifest lacks: {missing[:4]}...")
+        c = man.config
+        self.H, self.nL, self.d = man.hidden, int(c["nL"]), int(c["ple_d"])
+        self.vocab, self.softcap = int(c["vocab"]), float(c.get("softcap", 0.0))
+        self.embed_scale, self.ple_scale = float(c["embed_scale"]), float(c["ple_scale"])
+        self.attn = AttentionStack(man, max_seq, device)
+        dev = lambda a: torch.from_numpy(np.array(a)).to(device)  # noqa: E731  (a copy: the map is read-only)
+        words = lambda name: dev(man.tensor(name)).view(torch.int32).reshape(-1)  # noqa: E731
+        self.embed_q, self.embed_sc = dev(man.tensor("embed_q")), dev(man.tensor("embed_scale"))
+        self.ple_q, self.ple_sc = dev(man.tensor("ple_q")), dev(man.tensor("ple_scale"))
+        self.lm_rows = dev(lmhead_rows(man.tensor("lmhead_blk"))).view(torch.int32).reshape(-1)
+        self.lm_sc = dev(man.tensor("lmhead_scale"))
+        self.pl_proj = dev(man.tensor("pl_model_proj"))
+        self.final_norm, self.pl_norm = dev(man.tensor("final_norm")), dev(man.tensor("pl_proj_norm"))
+        H = self.H
+        self.w = []
+        for s in man.layers:
+            L = s.index
+            t = lambda n: dev(man.tensor(f"L{L}.{n}"))  # noqa: E731
+            w = {n: t(n) for n in ("in_norm", "o_scale", "o_w12", "down_nw", "gate_scale", "up_scale",
+                                   "down_scale", "plegate_rowscale", "pleproj_rowscale")}
+            for n in ("o_bits", "gate_bits", "up_bits", "down_bits", "plegate_codes", "pleproj_codes"):
+                w[n] = words(f"L{L}.{n}")
+            pl = man.tensor(f"L{L}.pleproj_w12s")
+            w["post_ple"] = dev(pl[:H])
+            w["layer_scalar"] = float(pl[2 * H])
+            w["o_w1"], w["o_w2"] = w["o_w12"][:H], w["o_w12"][H:]
+            w["gate_bits_n"] = packed_bits(w["gate_bits"], H, s.intermediate)
+            w["down_bits_n"] = packed_bits(w["down_bits"], s.intermediate, H)
+            w["o_bits_n"] = packed_bits(w["o_bits"], s.q_dim, H)
+            self.w.append(w)
+        f32 = lambda *shape: torch.zeros(*shape, dtype=torch.float32, device=device)  # noqa: E731
+        inter = max(s.intermediate for s in man.layers)
+        self.x, self.h, self.a, self.sum_a = f32(H), f32(H), f32(H), f32(1)
+        self.o, self.y2 = f32(H), f32(H)
+        self.gate, self.up, self.gg = f32(inter), f32(inter), f32(inter)
+        self.down = f32(H)
+        self.ple_tab, self.ple_proj, self.ple_in = f32(self.nL, self.d), f32(self.nL * self.d), f32(self.nL, self.d)
+        self.plegate, self.pleg, self.pleproj = f32(self.d), f32(self.d), f32(H)
+        self.logits = f32(self.vocab)
+        self.tok = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def embed_token(self):
+        """x = embed(tok), ple_in = ple_input(tok, x) (reference.py:114-139)."""
+        H, nL, d = self.H, self.nL, self.d
+        embed(self.embed_q, self.tok, self.embed_sc, H, 2, H, self.embed_scale, out=self.x)
+        embed(self.ple_q, self.tok, self.ple_sc, nL * d, 4, d, self.ple_scale, out=self.ple_tab.view(-1))
+        gemv_f16(self.x, self.pl_proj, out=self.ple_proj)
+        rms_norm(self.ple_proj.view(nL, d), self.pl_norm, res=self.ple_tab, pre=H ** -0.5, mult=2.0 ** -0.5,
+                 out=self.ple_in)
+
+    def layer(self, L: int, pos: int, trace: dict | None = None):
+        """Layer L on self.x in place (reference.py:141-191)."""
+        s, w, H = self.man.layers[L], self.w[L], self.H
+        sc, inter = s.scales, s.intermediate
+        snap = (lambda k, t: trace.__setitem__(k, t.clone())) if trace is not None else (lambda k, t: None)
+        snap("x0", self.x)
+        rms_norm(self.x, w["in_norm"], out=self.h, q2=sc["qkv_in"], out2=self.a, sum2=self.sum_a)
+        snap("a", self.a)
+        attn = self.attn.decode_layer(L, pos, self.a, self.sum_a).view(-1)
+        snap("attn", attn)
+        qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=sc["o_in"], out_q=sc["o_out"], bits=w["o_bits_n"],
+              out=self.o)
+        snap("o", self.o)
+        rms_norm(self.o, w["o_w1"], res=self.x, out=self.x)
+        snap("x1", self.x)
+        rms_norm(self.x, w["o_w2"], out=self.h, q2=sc["gate_in"], f16_2=True, out2=self.y2)
+        snap("y2", self.y2)
+        gb = w["gate_bits_n"]
+        gate, up, gg = self.gate[:inter], self.up[:inter], self.gg[:inter]
+        qgemv(self.y2, w["gate_bits"], w["gate_scale"], H, inter, in_q=sc["gate_in"], out_q=sc["gate_out"], bits=gb,
+              out=gate)
+        qgemv(self.y2, w["up_bits"], w["up_scale"], H, inter, in_q=sc["up_in"], out_q=sc["up_out"], bits=gb, out=up)
+        snap("gate", gate)
+        snap("up", up)
+        geglu(gate, up, sc["down_in"], out=gg)
+        snap("geglu", gg)
+        qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=sc["down_in"], out_q=sc["down_out"],
+              bits=w["down_bits_n"], out=self.down)
+        snap("down", self.down)
+        rms_norm(self.down, w["down_nw"], res=self.x, out=self.x)
+        snap("x2", self.x)
+        qgemv(self.x, w["plegate_codes"], w["plegate_rowscale"], H, self.d, in_q=sc["plegate_in"],
+              out_q=sc["plegate_out"], bits=8, out=self.plegate)
+        snap("plegate", self.plegate)
+        geglu(self.plegate, self.ple_in[L], 0.0, out=self.pleg)
+        snap("pleg", self.pleg)
+        qgemv(self.pleg, w["pleproj_codes"], w["pleproj_rowscale"], self.d, H, in_q=sc["pleproj_in"],
+              out_q=sc["pleproj_out"], bits=8, out=self.pleproj)
+        snap("pleproj", self.pleproj)
+        rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x)
+        snap("x3", self.x)
+
+    def head(self):
+        """Final norm, 2-bit lm_head, softcap and argmax into self.tok (reference.py:200-207)."""
+        rms_norm(self.x, self.final_norm, out=self.h)
+        qgemv(self.h, self.lm_rows, self.lm_sc, self.H, self.vocab, bits=2, out=self.logits)
+        softcap_argmax(self.logits, self.softcap, tok=self.tok)
+
+    def step(self, pos: int, trace: list | None = None):
+        """One token at position pos: self.tok in, the next token in self.tok out."""
+        self.embed_token()
+        if trace is not None:
+            trace.append({"x": self.x.clone(), "ple_in": self.ple_in.clone()})
+        for L in range(self.nL):
+            t = {} if trace is not None else None
+            self.layer(L, pos, t)
+            if trace is not None:
+                trace.append(t)
+        self.head()
+        return self.tok

@@ -40,8 +40,11 @@ class _Writer:
 
 
 def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHEDULE, seed=0,
-                extra_odd_tensor=True):
-    """Write the model; returns (manifest dict, {tensor name: array}) for the checks."""
+                extra_odd_tensor=True, full=False, vocab=512, ple_d=32, mlp_bits=(4, 2, 4, 2)):
+    """Write the model; returns (manifest dict, {tensor name: array}) for the checks.
+    full: also the tensors of the rest of the decoder (export.py:86-98, 113-160): the
+    embedding and per-layer-embedding tables, lm_head blocks, o_proj, the MLP (layer L's
+    gate/up/down rows mlp_bits[L]-bit), the int8 per-layer-embedding linears and the norms."""
     rng = np.random.default_rng(seed)
     os.makedirs(out_dir, exist_ok=True)
     w = _Writer(os.path.join(out_dir, "weights.bin"))
@@ -51,7 +54,20 @@ def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHED
         arrays[name] = arr
         w.put(name, arr, dtype)
 
-    if extra_odd_tensor:  # a u8 tensor of odd length first, so later offsets need the padding
+    nL = len(schedule)
+    if full:
+        gains = lambda n: (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+        put("embed_q", rng.integers(0, 256, size=(vocab, H // 4), dtype=np.uint8), "u8")
+        put("embed_scale", (0.02 * (1 + rng.random(vocab))).astype(np.float32), "f32")
+        put("ple_q", rng.integers(0, 256, size=(vocab, nL * ple_d // 2), dtype=np.uint8), "u8")
+        put("ple_scale", (0.05 * (1 + rng.random(vocab * nL))).astype(np.float32), "f32")
+        rows = pack_values(rng.integers(0, 4, size=(vocab, H)), 2)  # [vocab][H/16] words
+        put("lmhead_blk", np.ascontiguousarray(rows.reshape(vocab, H // 64, 4).transpose(1, 0, 2)), "u32")
+        put("lmhead_scale", (0.02 * (1 + rng.random(vocab))).astype(np.float32), "f32")
+        put("pl_model_proj", (0.05 * rng.standard_normal((nL * ple_d, H))).astype(np.float16), "f16")
+        put("final_norm", gains(H), "f32")
+        put("pl_proj_norm", gains(ple_d), "f32")
+    elif extra_odd_tensor:  # a u8 tensor of odd length first, so later offsets need the padding
         put("embed_q", rng.integers(0, 256, size=(3, 7), dtype=np.uint8), "u8")
     layers = []
     for L, (sliding, hd, cutoff, shared, src) in enumerate(schedule):
@@ -72,13 +88,32 @@ def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHED
         sc = {"qkv_in": 0.05, "q_out": 0.02, "o_in": 0.01, "o_out": 0.05}
         if not shared:
             sc.update(k_out=0.02, v_out=0.02)
+        if full:
+            inter, mb = 4 * H, mlp_bits[L % len(mlp_bits)]
+            qrows = lambda n_out, n_in, b: pack_values(rng.integers(0, 1 << b, size=(n_out, n_in)), b)  # noqa: E731
+            rsc = lambda n, s: (s * (1 + 0.2 * rng.random(n))).astype(np.float32)  # noqa: E731
+            put(f"L{L}.o_bits", qrows(H, q_dim, 4), "u32")
+            put(f"L{L}.o_scale", rsc(H, 0.01), "f32")
+            put(f"L{L}.o_w12", np.concatenate([gains(H), gains(H)]), "f32")
+            put(f"L{L}.down_nw", gains(H), "f32")
+            put(f"L{L}.pleproj_w12s", np.concatenate([gains(H), gains(H), [np.float32(0.5 + rng.random())]]
+                                                     ).astype(np.float32), "f32")
+            step = 0.01 * (1 << (4 - mb))  # coarser rows for fewer bits, similar output size
+            for tag, n_out, n_in in (("gate", inter, H), ("up", inter, H), ("down", H, inter)):
+                put(f"L{L}.{tag}_bits", qrows(n_out, n_in, mb), "u32")
+                put(f"L{L}.{tag}_scale", rsc(n_out, step), "f32")
+            for tag, n_out, n_in in (("plegate", ple_d, H), ("pleproj", H, ple_d)):
+                put(f"L{L}.{tag}_codes", qrows(n_out, n_in, 8), "u32")
+                put(f"L{L}.{tag}_rowscale", rsc(n_out, 0.002), "f32")
+            sc.update(gate_in=0.05, gate_out=0.02, up_in=0.04, up_out=0.02, down_in=0.01, down_out=0.02,
+                      plegate_in=0.05, plegate_out=0.03, pleproj_in=0.03, pleproj_out=0.01)
         layers.append({"index": L, "sliding": sliding, "head_dim": hd, "q_dim": q_dim,
                        "intermediate": 4 * H, "shared": shared, "kv_source": src,
                        "rope_theta": 1e4 if sliding else 1e6, "rope_cutoff": cutoff, "scales": sc})
     w.close()
-    man = {"config": {"H": H, "nL": len(schedule), "nH": n_heads, "vocab": 16, "window": window,
-                      "softcap": 30.0, "ple_d": 8, "embed_scale": float(np.sqrt(H)),
-                      "ple_scale": float(np.sqrt(8)), "bos": 2, "eos": 1},
+    man = {"config": {"H": H, "nL": nL, "nH": n_heads, "vocab": vocab if full else 16, "window": window,
+                      "softcap": 30.0, "ple_d": ple_d if full else 8, "embed_scale": float(np.sqrt(H)),
+                      "ple_scale": float(np.sqrt(ple_d if full else 8)), "bos": 2, "eos": 1},
            "layers": layers, "tensors": w.tensors, "bytes": w.pos}
     with open(os.path.join(out_dir, "manifest.json"), "w") as f:
         json.dump(man, f)

@@ -165,3 +165,36 @@ def test_gemm_mat_struct_layout():
     assert [f[0] for f in _lib.G4AGemmMat._fields_] == ["w_f16", "out", "n", "out_f32", "out_q"]
     assert _lib.G4AGemmMat.n.offset == 16 and _lib.G4AGemmMat.out_q.offset == 24
     assert ctypes.sizeof(_lib.G4AGemmMat) == 32
+
+
+def test_decoder_argument_errors(lib):
+    E, U = -1, -2
+    f = ctypes.c_float
+    # qgemv: bits, row shape, NULLs, alignment, negative steps
+    assert lib.g4a_qgemv(3, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == U
+    assert lib.g4a_qgemv(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == U
+    assert lib.g4a_qgemv(4, 48, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == E      # 48 % 32
+    assert lib.g4a_qgemv(2, 32, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == E      # 32 % 64
+    assert lib.g4a_qgemv(4, 64, 0, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == E
+    assert lib.g4a_qgemv(4, 64, 4, FAKE, f(0), FAKE, None, f(0), FAKE, None) == E      # no scale
+    assert lib.g4a_qgemv(4, 64, 4, ctypes.c_void_p(0x10004), f(0), FAKE, FAKE, f(0), FAKE, None) == E
+    assert lib.g4a_qgemv(4, 64, 4, FAKE, f(-1), FAKE, FAKE, f(0), FAKE, None) == E
+    assert lib.g4a_qgemv(4, 1 << 16, 1 << 16, FAKE, f(0), FAKE, FAKE, f(0), FAKE, None) == E  # 2 GiB rows
+    assert lib.g4a_gemv_f16(12, 4, FAKE, FAKE, FAKE, None) == E                          # 12 % 8
+    assert b"multiple" in lib.g4a_last_error()
+    # rms_norm: rows, NULLs, sum2 without out2, negative eps
+    args = lambda **k: [k.get(n, d) for n, d in (("rows", 1), ("n", 64), ("x", FAKE), ("pre", f(1)), ("w", None),  # noqa: E731
+                        ("res", None), ("mult", f(1)), ("eps", f(1e-6)), ("out", FAKE), ("q2", f(0)), ("f16", 0),
+                        ("out2", None), ("sum2", None), ("s", None))]
+    assert lib.g4a_rms_norm(*args(rows=0)) == E
+    assert lib.g4a_rms_norm(*args(x=None)) == E
+    assert lib.g4a_rms_norm(*args(sum2=FAKE)) == E
+    assert lib.g4a_rms_norm(*args(eps=f(-1))) == E
+    assert lib.g4a_geglu(0, FAKE, FAKE, f(0), FAKE, None) == E
+    assert lib.g4a_geglu(8, FAKE, FAKE, f(-0.5), FAKE, None) == E
+    # embed: bits, n vs group, NULL token
+    assert lib.g4a_embed(3, 64, FAKE, 8, FAKE, FAKE, 64, f(1), FAKE, None) == U
+    assert lib.g4a_embed(2, 64, FAKE, 8, FAKE, FAKE, 48, f(1), FAKE, None) == E
+    assert lib.g4a_embed(2, 64, FAKE, 8, None, FAKE, 64, f(1), FAKE, None) == E
+    assert lib.g4a_softcap_argmax(0, FAKE, f(30), FAKE, None) == E
+    assert lib.g4a_softcap_argmax(8, FAKE, f(-1), FAKE, None) == E

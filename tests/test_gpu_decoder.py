@@ -1,0 +1,181 @@
+"""GPU parity of the decode step around the attention block (g4a_qgemv, g4a_gemv_f16,
+g4a_rms_norm, g4a_geglu, g4a_embed, g4a_softcap_argmax and DecoderStack) against
+oracle/decoder.py. SRQ'd outputs are checked on their grid, at most one step from the
+oracle's unquantised value; every stage of a layer is checked from the GPU's own inputs."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.decoder as OD
+from helpers import contract_close, srq_close
+from manifest_fixture import write_model
+from oracle.projection import pack_values
+from slang_amd import decoder as D
+from slang_amd.manifest import load_manifest
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def host(t):
+    return t.detach().float().cpu().numpy() if t.dtype != torch.int32 else t.cpu().numpy()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+@pytest.mark.parametrize("bits,n_in,n_out,in_q,out_q", [
+    (4, 2048, 1536, 0.01, 0.05),    # o_proj
+    (4, 1536, 6144, 0.05, 0.02),    # gate / up
+    (2, 1536, 12288, 0.05, 0.02),   # the 2-bit double-wide MLP
+    (4, 6144, 1536, 0.01, 0.02),    # down
+    (2, 12288, 1536, 0.01, 0.02),
+    (8, 1536, 256, 0.05, 0.03),     # per-layer-embedding gate
+    (8, 256, 1536, 0.03, 0.01),     # per-layer-embedding projection
+    (2, 1536, 4099, 0.0, 0.0),      # lm_head rows (ragged count), no srq
+    (8, 16, 3, 0.0, 0.0),           # one chunk per row, fewer rows than a workgroup
+])
+def test_qgemv_parity(bits, n_in, n_out, in_q, out_q):
+    rng = np.random.default_rng(bits * 7 + n_out)
+    words = pack_values(rng.integers(0, 1 << bits, size=(n_out, n_in)), bits)
+    scale = (0.01 * (1 + rng.random(n_out))).astype(np.float32)
+    x = (2 * rng.standard_normal(n_in)).astype(np.float32)
+    got = host(D.qgemv(dev(x), dev(words).view(torch.int32).reshape(-1), dev(scale), n_in, n_out, in_q=in_q,
+                       out_q=out_q, bits=bits))
+    ref = OD.qlin(x, words, scale, n_in, bits, in_q, 0.0)
+    if out_q:
+        srq_close(got, ref, out_q, f"qgemv {bits}-bit {n_out}x{n_in}")
+    else:
+        contract_close(got, ref, f"qgemv {bits}-bit {n_out}x{n_in}")
+
+
+def test_gemv_f16_parity():
+    rng = np.random.default_rng(3)
+    w = (0.05 * rng.standard_normal((35 * 256, 1536))).astype(np.float16)
+    x = rng.standard_normal(1536).astype(np.float32)
+    contract_close(host(D.gemv_f16(dev(x), dev(w))), w.astype(np.float32) @ x, "gemv_f16")
+
+
+def test_rms_norm_variants():
+    rng = np.random.default_rng(4)
+    for rows, n in ((1, 1536), (35, 256), (1, 12288), (3, 100)):
+        x = (3 * rng.standard_normal((rows, n))).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        res = rng.standard_normal((rows, n)).astype(np.float32)
+        out, out2 = D.rms_norm(dev(x), dev(w), res=dev(res), pre=0.3, mult=0.7, q2=0.05, f16_2=True)
+        sum2 = torch.empty(rows, device=DEV)
+        D.rms_norm(dev(x), dev(w), out=torch.empty_like(out), q2=0.05, out2=torch.empty_like(out), sum2=sum2)
+        ref = (res + OD.rms_norm(x * np.float32(0.3), w)) * np.float32(0.7)
+        contract_close(host(out), ref, f"rms {rows}x{n}")
+        # the second output from the GPU's own first one: exact
+        o = host(out)
+        want2 = OD.srq(o.astype(np.float16).astype(np.float32), 0.05).astype(np.float16).astype(np.float32)
+        assert np.array_equal(host(out2), want2)
+        plain = OD.srq(OD.rms_norm(x, w), 0.05)
+        assert np.abs(host(sum2) - plain.sum(-1)).max() <= 0.05 * 3 + 1e-3 * n  # a few .5 flips at most
+    # in place: out aliases res (the residual adds)
+    x = rng.standard_normal(1536).astype(np.float32)
+    r = dev(rng.standard_normal(1536).astype(np.float32))
+    r0 = host(r)
+    D.rms_norm(dev(x), None, res=r, out=r)
+    contract_close(host(r), r0 + OD.rms_norm(x), "rms in place")
+
+
+def test_geglu_and_embed():
+    rng = np.random.default_rng(5)
+    a = (2 * rng.standard_normal(6144)).astype(np.float32)
+    b = rng.standard_normal(6144).astype(np.float32)
+    srq_close(host(D.geglu(dev(a), dev(b), 0.01)), OD.gelu_tanh(a) * b, 0.01, "geglu")
+    contract_close(host(D.geglu(dev(a), dev(b), 0.0)), OD.gelu_tanh(a) * b, "geglu no srq")
+    vocab, H, nL, d = 300, 1536, 35, 256
+    emb = rng.integers(0, 256, size=(vocab, H // 4), dtype=np.uint8)
+    esc = rng.random(vocab).astype(np.float32)
+    ple = rng.integers(0, 256, size=(vocab, nL * d // 2), dtype=np.uint8)
+    psc = rng.random(vocab * nL).astype(np.float32)
+    for t in (0, 7, vocab - 1):
+        tok = torch.tensor([t], dtype=torch.int32, device=DEV)
+        got = host(D.embed(dev(emb), tok, dev(esc), H, 2, H, 39.19))
+        assert np.array_equal(got, OD.embed_row(emb, t, esc, H, 2, H, 39.19))
+        got = host(D.embed(dev(ple), tok, dev(psc), nL * d, 4, d, 16.0))
+        assert np.array_equal(got, OD.embed_row(ple, t, psc, nL * d, 4, d, 16.0))
+    for t in (-1, vocab, 1 << 30):  # ids outside the table: zeros, no access outside it
+        tok = torch.tensor([t], dtype=torch.int32, device=DEV)
+        assert not host(D.embed(dev(emb), tok, dev(esc), H, 2, H, 1.0)).any()
+
+
+def test_softcap_argmax():
+    rng = np.random.default_rng(6)
+    for n in (1, 1000, 262144):
+        z = (5 * rng.standard_normal(n)).astype(np.float32)
+        if n > 10:
+            z[n // 3] = z[2 * n // 3] = z.max() + 1.0  # a tie: the first index wins
+        lg = dev(z)
+        tok = D.softcap_argmax(lg, 30.0)
+        ref, t = OD.softcap_argmax(z, 30.0)
+        contract_close(host(lg), ref, "softcap")
+        assert int(host(tok)[0]) == t == int(np.argmax(z))
+    lg = dev(np.array([3.0, 9.0, 9.0, -1.0], np.float32))
+    assert int(host(D.softcap_argmax(lg, 0.0))[0]) == 1 and host(lg)[1] == 9.0
+
+
+def _stage_checks(m, L, t, ple_in):
+    """Each stage of layer L from the GPU's own inputs to it (trace t of DecoderStack.layer)."""
+    s = m.layers[L]
+    sc, H, inter, d = s.scales, m.hidden, s.intermediate, int(m.config["ple_d"])
+    g = {k: host(v) for k, v in t.items()}
+    w = lambda n: m.tensor(f"L{L}.{n}")  # noqa: E731
+    o_w12, pl = w("o_w12"), w("pleproj_w12s")
+    bits = lambda n, n_out, n_in: OD.bits_of(m, f"L{L}.{n}", n_out, n_in)  # noqa: E731
+    what = f"layer {L}"
+    srq_close(g["a"], OD.rms_norm(g["x0"], w("in_norm")), sc["qkv_in"], what + " a")
+    srq_close(g["o"], OD.qlin(g["attn"], w("o_bits"), w("o_scale"), s.q_dim, bits("o_bits", H, s.q_dim), sc["o_in"]),
+              sc["o_out"], what + " o_proj")
+    contract_close(g["x1"], g["x0"] + OD.rms_norm(g["o"], o_w12[:H]), what + " x1")
+    y2 = OD.srq(OD.rms_norm(g["x1"], o_w12[H:]).astype(np.float16).astype(np.float32), sc["gate_in"])
+    assert np.abs(g["y2"] - y2).max() <= sc["gate_in"] * 1.001 and (g["y2"] != y2.astype(np.float16)).mean() < 0.05
+    gb = bits("gate_bits", inter, H)
+    srq_close(g["gate"], OD.qlin(g["y2"], w("gate_bits"), w("gate_scale"), H, gb, sc["gate_in"]), sc["gate_out"],
+              what + " gate")
+    srq_close(g["up"], OD.qlin(g["y2"], w("up_bits"), w("up_scale"), H, gb, sc["up_in"]), sc["up_out"], what + " up")
+    srq_close(g["geglu"], OD.gelu_tanh(g["gate"]) * g["up"], sc["down_in"], what + " geglu")
+    srq_close(g["down"], OD.qlin(g["geglu"], w("down_bits"), w("down_scale"), inter, bits("down_bits", H, inter),
+                                 sc["down_in"]), sc["down_out"], what + " down")
+    contract_close(g["x2"], g["x1"] + OD.rms_norm(g["down"], w("down_nw")), what + " x2")
+    srq_close(g["plegate"], OD.qlin(g["x2"], w("plegate_codes"), w("plegate_rowscale"), H, 8, sc["plegate_in"]),
+              sc["plegate_out"], what + " plegate", max_flip_frac=0.1)
+    contract_close(g["pleg"], OD.gelu_tanh(g["plegate"]) * ple_in[L], what + " pleg")
+    srq_close(g["pleproj"], OD.qlin(g["pleg"], w("pleproj_codes"), w("pleproj_rowscale"), d, 8, sc["pleproj_in"]),
+              sc["pleproj_out"], what + " pleproj")
+    contract_close(g["x3"], (g["x2"] + OD.rms_norm(g["pleproj"], pl[:H])) * pl[2 * H], what + " x3")
+
+
+def test_decoder_steps_stage_by_stage(tmp_path):
+    """Three resident steps of a four-layer model (sliding hd 256 / global hd 512 with
+    partial RoPE, two KV-sharing layers, 4- and 2-bit MLPs): each step's token is the
+    previous step's argmax, read on the device."""
+    write_model(tmp_path, full=True, seed=11)
+    m = load_manifest(tmp_path)
+    st = D.DecoderStack(m, max_seq=64, device=DEV)
+    st.tok.fill_(5)
+    prev = 5
+    for pos in range(3):
+        trace = []
+        st.step(pos, trace=trace)
+        torch.cuda.synchronize()
+        x = host(trace[0]["x"])
+        assert np.array_equal(x, OD.embed_row(m.tensor("embed_q"), prev, m.tensor("embed_scale"), m.hidden, 2,
+                                              m.hidden, m.config["embed_scale"]))
+        ple_in = host(trace[0]["ple_in"])
+        contract_close(ple_in, OD.ple_input(m, prev, x), f"step {pos} ple_in")
+        for L in range(len(m.layers)):
+            _stage_checks(m, L, trace[L + 1], ple_in)
+        logits, t = OD.final_logits(m, host(trace[-1]["x3"]))
+        got = host(st.logits)
+        contract_close(got, logits, f"step {pos} logits")
+        tok = int(host(st.tok)[0])
+        assert got[tok] == got.max() and tok == int(np.argmax(got))
+        top2 = np.sort(logits)[-2:]
+        if top2[1] - top2[0] > 1e-2:
+            assert tok == t
+        prev = tok

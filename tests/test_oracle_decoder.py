@@ -1,0 +1,105 @@
+"""Pins of oracle/decoder.py (the decode step around attention) against what does not
+restate it: the erf form of GELU, float64 loops, hand-packed words, closed forms."""
+import math
+import sys
+
+import numpy as np
+
+import oracle.decoder as OD
+from oracle.projection import pack_values
+
+sys.path.insert(0, __file__.rsplit("/", 1)[0])
+from manifest_fixture import write_model  # noqa: E402
+
+
+def test_gelu_tanh_against_erf_gelu_and_limits():
+    v = np.linspace(-6, 6, 2001, dtype=np.float32)
+    exact = np.array([0.5 * x * (1 + math.erf(x / math.sqrt(2))) for x in v.astype(np.float64)])
+    assert np.abs(OD.gelu_tanh(v) - exact).max() < 1e-3       # the tanh form's known accuracy
+    assert OD.gelu_tanh(np.float32(0.0)) == 0.0
+    assert abs(OD.gelu_tanh(np.float32(10.0)) - 10.0) < 1e-5 and abs(OD.gelu_tanh(np.float32(-10.0))) < 1e-5
+    assert OD.gelu_tanh(np.float32(1.0)) > 0.84 and OD.gelu_tanh(np.float32(-1.0)) < -0.15  # odd part
+
+
+def test_rms_norm_against_float64_loop_and_invariants():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 40)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(40)).astype(np.float32)
+    ref = np.empty_like(x, dtype=np.float64)
+    for r in range(3):
+        ms = sum(float(t) * float(t) for t in x[r]) / 40
+        ref[r] = [float(t) / math.sqrt(ms + 1e-6) * float(g) for t, g in zip(x[r], w)]
+    assert np.abs(OD.rms_norm(x, w) - ref).max() < 1e-5
+    y = OD.rms_norm(x)
+    assert np.allclose((y * y).mean(-1), 1.0, atol=1e-4)           # unit RMS
+    assert np.allclose(OD.rms_norm(7.5 * x), y, atol=1e-5)         # scale invariance
+
+
+def test_qlin_against_python_loop_all_widths():
+    rng = np.random.default_rng(1)
+    for bits in (2, 4, 8):
+        n_in, n_out = 128 // bits * 2, 5
+        codes = rng.integers(0, 1 << bits, size=(n_out, n_in))
+        words = pack_values(codes, bits)
+        scale = (0.01 * (1 + rng.random(n_out))).astype(np.float32)
+        x = rng.standard_normal(n_in).astype(np.float32)
+        in_q, out_q = 0.05, 0.02
+        got = OD.qlin(x, words, scale, n_in, bits, in_q, out_q)
+        zp = 1 << (bits - 1)
+        xq = [min(max(round(float(np.float32(t) / np.float32(in_q))), -128), 127) * in_q for t in x]
+        for o in range(n_out):
+            acc = sum((int(codes[o][i]) - zp) * float(scale[o]) * xq[i] for i in range(n_in))
+            want = min(max(round(acc / out_q), -128), 127) * out_q
+            assert abs(got[o] - want) <= out_q * 1.001, (bits, o)   # a .5 tie may round either way
+    # closed form: every value at the zero point gives 0 whatever the input
+    words = pack_values(np.full((3, 64), 8), 4)
+    assert not OD.qlin(rng.standard_normal(64).astype(np.float32), words, np.ones(3, np.float32), 64, 4).any()
+
+
+def test_embed_row_hand_packed_words():
+    # 2-bit row of 16 values 0,1,2,3,0,1,... in one word: value j at bits 2j
+    word = sum((j % 4) << (2 * j) for j in range(16))
+    table = np.frombuffer(np.array([[0] * 1, [word]], np.uint32).tobytes(), np.uint8).reshape(2, 4)
+    got = OD.embed_row(table, 1, np.array([0.5, 2.0], np.float32), 16, 2, 16, 3.0)
+    assert np.array_equal(got, 3.0 * 2.0 * (np.arange(16) % 4 - 2).astype(np.float32))
+    # 4-bit, two slices of 8 values with their own scales
+    word4 = [sum(((j + 8 * s) % 16) << (4 * j) for j in range(8)) for s in range(2)]
+    table = np.frombuffer(np.array(word4, np.uint32).tobytes(), np.uint8).reshape(1, 8)
+    got = OD.embed_row(table, 0, np.array([1.0, 0.25], np.float32), 16, 4, 8, 2.0)
+    want = 2.0 * np.repeat([1.0, 0.25], 8) * (np.arange(16) % 16 - 8)
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_lmhead_block_order_and_argmax_ties():
+    rng = np.random.default_rng(2)
+    rows = pack_values(rng.integers(0, 4, size=(7, 128)), 2)            # [7][8] words
+    blk = rows.reshape(7, 2, 4).transpose(1, 0, 2).copy()                 # export.py:91-93
+    assert np.array_equal(OD.lmhead_rows(blk), rows)
+    z, t = OD.softcap_argmax(np.array([1.0, 5.0, -2.0, 5.0], np.float32), 30.0)
+    assert t == 1 and np.allclose(z, 30 * np.tanh(np.array([1, 5, -2, 5]) / 30))
+    assert OD.softcap_argmax(np.array([0.0, 0.0], np.float32), 0.0)[1] == 0
+
+
+def test_stage_functions_compose_to_reference_layer(tmp_path):
+    """post_attention + ple_block == the reference layer's formula written out at once."""
+    from slang_amd.manifest import load_manifest
+    write_model(tmp_path, full=True, seed=4)
+    m = load_manifest(tmp_path)
+    rng = np.random.default_rng(3)
+    H, L = m.hidden, 1
+    s = m.layers[L]
+    x = rng.standard_normal(H).astype(np.float32)
+    attn = OD.srq(rng.standard_normal(s.q_dim).astype(np.float32), s.scales["o_in"])
+    ple_in = rng.standard_normal(m.config["ple_d"]).astype(np.float32)
+    st = OD.post_attention(m, L, x, attn)
+    pb = OD.ple_block(m, L, st["x2"], ple_in)
+    t = lambda n: m.tensor(f"L{L}.{n}")  # noqa: E731
+    sc = s.scales
+    W = lambda n, sname, n_in, bits: ((OD.unpack_values(t(n), n_in, bits) - (1 << (bits - 1)))  # noqa: E731
+                                      * t(sname)[:, None].astype(np.float64))
+    q = lambda v, step: np.clip(np.round(v / step), -128, 127) * step  # noqa: E731
+    o = q(W("o_bits", "o_scale", s.q_dim, 4) @ q(attn, sc["o_in"]), sc["o_out"])
+    assert np.abs(o - st["o"]).max() <= sc["o_out"] * 1.001
+    assert s.intermediate == 4 * H and OD.bits_of(m, f"L{L}.gate_bits", 4 * H, H) == 2
+    assert abs(pb["x3"] - (st["x2"] + OD.rms_norm(pb["pleproj"], t("pleproj_w12s")[:H])) * t("pleproj_w12s")[2 * H]
+               ).max() < 1e-5
