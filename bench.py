@@ -236,6 +236,104 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
                     "is given beside it"}
 
 
+def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, inter=6144, window=512):
+    """A Gemma 4 E2B-shaped model in the exported format (export.py:64-181), built in host
+    memory over random weights (no checkpoint): 35 layers, every fifth global (hd 512,
+    partial RoPE cutoff 64, theta 1e6), the others sliding (hd 256, W 512, theta 1e4),
+    nH 8 / kvH 1, layers 15.. sharing the caches of layers 13/14, 4-bit q/k/v/o and MLP
+    (intermediate 6144), int8 per-layer-embedding linears, 2-bit lm_head over 262144 tokens.
+    Packed rows are uniform random bytes, i.e. uniform codes of any width."""
+    from slang_amd.manifest import Manifest
+    rng = np.random.default_rng(seed)
+    parts, tensors, pos = [], {}, 0
+
+    def put(name, arr, dt):
+        nonlocal pos
+        b = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+        tensors[name] = {"off": pos, "len": int(b.size), "dtype": dt, "shape": list(arr.shape)}
+        parts.append(b)
+        pos += b.size
+        if pos % 4:
+            parts.append(np.zeros(4 - pos % 4, np.uint8))
+            pos += 4 - pos % 4
+
+    rbytes = lambda n_out, nb: np.frombuffer(rng.bytes(n_out * nb), np.uint8).reshape(n_out, nb)  # noqa: E731
+    rows = lambda n_out, n_in, bits: rbytes(n_out, n_in * bits // 8).view(np.uint32)  # noqa: E731
+    gains = lambda n: (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+    rsc = lambda n, s: (s * (1 + 0.2 * rng.random(n))).astype(np.float32)  # noqa: E731
+    put("embed_q", rbytes(vocab, H // 4), "u8")
+    put("embed_scale", rsc(vocab, 0.02), "f32")
+    put("ple_q", rbytes(vocab, n_layers * ple_d // 2), "u8")
+    put("ple_scale", rsc(vocab * n_layers, 0.05), "f32")
+    put("lmhead_blk", rows(H // 64 * vocab, 128, 1).reshape(H // 64, vocab, 4), "u32")
+    put("lmhead_scale", rsc(vocab, 0.02), "f32")
+    put("pl_model_proj", (0.02 * rng.standard_normal((n_layers * ple_d, H))).astype(np.float16), "f16")
+    put("final_norm", gains(H), "f32")
+    put("pl_proj_norm", gains(ple_d), "f32")
+    layers, first_shared = [], 15
+    for L in range(n_layers):
+        glob = L % 5 == 4
+        hd = 512 if glob else 256
+        shared = L >= first_shared
+        src = L if not shared else (14 if glob else 13)
+        q_dim = nH * hd
+        for n, a in (("in_norm", gains(H)), ("q_norm", gains(hd)), ("o_w12", gains(2 * H)),
+                     ("down_nw", gains(H)), ("pleproj_w12s", np.append(gains(2 * H), np.float32(0.8)))):
+            put(f"L{L}.{n}", a, "f32")
+        put(f"L{L}.q_bits", rows(q_dim, H, 4), "u32")
+        if shared:
+            put(f"L{L}.q_scale", rsc(q_dim, 0.01), "f32")
+        else:
+            put(f"L{L}.k_norm", gains(hd), "f32")
+            put(f"L{L}.k_bits", rows(hd, H, 4), "u32")
+            put(f"L{L}.v_bits", rows(hd, H, 4), "u32")
+            put(f"L{L}.qkv_scales", rsc(q_dim + 2 * hd, 0.01), "f32")
+        put(f"L{L}.o_bits", rows(H, q_dim, 4), "u32")
+        put(f"L{L}.o_scale", rsc(H, 0.01), "f32")
+        for tag, n_out, n_in in (("gate", inter, H), ("up", inter, H), ("down", H, inter)):
+            put(f"L{L}.{tag}_bits", rows(n_out, n_in, 4), "u32")
+            put(f"L{L}.{tag}_scale", rsc(n_out, 0.01), "f32")
+        for tag, n_out, n_in in (("plegate", ple_d, H), ("pleproj", H, ple_d)):
+            put(f"L{L}.{tag}_codes", rows(n_out, n_in, 8), "u32")
+            put(f"L{L}.{tag}_rowscale", rsc(n_out, 0.002), "f32")
+        sc = {"qkv_in": 0.05, "q_out": 0.02, "o_in": 0.01, "o_out": 0.05, "gate_in": 0.05, "gate_out": 0.02,
+              "up_in": 0.04, "up_out": 0.02, "down_in": 0.01, "down_out": 0.02, "plegate_in": 0.05,
+              "plegate_out": 0.03, "pleproj_in": 0.03, "pleproj_out": 0.01}
+        if not shared:
+            sc.update(k_out=0.02, v_out=0.02)
+        layers.append({"index": L, "sliding": not glob, "head_dim": hd, "q_dim": q_dim, "intermediate": inter,
+                       "shared": shared, "kv_source": src, "rope_theta": 1e6 if glob else 1e4,
+                       "rope_cutoff": 64 if glob else hd // 2, "scales": sc})
+    meta = {"config": {"H": H, "nL": n_layers, "nH": nH, "vocab": vocab, "window": window, "softcap": 30.0,
+                       "ple_d": ple_d, "embed_scale": float(np.sqrt(H)), "ple_scale": float(np.sqrt(ple_d)),
+                       "bos": 2, "eos": 1},
+            "layers": layers, "tensors": tensors, "bytes": pos}
+    return Manifest(meta, np.concatenate(parts))
+
+
+def decoder_case(steps=32, T=4096):
+    """Resident greedy decode of the E2B-shaped model (e2b_manifest): `steps` consecutive
+    tokens at positions T.., each step's token the previous step's device argmax, captured
+    as one HIP graph. Returns ms per token and the bytes one token must read (every weight
+    row once, the attended K/V rows, the lm_head and the per-layer-input projection)."""
+    from slang_amd.decoder import DecoderStack
+    man = e2b_manifest()
+    st = DecoderStack(man, max_seq=T + steps + 1)
+    del man
+    st.tok.fill_(2)
+    ms = graph_time_ms([lambda: [st.step(T + t) for t in range(steps)]], 1, 1) / steps
+    wbytes = sum(t.numel() * t.element_size() for w in st.w for k, t in w.items()
+                 if isinstance(t, torch.Tensor) and k.endswith(("_bits", "_codes")))
+    wbytes += sum(t.numel() * t.element_size() for w in st.attn.w.values() for k, t in w.items() if k.endswith("_bits"))
+    wbytes += st.lm_rows.numel() * 4 + st.pl_proj.numel() * 2
+    kv = 0
+    for s in st.man.layers:
+        rows = T + steps // 2 + 1  # the middle step's key count
+        rows = min(rows, st.man.window) if s.sliding else rows
+        kv += 2 * rows * st.man.n_kv_heads(s.index) * s.head_dim * 2
+    return ms, wbytes + kv, wbytes, kv
+
+
 def qkv_gemv_case(sa, steps, warmup, gen, n_sets=128):
     """Decode q/k/v projections of one token (qkv_70) at the config-2 layer shape: H 1536,
     q 8x256, k/v 2x256 rows of 4-bit weights; n_sets distinct weight sets (302 MB, more
@@ -344,6 +442,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 35-layer config 5 stack")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the E2B-shaped whole-decoder step")
+    ap.add_argument("--decoder-only", action="store_true", help="only the whole-decoder step row")
     ap.add_argument("--eager", action="store_true",
                     help="launch calls one by one instead of replaying a HIP graph (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -375,6 +475,11 @@ def main():
             msp, fl = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen)
             out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
         print(json.dumps(out), flush=True)
+        return
+    if args.decoder_only:
+        msd, nbd, wb, kvb = decoder_case()
+        print(json.dumps({"decoder_e2b": {"ms_per_token": round(msd, 4), "GB/s": round(nbd / msd / 1e6, 2),
+                                          "weight_bytes": wb, "kv_bytes": kvb}}), flush=True)
         return
     if args.batched_only:
         ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
@@ -428,6 +533,14 @@ def main():
                          "note": "prefill q/k/v projection GEMMs of one layer at S 1024, f16 weights"}
         if not args.no_stack:
             sec["stack_5"] = stack_case(sa, gen)
+        if not args.no_decoder:
+            msd, nbd, wb, kvb = decoder_case()
+            sec["decoder_e2b"] = {"ms_per_token": round(msd, 4), "tokens/s": round(1e3 / msd, 1),
+                                  "GB/s": round(nbd / msd / 1e6, 2), "hbm_frac": round(nbd / msd / 1e6 / HBM_PEAK_GBS, 4),
+                                  "bytes_per_token": nbd, "weight_bytes": wb, "kv_bytes": kvb,
+                                  "note": "whole decode step of an E2B-shaped synthetic model (35 layers, "
+                                          "vocab 262144, random weights), greedy token resident on the GPU, "
+                                          "32 steps at KV ~4096 in one HIP graph"}
         rec["secondary"] = sec
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds)

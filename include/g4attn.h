@@ -244,6 +244,19 @@ int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* 
  */
 int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
               const float* w_scale, float out_q, float* out, void* stream);
+/*
+ * The MLP's gate/up pair with its GeGLU in one pass over x (gateup_74/95; reference.py:176-181):
+ *   out[o] = srq(gelu_tanh(g[o]) * u[o], out_q),
+ *   g = the g4a_qgemv output of the gate rows (gate_in_q, gate_out_q), u that of the up rows.
+ */
+int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
+                    const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
+                    const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
+                    void* stream);
+/* g4a_qgemv with the per-layer-embedding gate's epilogue: out[o] = gelu_tanh(y[o]) * mul[o]
+ * (plegate_76; reference.py:186-187, mul = the layer's per-layer input). */
+int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
+                       const float* w_scale, float out_q, const float* mul, float* out, void* stream);
 /* Dense f16 GEMV: out[o] = sum_i w[o][i] x[i] in f32 (the per-layer-input projection,
  * reference.py:136, exported f16 by export.py:95). n_in a multiple of 8. */
 int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* out, void* stream);
@@ -252,13 +265,15 @@ int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* 
  * of :170, :183, :191; :133-139 for the per-layer-input context):
  *   y = x' / sqrt(mean(x'^2) + eps) * w (w NULL: no gain), x' = x * pre
  *   out = (res + y) * mult (res NULL: 0)
- *   out2 = srq(out, q2), or with f16_2 f16(srq(f16(out), q2)) (reference.py:153-156);
- *   sum2[row] = sum of out2 (qkv_70's sum_a). out2 and sum2 may be NULL.
- * out may alias x or res.
+ *   z = out, or with w2 the next norm z = out / sqrt(mean(out^2) + eps) * w2 (the pre-FFN
+ *   norm after the o_proj add, the next layer's input norm after the layer's last add)
+ *   out2 = srq(z, q2), or with f16_2 f16(srq(f16(z), q2)) (reference.py:176-178);
+ *   sum2[row] = sum of out2 (qkv_70's sum_a). w2, out2 and sum2 may be NULL.
+ * out may alias res (not x).
  */
 int g4a_rms_norm(int n_rows, int n, const float* x, float pre, const float* w, const float* res,
-                 float mult, float eps, float* out, float q2, int f16_2, float* out2, float* sum2,
-                 void* stream);
+                 float mult, float eps, float* out, const float* w2, float q2, int f16_2, float* out2,
+                 float* sum2, void* stream);
 /* out[i] = srq(gelu_tanh(a[i]) * b[i], out_q) (reference.py:34-35, :181, :188). */
 int g4a_geglu(int n, const float* a, const float* b, float out_q, float* out, void* stream);
 /*
@@ -270,8 +285,12 @@ int g4a_geglu(int n, const float* a, const float* b, float out_q, float* out, vo
 int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok,
               const float* row_scale, int group, float mult, float* out, void* stream);
 /* logits <- cap * tanh(logits / cap) in place (cap 0: unchanged) and tok[0] = the first
- * index of the maximum (reference.py:207; runner.py:501-505 argmax on the GPU). */
-int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* stream);
+ * index of the maximum (reference.py:207; runner.py:501-505 argmax1_34 -> argmax2_35 on the
+ * GPU). ws: g4a_softcap_argmax_ws_bytes(n) bytes for the per-workgroup candidates; logits
+ * 16-byte aligned. */
+size_t g4a_softcap_argmax_ws_bytes(int n);
+int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* ws, size_t ws_bytes,
+                       void* stream);
 
 #ifdef __cplusplus
 }

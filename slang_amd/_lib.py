@@ -26,7 +26,8 @@ EXPORTS = (
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
     "g4a_dequant", "g4a_qkv_gemv", "g4a_srqh", "g4a_gemm16",
-    "g4a_qgemv", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu", "g4a_embed", "g4a_softcap_argmax",
+    "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
+    "g4a_embed", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
 )
 
 
@@ -114,13 +115,19 @@ def load() -> ctypes.CDLL:
     lib.g4a_gemv_f16.restype = ctypes.c_int
     lib.g4a_gemv_f16.argtypes = [i, i, P, P, P, P]
     lib.g4a_rms_norm.restype = ctypes.c_int
-    lib.g4a_rms_norm.argtypes = [i, i, P, f, P, P, f, f, P, f, i, P, P, P]
+    lib.g4a_qgemv_geglu.restype = ctypes.c_int
+    lib.g4a_qgemv_geglu.argtypes = [i, i, i, P, P, P, f, f, P, P, f, f, f, P, P]
+    lib.g4a_qgemv_gelu_mul.restype = ctypes.c_int
+    lib.g4a_qgemv_gelu_mul.argtypes = [i, i, i, P, f, P, P, f, P, P, P]
+    lib.g4a_rms_norm.argtypes = [i, i, P, f, P, P, f, f, P, P, f, i, P, P, P]
     lib.g4a_geglu.restype = ctypes.c_int
     lib.g4a_geglu.argtypes = [i, P, P, f, P, P]
     lib.g4a_embed.restype = ctypes.c_int
     lib.g4a_embed.argtypes = [i, i, P, ctypes.c_int64, P, P, i, f, P, P]
     lib.g4a_softcap_argmax.restype = ctypes.c_int
-    lib.g4a_softcap_argmax.argtypes = [i, P, f, P, P]
+    lib.g4a_softcap_argmax_ws_bytes.restype = ctypes.c_size_t
+    lib.g4a_softcap_argmax_ws_bytes.argtypes = [i]
+    lib.g4a_softcap_argmax.argtypes = [i, P, f, P, P, ctypes.c_size_t, P]
     _lib = lib
     return lib
 

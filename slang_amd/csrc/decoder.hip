@@ -17,12 +17,16 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- quantised GEMV
 // out[o] = srq(scale[o] * sum_i (q[o][i] - zp) * srq(x[i], in_q), out_q)
-// (reference.py:99-104 _qlin, :106-114 _ilin_raw with the biased int8 codes of export.py:150-156,
-// :202-206 lm_head). Rows are packed BITS-bit values, value i of a row at bit
-// BITS*(i % (32/BITS)) of word i / (32/BITS) (the loader's and dq_f16's order); zp =
+// (reference.py:96-101 _qlin, :103-111 _ilin_raw with the biased int8 codes of
+// export.py:150-156, :200-206 lm_head). Rows are packed BITS-bit values, value i of a row at
+// bit BITS*(i % (32/BITS)) of word i / (32/BITS) (the loader's and dq_f16's order); zp =
 // 2^(BITS-1). BITS = 16: plain f16 rows (pl_model_proj), no zero point, no row scale.
 // A wave splits into 64/LPR lane groups; a group owns RPW rows and walks their 16-byte
-// chunks LPR at a time, so short rows (the 384-byte lm_head rows) keep every lane busy.
+// chunks LPR at a time, so short rows (the 384-byte lm_head rows) keep most lanes busy and
+// each chunk of x is loaded and quantised once for RPW rows. Epilogues (EPI):
+//   0  out = y
+//   1  gate/up pair (gateup_74/95): y_b from the second matrix, out = srq(gelu(y) * y_b, epi_q)
+//   2  out = gelu(y) * mul[o] (plegate_76: the gate times the layer's per-layer input)
 struct QgemvArgs {
     const float* x;
     const uint32_t* w;
@@ -30,79 +34,228 @@ struct QgemvArgs {
     float* out;
     int n_in, n_out, row_chunks;  // 16-byte chunks per row
     float in_q, out_q;
+    const uint32_t* w2;  // EPI 1: the up rows, their scales and steps
+    const float* scale2;
+    float in_q2, out_q2, epi_q;
+    const float* mul;  // EPI 2
 };
 
-template <int BITS, int LPR, int RPW>
-__global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
-    constexpr int VPC = 128 / BITS;  // values per 16-byte chunk
-    constexpr int VPW = 32 / BITS;   // values per word
-    constexpr int NG = 64 / LPR;
-    constexpr float ZP = BITS == 16 ? 0.0f : (float)(1 << (BITS - 1));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane % LPR, grp = lane / LPR;
-    const int row0 = ((blockIdx.x * 4 + wave) * NG + grp) * RPW;
-    const int nch = g.row_chunks;
-    // rows past n_out and chunks past a row read as zeros through the buffer ranges
-    const rsrc_t rw = make_rsrc(g.w, (uint32_t)g.n_out * (uint32_t)nch * 16u);
-    const rsrc_t rx = make_rsrc(g.x, (uint32_t)g.n_in * 4u);
-    float acc[RPW];
+__device__ __forceinline__ float gelu_tanh(float v) {
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+// sum over the LPR lanes of a lane group (16, 32 or 64), every lane of the group gets it
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+    v = row16_sum(v);
+    if constexpr (LPR >= 32) v = add16(v);
+    if constexpr (LPR == 64) v = add32(v);
+    return v;
+}
+
+// acc += sum_j q_j * x[j] over the VPC values of one 16-byte chunk, x from LDS in the
+// interleaved layout below. Codes go through byte lanes (v_cvt_f32_ubyteN after one mask):
+// the zero point is taken out once per row from the sum of x, as qkv_70 does.
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(u32x4_t w, const float4v* xq, int stride, float acc) {
+    constexpr int VPC = 128 / BITS;
+    float v[VPC];  // the chunk's codes (f16 values for BITS 16) in row order
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    for (int c = sub; c < nch; c += LPR) {
-        u32x4_t wv[RPW];
+    for (int k = 0; k < 4; ++k) {  // word k holds values VPC/4*k ..
+        const uint32_t u = w[k];
+        float* vk = v + (VPC / 4) * k;
+        if constexpr (BITS == 16) {
+            vk[0] = (float)__builtin_bit_cast(half_t, (uint16_t)(u & 0xFFFFu));
+            vk[1] = (float)__builtin_bit_cast(half_t, (uint16_t)(u >> 16));
+        } else if constexpr (BITS == 8) {
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int row = row0 + r < g.n_out ? row0 + r : g.n_out;  // n_out: past the range
-            wv[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rw, (row * nch + c) * 16, 0, kCpolNT));
-        }
-        float xv[VPC];
+            for (int b = 0; b < 4; ++b) vk[b] = (float)((u >> (8 * b)) & 0xFFu);
+        } else {
+            constexpr int PB = 8 / BITS;  // values per byte
+            constexpr uint32_t M = BITS == 4 ? 0x0F0F0F0Fu : 0x03030303u;
 #pragma unroll
-        for (int i = 0; i < VPC / 4; ++i) {
-            const float4v v = bload_f32x4(rx, (c * VPC + 4 * i) * 4);
+            for (int f = 0; f < PB; ++f) {
+                const uint32_t m = (u >> (BITS * f)) & M;  // value PB*b + f sits in byte b
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xv[4 * i + e] = srq(v[e], g.in_q);
-        }
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-#pragma unroll
-            for (int j = 0; j < VPC; ++j) {
-                const uint32_t word = wv[r][j / VPW];
-                float wq;
-                if constexpr (BITS == 16) {
-                    const uint16_t h = (uint16_t)(word >> (16 * (j % 2)));
-                    wq = (float)__builtin_bit_cast(half_t, h);
-                } else {
-                    wq = (float)((word >> (BITS * (j % VPW))) & ((1u << BITS) - 1u)) - ZP;
-                }
-                acc[r] = __builtin_fmaf(wq, xv[j], acc[r]);
+                for (int b = 0; b < 4; ++b) vk[PB * b + f] = (float)((m >> (8 * b)) & 0xFFu);
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
+    for (int e = 0; e < VPC / 4; ++e) {
+        const float4v xv = xq[e * stride];
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
+        for (int t = 0; t < 4; ++t) acc = __builtin_fmaf(v[4 * e + t], xv[t], acc);
     }
-    if (sub == 0) {
+    return acc;
+}
+
+template <int BITS, int T, int RPW, int EPI>
+__global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
+    // T threads per row group (16..256, the chunks of a row spread over them), 256/T groups
+    // per workgroup, RPW rows per group; groups wider than a wave reduce through LDS.
+    // With several groups per workgroup (T <= 64) x is quantised once per workgroup into LDS,
+    // float4 i of chunk c at [i][c] (threads of a group read consecutive chunks: conflict-free),
+    // one copy per matrix step; wider groups use each chunk of x in one thread only and load
+    // it straight from memory.
+    constexpr int VPC = 128 / BITS;  // values per 16-byte chunk
+    constexpr int NGRP = 256 / T;
+    constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
+    constexpr float ZP = BITS == 16 ? 0.0f : (float)(1 << (BITS - 1));
+    constexpr bool STAGE = T <= 64;
+    extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
+    __shared__ float red[T > 64 ? 4 : 1][NM][RPW];
+    __shared__ float xsum_part[8][NM];
+    const int tid = threadIdx.x;
+    const int sub = tid % T, grp = tid / T;
+    const int row0 = (blockIdx.x * NGRP + grp) * RPW;
+    const int nch = g.row_chunks, n_in = g.n_in;
+    // rows past n_out read as zeros through the buffer range
+    const uint32_t wbytes = (uint32_t)g.n_out * (uint32_t)nch * 16u;
+    const rsrc_t rw[2] = {make_rsrc(g.w, wbytes), make_rsrc(EPI == 1 ? g.w2 : g.w, wbytes)};
+    // weight loads of the first chunk go out before the staging of x
+    u32x4_t wv[NM][RPW];
+    auto load_w = [&](int c) {
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int row = row0 + r;
-            if (row < g.n_out) g.out[row] = srq((g.scale ? g.scale[row] : 1.0f) * acc[r], g.out_q);
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const int row = row0 + r < g.n_out ? row0 + r : g.n_out;  // n_out: past the range
+                wv[m][r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           rw[m], (row * nch + c) * 16, 0, kCpolNT));
+            }
+    };
+    if (sub < nch) load_w(sub);
+    float sx[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) sx[m] = 0.0f;
+    float* xsf = reinterpret_cast<float*>(xs);
+    for (int i = tid; STAGE && i < n_in; i += 256) {
+        const float v = g.x[i];
+        const int c = i / VPC, e = i % VPC;
+        const int at = ((e >> 2) * nch + c) * 4 + (e & 3);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const float q = srq(v, m == 0 ? g.in_q : g.in_q2);
+            xsf[m * n_in + at] = q;
+            sx[m] += q;
+        }
+    }
+    if constexpr (STAGE) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const float t = wave_sum(sx[m]);
+            if ((tid & 63) == 0) xsum_part[tid >> 6][m] = t;
+        }
+        __syncthreads();
+    }
+    const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
+    float acc[NM][RPW];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.0f;
+    for (int c = sub; c < nch; c += T) {
+        if (c != sub) load_w(c);
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+                    acc[m][r] = chunk_dot<BITS>(wv[m][r], xs + (size_t)m * (VPC / 4) * nch + c, nch, acc[m][r]);
+        } else {
+            float4v xr[VPC / 4];
+#pragma unroll
+            for (int e = 0; e < VPC / 4; ++e) xr[e] = bload_f32x4(rx, (c * VPC + 4 * e) * 4);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float q = m == 0 ? g.in_q : g.in_q2;
+                float4v xq[VPC / 4];
+#pragma unroll
+                for (int e = 0; e < VPC / 4; ++e) {
+                    xq[e] = srq4(xr[e], q);
+                    sx[m] += (xq[e][0] + xq[e][1]) + (xq[e][2] + xq[e][3]);
+                }
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) acc[m][r] = chunk_dot<BITS>(wv[m][r], xq, 1, acc[m][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[m][r] = group_sum<T >= 64 ? 64 : T>(acc[m][r]);
+        if constexpr (!STAGE) sx[m] = group_sum<64>(sx[m]);
+    }
+    if constexpr (T > 64) {  // the group's waves through LDS (one group per 128/256 threads)
+        const int wig = sub >> 6;  // wave in group
+        const int slot = (grp * (T / 64) + wig) & 3;
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) red[slot][m][r] = acc[m][r];
+                xsum_part[slot][m] = sx[m];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                float t = 0.0f;
+#pragma unroll
+                for (int k = 0; k < T / 64; ++k) t += red[(grp * (T / 64) + k) & 3][m][r];
+                acc[m][r] = t;
+            }
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < T / 64; ++k) t += xsum_part[(grp * (T / 64) + k) & 3][m];
+            sx[m] = t;
+        }
+    }
+    float zsx[NM];  // zero point times the sum of the quantised x (over the whole row)
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        float t = 0.0f;
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t += xsum_part[k][m];
+        } else {
+            t = sx[m];
+        }
+        zsx[m] = ZP * t;
+    }
+    // thread r of the group writes row r
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        if (sub == r && row < g.n_out) {
+            float y = srq((g.scale ? g.scale[row] : 1.0f) * (acc[0][r] - zsx[0]), g.out_q);
+            if constexpr (EPI == 1) {
+                const float yb = srq(g.scale2[row] * (acc[NM - 1][r] - zsx[NM - 1]), g.out_q2);
+                y = srq(gelu_tanh(y) * yb, g.epi_q);
+            } else if constexpr (EPI == 2) {
+                y = gelu_tanh(y) * g.mul[row];
+            }
+            g.out[row] = y;
         }
     }
 }
 
 // ---------------------------------------------------------------- RMSNorm family
 // Row r of n values: y = x' / sqrt(mean(x'^2) + eps) * w, x' = x * pre; out = (res + y) * mult
-// (reference.py:38-43 rms_norm, the sandwich adds of :150, :162, :170, :132-137 for the
-// per-layer-embedding context). Optional second output out2 = srq(out, q2), or with f16_2
-// f16(srq(f16(out), q2)) (the MLP input of :153-156), and sum2 = sum of out2 (the
+// (reference.py:38-43 rms_norm, the sandwich adds of :170, :183, :191, :133-139 for the
+// per-layer-embedding context). Optional second output from out itself or, with w2, from
+// the next norm z = rms(out) * w2 (the runner's cross-kernel fusions: oproj_73 ends with the
+// pre-FFN norm, pleproj_77 with the next layer's input norm): out2 = srq(z, q2), or with
+// f16_2 f16(srq(f16(z), q2)) (the MLP input of :176-178), and sum2 = sum of out2 (the
 // zero-point sum the q/k/v GEMV takes).
 struct RmsArgs {
     const float* x;
     const float* w;
     const float* res;
+    const float* w2;
     float* out;
     float* out2;
     float* sum2;
@@ -122,25 +275,50 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
+// Thread t holds elements t + k*blockDim (k < PER) in registers: every operand is loaded
+// once, up front, and the three sums cost only LDS round trips.
+template <int PER>
 __global__ __launch_bounds__(1024) void rms_kernel(RmsArgs a) {
     __shared__ float red[16];
-    const int r = blockIdx.x, n = a.n;
+    const int r = blockIdx.x, n = a.n, nt = blockDim.x;
     const float* x = a.x + (size_t)r * n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i] * a.pre;
-        ss = __builtin_fmaf(v, v, ss);
+    float* out = a.out + (size_t)r * n;
+    float xv[PER], wv[PER], rv[PER], w2v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + k * nt;
+        const bool ok = i < n;
+        xv[k] = ok ? x[i] * a.pre : 0.0f;
+        wv[k] = ok && a.w ? a.w[i] : 1.0f;
+        rv[k] = ok && a.res ? a.res[(size_t)r * n + i] : 0.0f;
+        w2v[k] = ok && a.w2 ? a.w2[i] : 1.0f;
     }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
     const float d = sqrtf(block_sum(ss, red) / (float)n + a.eps);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + k * nt;
+        float y = xv[k] / d;
+        if (a.w) y *= wv[k];
+        y = (rv[k] + y) * a.mult;
+        xv[k] = y;
+        if (i < n) {
+            out[i] = y;
+            ss2 = __builtin_fmaf(y, y, ss2);
+        }
+    }
+    if (!a.out2) return;
+    const float d2 = a.w2 ? sqrtf(block_sum(ss2, red) / (float)n + a.eps) : 1.0f;
     float s2 = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float y = (x[i] * a.pre) / d;
-        if (a.w) y *= a.w[i];
-        if (a.res) y = a.res[(size_t)r * n + i] + y;
-        y *= a.mult;
-        a.out[(size_t)r * n + i] = y;
-        if (a.out2) {
-            const float y2 = a.f16_2 ? (float)(half_t)srq((float)(half_t)y, a.q2) : srq(y, a.q2);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + k * nt;
+        const float z = a.w2 ? xv[k] / d2 * w2v[k] : xv[k];
+        const float y2 = a.f16_2 ? (float)(half_t)srq((float)(half_t)z, a.q2) : srq(z, a.q2);
+        if (i < n) {
             a.out2[(size_t)r * n + i] = y2;
             s2 += y2;
         }
@@ -153,10 +331,6 @@ __global__ __launch_bounds__(1024) void rms_kernel(RmsArgs a) {
 
 // ---------------------------------------------------------------- GeGLU
 // out = srq(gelu_tanh(a) * b, q) (reference.py:33-35, :159, :167)
-__device__ __forceinline__ float gelu_tanh(float v) {
-    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-}
-
 __global__ __launch_bounds__(256) void geglu_kernel(int n, const float* a, const float* b, float q, float* out) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) out[i] = srq(gelu_tanh(a[i]) * b[i], q);
@@ -188,31 +362,25 @@ __global__ __launch_bounds__(256) void embed_kernel(int bits, int n, const uint3
 
 // ---------------------------------------------------------------- softcap + argmax
 // logits <- cap * tanh(logits / cap) (cap 0: unchanged), tok = the first index of the
-// maximum (reference.py:207; numpy's argmax order). One workgroup.
-__global__ __launch_bounds__(1024) void softcap_argmax_kernel(int n, float* logits, float cap, int32_t* tok) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    float best = kNegInf;
-    int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        float v = logits[i];
-        if (cap != 0.0f) {
-            v = cap * tanhf(v / cap);
-            logits[i] = v;
-        }
-        if (v > best) {  // ascending i per thread: the first maximum stays
-            best = v;
-            bi = i;
-        }
+// maximum (reference.py:207; numpy's argmax order). Two stages as the runner's argmax1_34 /
+// argmax2_35 (runner.py:501-505): workgroup b caps and scans [b*kArgChunk, (b+1)*kArgChunk)
+// and leaves its (max, first index) in part[b]; one workgroup reduces the parts.
+constexpr int kArgChunk = 4096;
+
+__device__ __forceinline__ void argmax_step(float& best, int& bi, float v, int i) {
+    if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
     }
+}
+
+// the workgroup's (max, first index) into lane 0 of wave 0
+__device__ __forceinline__ void block_argmax(float& best, int& bi, float* sv, int* si) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(best, off);
         const int oi = __shfl_xor(bi, off);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
+        argmax_step(best, bi, ov, oi);
     }
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
@@ -220,34 +388,82 @@ __global__ __launch_bounds__(1024) void softcap_argmax_kernel(int n, float* logi
         si[wave] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; ++w)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
-        tok[0] = bi == 0x7fffffff ? 0 : bi;
-    }
+    if (threadIdx.x == 0)
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) argmax_step(best, bi, sv[w], si[w]);
 }
 
-template <int BITS, int LPR, int RPW>
+__global__ __launch_bounds__(256) void softcap_part_kernel(int n, float* logits, float cap, float2* part) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int base = blockIdx.x * kArgChunk;
+    float best = kNegInf;
+    int bi = 0x7fffffff;
+#pragma unroll 4
+    for (int k = 0; k < kArgChunk / 1024; ++k) {
+        const int i0 = base + 4 * (k * 256 + (int)threadIdx.x);  // 4 consecutive logits per thread
+        if (i0 + 3 < n) {
+            float4v v = *reinterpret_cast<const float4v*>(logits + i0);
+            if (cap != 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = cap * tanhf(v[e] / cap);
+                *reinterpret_cast<float4v*>(logits + i0) = v;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) argmax_step(best, bi, v[e], i0 + e);
+        } else {
+            for (int e = 0; e < 4 && i0 + e < n; ++e) {
+                float v = logits[i0 + e];
+                if (cap != 0.0f) {
+                    v = cap * tanhf(v / cap);
+                    logits[i0 + e] = v;
+                }
+                argmax_step(best, bi, v, i0 + e);
+            }
+        }
+    }
+    block_argmax(best, bi, sv, si);
+    if (threadIdx.x == 0) part[blockIdx.x] = make_float2(best, __builtin_bit_cast(float, bi));
+}
+
+__global__ __launch_bounds__(1024) void argmax_final_kernel(int n_part, const float2* part, int32_t* tok) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    float best = kNegInf;
+    int bi = 0x7fffffff;
+    for (int b = threadIdx.x; b < n_part; b += 1024) {
+        const float2 p = part[b];
+        argmax_step(best, bi, p.x, __builtin_bit_cast(int, p.y));
+    }
+    block_argmax(best, bi, sv, si);
+    if (threadIdx.x == 0) tok[0] = bi == 0x7fffffff ? 0 : bi;  // no finite maximum: 0, as numpy
+}
+
+template <int BITS, int T, int RPW, int EPI>
 static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
-    const int rows_per_wg = 4 * (64 / LPR) * RPW;
-    hipLaunchKernelGGL((qgemv_kernel<BITS, LPR, RPW>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg), dim3(256), 0,
-                       s, g);
+    const int rows_per_wg = (256 / T) * RPW;
+    const size_t lds = T <= 64 ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
+    hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg),
+                       dim3(256), lds, s, g);
     return hipGetLastError();
 }
 
-// lane-group width: the smallest power of two >= the chunks per row, at most 64
-template <int BITS>
+// Threads per row group: the smallest of 16..256 covering a row's chunks, so one pass
+// reads every row of the workgroup and all of them are in flight together (decode GEMVs
+// are latency-bound: o_proj and down have only 1536 rows). Rows per group: 8 for the
+// short 2-bit rows of the lm_head (x loaded once per 8 rows), else 2 (measured: 8 rows
+// per group on the 1536-row down projection, 192 workgroups, was 20 % slower).
+template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
-    if (g.row_chunks <= 16) return launch_qgemv<BITS, 16, 2>(g, s);
-    if (g.row_chunks <= 32) return launch_qgemv<BITS, 32, 2>(g, s);
-    return launch_qgemv<BITS, 64, 2>(g, s);
+    const int c = g.row_chunks;
+    if (c <= 16) return launch_qgemv<BITS, 16, 2, EPI>(g, s);
+    if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
+    if (c <= 64) return launch_qgemv<BITS, 64, 2, EPI>(g, s);
+    if (c <= 128) return launch_qgemv<BITS, 128, 2, EPI>(g, s);
+    return launch_qgemv<BITS, 256, 2, EPI>(g, s);
 }
 
-static int qgemv_impl(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w,
-                      const float* scale, float out_q, float* out, void* stream) {
+static int qgemv_check(int bits, int n_in, int n_out, const float* x, const uint32_t* w, const float* scale,
+                       const float* out, float in_q, float out_q) {
     if (bits != 2 && bits != 4 && bits != 8 && bits != 16) {
         set_error("bits %d not supported (2, 4, 8, or 16 for f16 rows)", bits);
         return G4A_EUNSUPPORTED;
@@ -258,8 +474,12 @@ static int qgemv_impl(int bits, int n_in, int n_out, const float* x, float in_q,
         return G4A_EINVAL;
     }
     const int64_t row_bytes = (int64_t)n_in * bits / 8;
-    if ((int64_t)(n_out + 512) * row_bytes > 0x7fffffff || n_in > (1 << 24)) {
+    if ((int64_t)(n_out + 512) * row_bytes > 0x7fffffff) {
         set_error("weights beyond 32-bit buffer offsets");
+        return G4A_EINVAL;
+    }
+    if (n_in > 16384) {  // x is staged in LDS, two copies for the gate/up pair
+        set_error("n_in (%d) above 16384", n_in);
         return G4A_EINVAL;
     }
     if (!x || !w || !out || (bits != 16 && !scale)) {
@@ -274,23 +494,42 @@ static int qgemv_impl(int bits, int n_in, int n_out, const float* x, float in_q,
         set_error("in_q/out_q must be >= 0");
         return G4A_EINVAL;
     }
-    QgemvArgs g;
+    return G4A_OK;
+}
+
+static int qgemv_run(int bits, int epi, QgemvArgs& g, void* stream) {
+    g.row_chunks = (int)((int64_t)g.n_in * bits / 128);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    switch (epi * 32 + bits) {
+        case 0 * 32 + 2: e = qgemv_dispatch<2, 0>(g, s); break;
+        case 0 * 32 + 4: e = qgemv_dispatch<4, 0>(g, s); break;
+        case 0 * 32 + 8: e = qgemv_dispatch<8, 0>(g, s); break;
+        case 0 * 32 + 16: e = qgemv_dispatch<16, 0>(g, s); break;
+        case 1 * 32 + 2: e = qgemv_dispatch<2, 1>(g, s); break;
+        case 1 * 32 + 4: e = qgemv_dispatch<4, 1>(g, s); break;
+        case 1 * 32 + 8: e = qgemv_dispatch<8, 1>(g, s); break;
+        case 2 * 32 + 2: e = qgemv_dispatch<2, 2>(g, s); break;
+        case 2 * 32 + 4: e = qgemv_dispatch<4, 2>(g, s); break;
+        case 2 * 32 + 8: e = qgemv_dispatch<8, 2>(g, s); break;
+        default: set_error("no GEMV for %d-bit rows with epilogue %d", bits, epi); return G4A_EUNSUPPORTED;
+    }
+    if (e != hipSuccess) return hip_error(e, "qgemv launch");
+    return G4A_OK;
+}
+
+static QgemvArgs qgemv_args(int n_in, int n_out, const float* x, float in_q, const uint32_t* w, const float* scale,
+                            float out_q, float* out) {
+    QgemvArgs g{};
     g.x = x;
     g.w = w;
-    g.scale = bits == 16 ? nullptr : scale;
+    g.scale = scale;
     g.out = out;
     g.n_in = n_in;
     g.n_out = n_out;
-    g.row_chunks = (int)(row_bytes / 16);
     g.in_q = in_q;
     g.out_q = out_q;
-    hipStream_t s = (hipStream_t)stream;
-    hipError_t e = bits == 2   ? qgemv_dispatch<2>(g, s)
-                   : bits == 4 ? qgemv_dispatch<4>(g, s)
-                   : bits == 8 ? qgemv_dispatch<8>(g, s)
-                               : qgemv_dispatch<16>(g, s);
-    if (e != hipSuccess) return hip_error(e, "qgemv launch");
-    return G4A_OK;
+    return g;
 }
 
 }  // namespace g4a
@@ -303,22 +542,69 @@ extern "C" int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in
         set_error("bits 16 is g4a_gemv_f16");
         return G4A_EUNSUPPORTED;
     }
-    return qgemv_impl(bits, n_in, n_out, x, in_q, w_bits, w_scale, out_q, out, stream);
+    const int rc = qgemv_check(bits, n_in, n_out, x, w_bits, w_scale, out, in_q, out_q);
+    if (rc != G4A_OK) return rc;
+    QgemvArgs g = qgemv_args(n_in, n_out, x, in_q, w_bits, w_scale, out_q, out);
+    return qgemv_run(bits, 0, g, stream);
+}
+
+extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
+                               const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
+                               const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
+                               void* stream) {
+    if (bits == 16) {
+        set_error("bits 16 not supported for the gate/up pair");
+        return G4A_EUNSUPPORTED;
+    }
+    int rc = qgemv_check(bits, n_in, n_out, x, gate_bits, gate_scale, out, gate_in_q, gate_out_q);
+    if (rc == G4A_OK) rc = qgemv_check(bits, n_in, n_out, x, up_bits, up_scale, out, up_in_q, up_out_q);
+    if (rc != G4A_OK) return rc;
+    if (!(out_q >= 0.0f)) {
+        set_error("out_q must be >= 0");
+        return G4A_EINVAL;
+    }
+    QgemvArgs g = qgemv_args(n_in, n_out, x, gate_in_q, gate_bits, gate_scale, gate_out_q, out);
+    g.w2 = up_bits;
+    g.scale2 = up_scale;
+    g.in_q2 = up_in_q;
+    g.out_q2 = up_out_q;
+    g.epi_q = out_q;
+    return qgemv_run(bits, 1, g, stream);
+}
+
+extern "C" int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
+                                  const float* w_scale, float out_q, const float* mul, float* out, void* stream) {
+    if (bits == 16) {
+        set_error("bits 16 not supported with the gelu epilogue");
+        return G4A_EUNSUPPORTED;
+    }
+    const int rc = qgemv_check(bits, n_in, n_out, x, w_bits, w_scale, out, in_q, out_q);
+    if (rc != G4A_OK) return rc;
+    if (!mul) {
+        set_error("mul must be non-NULL");
+        return G4A_EINVAL;
+    }
+    QgemvArgs g = qgemv_args(n_in, n_out, x, in_q, w_bits, w_scale, out_q, out);
+    g.mul = mul;
+    return qgemv_run(bits, 2, g, stream);
 }
 
 extern "C" int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* out, void* stream) {
-    return qgemv_impl(16, n_in, n_out, x, 0.0f, (const uint32_t*)w_f16, nullptr, 0.0f, out, stream);
+    const int rc = qgemv_check(16, n_in, n_out, x, (const uint32_t*)w_f16, nullptr, out, 0.0f, 0.0f);
+    if (rc != G4A_OK) return rc;
+    QgemvArgs g = qgemv_args(n_in, n_out, x, 0.0f, (const uint32_t*)w_f16, nullptr, 0.0f, out);
+    return qgemv_run(16, 0, g, stream);
 }
 
 extern "C" int g4a_rms_norm(int n_rows, int n, const float* x, float pre, const float* w, const float* res,
-                            float mult, float eps, float* out, float q2, int f16_2, float* out2, float* sum2,
-                            void* stream) {
+                            float mult, float eps, float* out, const float* w2, float q2, int f16_2, float* out2,
+                            float* sum2, void* stream) {
     if (n_rows <= 0 || n <= 0 || n_rows > 65535) {
         set_error("n_rows (%d) must be in [1, 65535] and n (%d) positive", n_rows, n);
         return G4A_EINVAL;
     }
-    if (!x || !out || (sum2 && !out2)) {
-        set_error("x and out (and out2 when sum2 is given) must be non-NULL");
+    if (!x || !out || (sum2 && !out2) || (w2 && !out2)) {
+        set_error("x and out (and out2 when w2 or sum2 is given) must be non-NULL");
         return G4A_EINVAL;
     }
     if (!(eps >= 0.0f) || !(q2 >= 0.0f)) {
@@ -329,6 +615,7 @@ extern "C" int g4a_rms_norm(int n_rows, int n, const float* x, float pre, const 
     a.x = x;
     a.w = w;
     a.res = res;
+    a.w2 = w2;
     a.out = out;
     a.out2 = out2;
     a.sum2 = sum2;
@@ -338,8 +625,13 @@ extern "C" int g4a_rms_norm(int n_rows, int n, const float* x, float pre, const 
     a.eps = eps;
     a.q2 = q2;
     a.f16_2 = f16_2 != 0;
-    const int threads = n >= 4096 ? 1024 : n >= 1024 ? 512 : 256;
-    hipLaunchKernelGGL(rms_kernel, dim3(n_rows), dim3(threads), 0, (hipStream_t)stream, a);
+    if (n > 16384) {
+        set_error("n (%d) above 16384", n);
+        return G4A_EINVAL;
+    }
+    const int threads = n > 4096 ? 1024 : 256, per = (n + threads - 1) / threads;
+    auto fn = per <= 2 ? rms_kernel<2> : per <= 4 ? rms_kernel<4> : per <= 8 ? rms_kernel<8> : rms_kernel<16>;
+    hipLaunchKernelGGL(fn, dim3(n_rows), dim3(threads), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "rms_norm launch");
     return G4A_OK;
@@ -383,13 +675,27 @@ extern "C" int g4a_embed(int bits, int n, const void* table, int64_t n_rows, con
     return G4A_OK;
 }
 
-extern "C" int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* stream) {
+extern "C" size_t g4a_softcap_argmax_ws_bytes(int n) {
+    return n > 0 ? (size_t)((n + kArgChunk - 1) / kArgChunk) * sizeof(float2) : 0;
+}
+
+extern "C" int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* ws, size_t ws_bytes,
+                                  void* stream) {
     if (n <= 0 || !logits || !tok || !(cap >= 0.0f)) {
         set_error("n must be positive, logits and tok non-NULL, cap >= 0");
         return G4A_EINVAL;
     }
-    hipLaunchKernelGGL(softcap_argmax_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, n, logits, cap, tok);
+    const int nb = (n + kArgChunk - 1) / kArgChunk;
+    if (!ws || ws_bytes < (size_t)nb * sizeof(float2) || (uintptr_t)ws % 8 || (uintptr_t)logits % 16) {
+        set_error("softcap_argmax needs %zu workspace bytes (8-byte aligned) and 16-byte aligned logits",
+                  (size_t)nb * sizeof(float2));
+        return G4A_EWORKSPACE;
+    }
+    hipLaunchKernelGGL(softcap_part_kernel, dim3(nb), dim3(256), 0, (hipStream_t)stream, n, logits, cap, (float2*)ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "softcap_argmax launch");
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, nb, (const float2*)ws, tok);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "argmax launch");
     return G4A_OK;
 }

@@ -26,7 +26,8 @@ from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
 from .projection import packed_bits
 
-__all__ = ["qgemv", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax", "DecoderStack", "EPS"]
+__all__ = ["qgemv", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
+           "DecoderStack", "EPS"]
 
 EPS = 1e-6  # reference.py:27
 _WORDS = (torch.int32, torch.uint32)
@@ -46,6 +47,35 @@ def qgemv(x, words, scale, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: f
     return out
 
 
+def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int | None = None, out=None):
+    """out = srq(gelu(qgemv(x, *gate)) * qgemv(x, *up), out_q) in one pass (gateup_74/95,
+    reference.py:176-181); gate and up are (words, scale, in_q, out_q)."""
+    (gw, gs, gi, go), (uw, us, ui, uo) = gate, up
+    _need(x, "x", torch.float32)
+    for t, n in ((gw, "gate words"), (uw, "up words")):
+        _need(t, n, _WORDS)
+    bits = bits or packed_bits(gw, n_in, n_out)
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
+    check(_lib.load().g4a_qgemv_geglu(bits, n_in, n_out, _ptr(x), _ptr(gw), _ptr(gs), float(gi), float(go), _ptr(uw),
+                                      _ptr(us), float(ui), float(uo), float(out_q), _ptr(out), _stream()))
+    return out
+
+
+def qgemv_gelu_mul(x, words, scale, mul, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: float = 0.0,
+                   bits: int | None = None, out=None):
+    """out = gelu(qgemv(x)) * mul (plegate_76; reference.py:186-187)."""
+    _need(x, "x", torch.float32)
+    _need(words, "words", _WORDS)
+    _need(mul, "mul", torch.float32)
+    bits = bits or packed_bits(words, n_in, n_out)
+    if out is None:
+        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
+    check(_lib.load().g4a_qgemv_gelu_mul(bits, n_in, n_out, _ptr(x), float(in_q), _ptr(words), _ptr(scale),
+                                         float(out_q), _ptr(mul), _ptr(out), _stream()))
+    return out
+
+
 def gemv_f16(x, w_f16, out=None):
     """out = w @ x, w f16 [n_out][n_in], f32 accumulation (reference.py:136)."""
     _need(x, "x", torch.float32)
@@ -58,20 +88,21 @@ def gemv_f16(x, w_f16, out=None):
 
 
 def rms_norm(x, w=None, *, res=None, pre: float = 1.0, mult: float = 1.0, eps: float = EPS, out=None,
-             q2: float | None = None, f16_2: bool = False, out2=None, sum2=None):
-    """Rows of x [.., n]: out = (res + rms(x * pre) * w) * mult; optional out2 = srq(out, q2)
-    (f16_2: f16(srq(f16(out), q2))) and sum2 = sum of out2 per row (reference.py:38-43)."""
+             w2=None, q2: float | None = None, f16_2: bool = False, out2=None, sum2=None):
+    """Rows of x [.., n]: out = (res + rms(x * pre) * w) * mult; optional out2 = srq(z, q2)
+    (f16_2: f16(srq(f16(z), q2))) with z = out or, given w2, z = rms(out) * w2, and sum2 =
+    sum of out2 per row (reference.py:38-43)."""
     _need(x, "x", torch.float32)
     n = x.shape[-1]
     rows = x.numel() // n
     if out is None:
         out = torch.empty_like(x)
-    if q2 is not None and out2 is None:
+    if (q2 is not None or w2 is not None) and out2 is None:
         out2 = torch.empty_like(x)
     lib = _lib.load()
     check(lib.g4a_rms_norm(rows, n, _ptr(x), float(pre), _ptr(w) if w is not None else None,
                            _ptr(res) if res is not None else None, float(mult), float(eps), _ptr(out),
-                           float(q2 or 0.0), int(f16_2), _ptr(out2) if out2 is not None else None,
+                           _ptr(w2) if w2 is not None else None, float(q2 or 0.0), int(f16_2), _ptr(out2) if out2 is not None else None,
                            _ptr(sum2) if sum2 is not None else None, _stream()))
     return (out, out2) if out2 is not None else out
 
@@ -98,12 +129,17 @@ def embed(table_u8, tok, row_scale, n: int, bits: int, group: int, mult: float, 
     return out
 
 
-def softcap_argmax(logits, cap: float, tok=None):
-    """logits <- cap * tanh(logits / cap) in place; tok[0] = first argmax (reference.py:207)."""
+def softcap_argmax(logits, cap: float, tok=None, ws=None):
+    """logits <- cap * tanh(logits / cap) in place; tok[0] = first argmax (reference.py:207).
+    ws: a byte tensor of at least g4a_softcap_argmax_ws_bytes(n) (allocated when absent)."""
     _need(logits, "logits", torch.float32)
+    lib = _lib.load()
     if tok is None:
         tok = torch.empty(1, dtype=torch.int32, device=logits.device)
-    check(_lib.load().g4a_softcap_argmax(logits.numel(), _ptr(logits), float(cap), _ptr(tok), _stream()))
+    if ws is None:
+        ws = torch.empty(lib.g4a_softcap_argmax_ws_bytes(logits.numel()), dtype=torch.uint8, device=logits.device)
+    check(lib.g4a_softcap_argmax(logits.numel(), _ptr(logits), float(cap), _ptr(tok), _ptr(ws), ws.numel(),
+                                 _stream()))
     return tok
 
 
@@ -170,70 +206,80 @@ class DecoderStack:
         f32 = lambda *shape: torch.zeros(*shape, dtype=torch.float32, device=device)  # noqa: E731
         inter = max(s.intermediate for s in man.layers)
         self.x, self.h, self.a, self.sum_a = f32(H), f32(H), f32(H), f32(1)
-        self.o, self.y2 = f32(H), f32(H)
-        self.gate, self.up, self.gg = f32(inter), f32(inter), f32(inter)
+        self.o, self.y2, self.hf = f32(H), f32(H), f32(H)
+        self.gg = f32(inter)
         self.down = f32(H)
         self.ple_tab, self.ple_proj, self.ple_in = f32(self.nL, self.d), f32(self.nL * self.d), f32(self.nL, self.d)
-        self.plegate, self.pleg, self.pleproj = f32(self.d), f32(self.d), f32(H)
+        self.pleg, self.pleproj = f32(self.d), f32(H)
         self.logits = f32(self.vocab)
+        self.arg_ws = torch.empty(_lib.load().g4a_softcap_argmax_ws_bytes(self.vocab), dtype=torch.uint8,
+                                  device=device)
         self.tok = torch.zeros(1, dtype=torch.int32, device=device)
 
     def embed_token(self):
-        """x = embed(tok), ple_in = ple_input(tok, x) (reference.py:114-139)."""
+        """x = embed(tok), ple_in = ple_input(tok, x), and layer 0's srq'd input norm
+        (reference.py:114-139, 145-147)."""
         H, nL, d = self.H, self.nL, self.d
         embed(self.embed_q, self.tok, self.embed_sc, H, 2, H, self.embed_scale, out=self.x)
         embed(self.ple_q, self.tok, self.ple_sc, nL * d, 4, d, self.ple_scale, out=self.ple_tab.view(-1))
         gemv_f16(self.x, self.pl_proj, out=self.ple_proj)
         rms_norm(self.ple_proj.view(nL, d), self.pl_norm, res=self.ple_tab, pre=H ** -0.5, mult=2.0 ** -0.5,
                  out=self.ple_in)
+        rms_norm(self.x, self.w[0]["in_norm"], out=self.h, q2=self.man.layers[0].scales["qkv_in"], out2=self.a,
+                 sum2=self.sum_a)
 
     def layer(self, L: int, pos: int, trace: dict | None = None):
-        """Layer L on self.x in place (reference.py:141-191)."""
+        """Layer L on self.x in place (reference.py:141-191), from its srq'd input norm in
+        self.a / self.sum_a; it leaves the next layer's (or, last, the final norm in self.hf).
+        The norms ride on the kernels after the adds as the runner fuses them (oproj_73 ends
+        with the pre-FFN norm, pleproj_77 with the next layer's input norm)."""
         s, w, H = self.man.layers[L], self.w[L], self.H
         sc, inter = s.scales, s.intermediate
         snap = (lambda k, t: trace.__setitem__(k, t.clone())) if trace is not None else (lambda k, t: None)
         snap("x0", self.x)
-        rms_norm(self.x, w["in_norm"], out=self.h, q2=sc["qkv_in"], out2=self.a, sum2=self.sum_a)
         snap("a", self.a)
         attn = self.attn.decode_layer(L, pos, self.a, self.sum_a).view(-1)
         snap("attn", attn)
-        qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=sc["o_in"], out_q=sc["o_out"], bits=w["o_bits_n"],
+        # inputs already on their step's grid skip the GEMV's srq (srq(srq(v, s), s) = srq(v, s)
+        # exactly): the attention output carries o_in, the GeGLU output down_in
+        qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=0.0, out_q=sc["o_out"], bits=w["o_bits_n"],
               out=self.o)
         snap("o", self.o)
-        rms_norm(self.o, w["o_w1"], res=self.x, out=self.x)
+        rms_norm(self.o, w["o_w1"], res=self.x, out=self.x, w2=w["o_w2"], q2=sc["gate_in"], f16_2=True, out2=self.y2)
         snap("x1", self.x)
-        rms_norm(self.x, w["o_w2"], out=self.h, q2=sc["gate_in"], f16_2=True, out2=self.y2)
         snap("y2", self.y2)
-        gb = w["gate_bits_n"]
-        gate, up, gg = self.gate[:inter], self.up[:inter], self.gg[:inter]
-        qgemv(self.y2, w["gate_bits"], w["gate_scale"], H, inter, in_q=sc["gate_in"], out_q=sc["gate_out"], bits=gb,
-              out=gate)
-        qgemv(self.y2, w["up_bits"], w["up_scale"], H, inter, in_q=sc["up_in"], out_q=sc["up_out"], bits=gb, out=up)
-        snap("gate", gate)
-        snap("up", up)
-        geglu(gate, up, sc["down_in"], out=gg)
+        gg = self.gg[:inter]
+        qgemv_geglu(self.y2, (w["gate_bits"], w["gate_scale"], sc["gate_in"], sc["gate_out"]),
+                    (w["up_bits"], w["up_scale"], sc["up_in"], sc["up_out"]), H, inter, out_q=sc["down_in"],
+                    bits=w["gate_bits_n"], out=gg)
         snap("geglu", gg)
-        qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=sc["down_in"], out_q=sc["down_out"],
+        qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=0.0, out_q=sc["down_out"],
               bits=w["down_bits_n"], out=self.down)
         snap("down", self.down)
         rms_norm(self.down, w["down_nw"], res=self.x, out=self.x)
         snap("x2", self.x)
-        qgemv(self.x, w["plegate_codes"], w["plegate_rowscale"], H, self.d, in_q=sc["plegate_in"],
-              out_q=sc["plegate_out"], bits=8, out=self.plegate)
-        snap("plegate", self.plegate)
-        geglu(self.plegate, self.ple_in[L], 0.0, out=self.pleg)
+        qgemv_gelu_mul(self.x, w["plegate_codes"], w["plegate_rowscale"], self.ple_in[L], H, self.d,
+                       in_q=sc["plegate_in"], out_q=sc["plegate_out"], bits=8, out=self.pleg)
         snap("pleg", self.pleg)
         qgemv(self.pleg, w["pleproj_codes"], w["pleproj_rowscale"], self.d, H, in_q=sc["pleproj_in"],
               out_q=sc["pleproj_out"], bits=8, out=self.pleproj)
         snap("pleproj", self.pleproj)
-        rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x)
-        snap("x3", self.x)
+        if L + 1 < self.nL:
+            rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x,
+                     w2=self.w[L + 1]["in_norm"], q2=self.man.layers[L + 1].scales["qkv_in"], out2=self.a,
+                     sum2=self.sum_a)
+            snap("x3", self.x)
+            snap("a_next", self.a)
+        else:
+            rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x,
+                     w2=self.final_norm, out2=self.hf)
+            snap("x3", self.x)
+            snap("hf", self.hf)
 
     def head(self):
-        """Final norm, 2-bit lm_head, softcap and argmax into self.tok (reference.py:200-207)."""
-        rms_norm(self.x, self.final_norm, out=self.h)
-        qgemv(self.h, self.lm_rows, self.lm_sc, self.H, self.vocab, bits=2, out=self.logits)
-        softcap_argmax(self.logits, self.softcap, tok=self.tok)
+        """2-bit lm_head over the final norm, softcap and argmax into self.tok (reference.py:200-207)."""
+        qgemv(self.hf, self.lm_rows, self.lm_sc, self.H, self.vocab, bits=2, out=self.logits)
+        softcap_argmax(self.logits, self.softcap, tok=self.tok, ws=self.arg_ws)
 
     def step(self, pos: int, trace: list | None = None):
         """One token at position pos: self.tok in, the next token in self.tok out."""

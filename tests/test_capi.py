@@ -184,11 +184,12 @@ def test_decoder_argument_errors(lib):
     assert b"multiple" in lib.g4a_last_error()
     # rms_norm: rows, NULLs, sum2 without out2, negative eps
     args = lambda **k: [k.get(n, d) for n, d in (("rows", 1), ("n", 64), ("x", FAKE), ("pre", f(1)), ("w", None),  # noqa: E731
-                        ("res", None), ("mult", f(1)), ("eps", f(1e-6)), ("out", FAKE), ("q2", f(0)), ("f16", 0),
+                        ("res", None), ("mult", f(1)), ("eps", f(1e-6)), ("out", FAKE), ("w2", None), ("q2", f(0)), ("f16", 0),
                         ("out2", None), ("sum2", None), ("s", None))]
     assert lib.g4a_rms_norm(*args(rows=0)) == E
     assert lib.g4a_rms_norm(*args(x=None)) == E
     assert lib.g4a_rms_norm(*args(sum2=FAKE)) == E
+    assert lib.g4a_rms_norm(*args(w2=FAKE)) == E                                        # w2 without out2
     assert lib.g4a_rms_norm(*args(eps=f(-1))) == E
     assert lib.g4a_geglu(0, FAKE, FAKE, f(0), FAKE, None) == E
     assert lib.g4a_geglu(8, FAKE, FAKE, f(-0.5), FAKE, None) == E
@@ -196,5 +197,13 @@ def test_decoder_argument_errors(lib):
     assert lib.g4a_embed(3, 64, FAKE, 8, FAKE, FAKE, 64, f(1), FAKE, None) == U
     assert lib.g4a_embed(2, 64, FAKE, 8, FAKE, FAKE, 48, f(1), FAKE, None) == E
     assert lib.g4a_embed(2, 64, FAKE, 8, None, FAKE, 64, f(1), FAKE, None) == E
-    assert lib.g4a_softcap_argmax(0, FAKE, f(30), FAKE, None) == E
-    assert lib.g4a_softcap_argmax(8, FAKE, f(-1), FAKE, None) == E
+    assert lib.g4a_softcap_argmax(0, FAKE, f(30), FAKE, FAKE, 64, None) == E
+    assert lib.g4a_softcap_argmax(8, FAKE, f(-1), FAKE, FAKE, 64, None) == E
+    assert lib.g4a_softcap_argmax_ws_bytes(262144) == 64 * 8 and lib.g4a_softcap_argmax_ws_bytes(0) == 0
+    assert lib.g4a_softcap_argmax(262144, FAKE, f(30), FAKE, FAKE, 511, None) == -3        # workspace
+    # fused GEMV variants: the same checks, and their own operands
+    assert lib.g4a_qgemv_geglu(4, 48, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(0), FAKE, None) == E
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, None, f(0), f(0), f(0), FAKE, None) == E
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(-1), FAKE, None) == E
+    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), None, FAKE, None) == E
+    assert lib.g4a_qgemv_gelu_mul(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, FAKE, None) == U
