@@ -245,6 +245,26 @@ int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* 
 int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
               const float* w_scale, float out_q, float* out, void* stream);
 /*
+ * Optional norm prologue of the two fused GEMVs below: the residual add and norm(s) in front
+ * of them, done by every workgroup while it stages x (the runner's kernels fuse them the
+ * same way, oproj_73 ending with the pre-FFN norm), so no kernel of its own runs:
+ *   x = res + a / sqrt(mean(a^2) + eps) * w1          (stored to x_out by one workgroup)
+ *   z = x / sqrt(mean(x^2) + eps) * w2, or z = x when w2 is NULL
+ *   GEMV input = f16 ? f16(srq(f16(z), q2)) : srq(z, q2)   (stored to z_out if non-NULL)
+ * n_in <= 2048; x_out must not alias a, res or w1 (other workgroups still read them).
+ */
+typedef struct {
+    const float* a;
+    const float* res;
+    const float* w1;
+    const float* w2;
+    float* x_out;
+    float* z_out;
+    float q2;
+    int f16;
+    float eps;
+} g4a_norm_in;
+/*
  * The MLP's gate/up pair with its GeGLU in one pass over x (gateup_74/95; reference.py:176-181):
  *   out[o] = srq(gelu_tanh(g[o]) * u[o], out_q),
  *   g = the g4a_qgemv output of the gate rows (gate_in_q, gate_out_q), u that of the up rows.
@@ -252,11 +272,12 @@ int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const u
 int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
                     const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
                     const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
-                    void* stream);
+                    const g4a_norm_in* pro, void* stream);
 /* g4a_qgemv with the per-layer-embedding gate's epilogue: out[o] = gelu_tanh(y[o]) * mul[o]
- * (plegate_76; reference.py:186-187, mul = the layer's per-layer input). */
+ * (plegate_76; reference.py:186-187, mul = the layer's per-layer input). pro as above. */
 int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
-                       const float* w_scale, float out_q, const float* mul, float* out, void* stream);
+                       const float* w_scale, float out_q, const float* mul, float* out,
+                       const g4a_norm_in* pro, void* stream);
 /* Dense f16 GEMV: out[o] = sum_i w[o][i] x[i] in f32 (the per-layer-input projection,
  * reference.py:136, exported f16 by export.py:95). n_in a multiple of 8. */
 int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* out, void* stream);

@@ -55,6 +55,21 @@ class G4AGemmMat(ctypes.Structure):
     ]
 
 
+class G4ANormIn(ctypes.Structure):
+    """struct g4a_norm_in: the residual-add + norm prologue of the fused GEMVs."""
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("res", ctypes.c_void_p),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("x_out", ctypes.c_void_p),
+        ("z_out", ctypes.c_void_p),
+        ("q2", ctypes.c_float),
+        ("f16", ctypes.c_int),
+        ("eps", ctypes.c_float),
+    ]
+
+
 class G4AError(RuntimeError):
     """A libg4attn call returned an error code."""
 
@@ -116,9 +131,10 @@ def load() -> ctypes.CDLL:
     lib.g4a_gemv_f16.argtypes = [i, i, P, P, P, P]
     lib.g4a_rms_norm.restype = ctypes.c_int
     lib.g4a_qgemv_geglu.restype = ctypes.c_int
-    lib.g4a_qgemv_geglu.argtypes = [i, i, i, P, P, P, f, f, P, P, f, f, f, P, P]
+    npro = ctypes.POINTER(G4ANormIn)
+    lib.g4a_qgemv_geglu.argtypes = [i, i, i, P, P, P, f, f, P, P, f, f, f, P, npro, P]
     lib.g4a_qgemv_gelu_mul.restype = ctypes.c_int
-    lib.g4a_qgemv_gelu_mul.argtypes = [i, i, i, P, f, P, P, f, P, P, P]
+    lib.g4a_qgemv_gelu_mul.argtypes = [i, i, i, P, f, P, P, f, P, P, npro, P]
     lib.g4a_rms_norm.argtypes = [i, i, P, f, P, P, f, f, P, P, f, i, P, P, P]
     lib.g4a_geglu.restype = ctypes.c_int
     lib.g4a_geglu.argtypes = [i, P, P, f, P, P]

@@ -38,7 +38,29 @@ struct QgemvArgs {
     const float* scale2;
     float in_q2, out_q2, epi_q;
     const float* mul;  // EPI 2
+    // norm prologue (pa != NULL, staged kernels only): x = res + rms(pa) * w1, stored to xout by
+    // workgroup 0; z = rms(x) * w2 (w2 != NULL) or x; the GEMV input is f16 ? f16(srq(f16(z),
+    // q2)) : srq(z, q2), stored to zout (if given) by workgroup 0 -- the rms_kernel arithmetic
+    const float* pa;
+    const float* pres;
+    const float* pw1;
+    const float* pw2;
+    float* pxout;
+    float* pzout;
+    float pq2, peps;
+    int pf16;
 };
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();  // red may still be read from a previous reduction
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
 
 __device__ __forceinline__ float gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
@@ -130,8 +152,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) sx[m] = 0.0f;
     float* xsf = reinterpret_cast<float*>(xs);
-    for (int i = tid; STAGE && i < n_in; i += 256) {
-        const float v = g.x[i];
+    auto stage = [&](int i, float v) {
         const int c = i / VPC, e = i % VPC;
         const int at = ((e >> 2) * nch + c) * 4 + (e & 3);
 #pragma unroll
@@ -140,6 +161,48 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
             xsf[m * n_in + at] = q;
             sx[m] += q;
         }
+    };
+    if (STAGE && g.pa) {  // workgroup-uniform; n_in <= 2048
+        constexpr int PER = 8;
+        __shared__ float pred[16];
+        float av[PER], rv[PER], w1v[PER], w2v[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + 256 * k;
+            const bool ok = i < n_in;
+            av[k] = ok ? g.pa[i] : 0.0f;
+            rv[k] = ok ? g.pres[i] : 0.0f;
+            w1v[k] = ok ? g.pw1[i] : 1.0f;
+            w2v[k] = ok && g.pw2 ? g.pw2[i] : 1.0f;
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(av[k], av[k], ss);
+        const float d = sqrtf(block_sum(ss, pred) / (float)n_in + g.peps);
+        float ss2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + 256 * k;
+            const float y = rv[k] + av[k] / d * w1v[k];
+            av[k] = y;
+            if (i < n_in) {
+                if (blockIdx.x == 0) g.pxout[i] = y;
+                ss2 = __builtin_fmaf(y, y, ss2);
+            }
+        }
+        const float d2 = g.pw2 ? sqrtf(block_sum(ss2, pred) / (float)n_in + g.peps) : 1.0f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + 256 * k;
+            const float z = g.pw2 ? av[k] / d2 * w2v[k] : av[k];
+            const float zq = g.pf16 ? (float)(half_t)srq((float)(half_t)z, g.pq2) : srq(z, g.pq2);
+            if (i < n_in) {
+                if (blockIdx.x == 0 && g.pzout) g.pzout[i] = zq;
+                stage(i, zq);
+            }
+        }
+    } else {
+        for (int i = tid; STAGE && i < n_in; i += 256) stage(i, g.x[i]);
     }
     if constexpr (STAGE) {
 #pragma unroll
@@ -263,17 +326,6 @@ struct RmsArgs {
     float pre, mult, eps, q2;
     int f16_2;
 };
-
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();  // red may still be read from a previous reduction
-    if ((threadIdx.x & 63) == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.0f;
-    for (int i = 0; i < nw; ++i) t += red[i];
-    return t;
-}
 
 // Thread t holds elements t + k*blockDim (k < PER) in registers: every operand is loaded
 // once, up front, and the three sums cost only LDS round trips.
@@ -455,6 +507,7 @@ static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
 template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
+    if (g.pa) return c <= 16 ? launch_qgemv<BITS, 16, 2, EPI>(g, s) : launch_qgemv<BITS, 64, 2, EPI>(g, s);  // staged
     if (c <= 16) return launch_qgemv<BITS, 16, 2, EPI>(g, s);
     if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
     if (c <= 64) return launch_qgemv<BITS, 64, 2, EPI>(g, s);
@@ -518,6 +571,25 @@ static int qgemv_run(int bits, int epi, QgemvArgs& g, void* stream) {
     return G4A_OK;
 }
 
+// the norm prologue: checks and arguments (x is then unused)
+static int norm_in_set(const g4a_norm_in* pro, int n_in, QgemvArgs& g) {
+    if (!pro) return G4A_OK;
+    if (!pro->a || !pro->res || !pro->w1 || !pro->x_out || n_in > 2048 || !(pro->q2 >= 0.0f) || !(pro->eps >= 0.0f)) {
+        set_error("norm prologue: a, res, w1, x_out non-NULL, n_in <= 2048, q2 and eps >= 0");
+        return G4A_EINVAL;
+    }
+    g.pa = pro->a;
+    g.pres = pro->res;
+    g.pw1 = pro->w1;
+    g.pw2 = pro->w2;
+    g.pxout = pro->x_out;
+    g.pzout = pro->z_out;
+    g.pq2 = pro->q2;
+    g.peps = pro->eps;
+    g.pf16 = pro->f16 != 0;
+    return G4A_OK;
+}
+
 static QgemvArgs qgemv_args(int n_in, int n_out, const float* x, float in_q, const uint32_t* w, const float* scale,
                             float out_q, float* out) {
     QgemvArgs g{};
@@ -551,7 +623,8 @@ extern "C" int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in
 extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
                                const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
                                const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
-                               void* stream) {
+                               const g4a_norm_in* pro, void* stream) {
+    if (pro && pro->a) x = pro->a;  // checked as the input; the prologue makes the real one
     if (bits == 16) {
         set_error("bits 16 not supported for the gate/up pair");
         return G4A_EUNSUPPORTED;
@@ -564,6 +637,7 @@ extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, co
         return G4A_EINVAL;
     }
     QgemvArgs g = qgemv_args(n_in, n_out, x, gate_in_q, gate_bits, gate_scale, gate_out_q, out);
+    if ((rc = norm_in_set(pro, n_in, g)) != G4A_OK) return rc;
     g.w2 = up_bits;
     g.scale2 = up_scale;
     g.in_q2 = up_in_q;
@@ -573,18 +647,21 @@ extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, co
 }
 
 extern "C" int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
-                                  const float* w_scale, float out_q, const float* mul, float* out, void* stream) {
+                                  const float* w_scale, float out_q, const float* mul, float* out,
+                                  const g4a_norm_in* pro, void* stream) {
+    if (pro && pro->a) x = pro->a;
     if (bits == 16) {
         set_error("bits 16 not supported with the gelu epilogue");
         return G4A_EUNSUPPORTED;
     }
-    const int rc = qgemv_check(bits, n_in, n_out, x, w_bits, w_scale, out, in_q, out_q);
+    int rc = qgemv_check(bits, n_in, n_out, x, w_bits, w_scale, out, in_q, out_q);
     if (rc != G4A_OK) return rc;
     if (!mul) {
         set_error("mul must be non-NULL");
         return G4A_EINVAL;
     }
     QgemvArgs g = qgemv_args(n_in, n_out, x, in_q, w_bits, w_scale, out_q, out);
+    if ((rc = norm_in_set(pro, n_in, g)) != G4A_OK) return rc;
     g.mul = mul;
     return qgemv_run(bits, 2, g, stream);
 }

@@ -17,6 +17,8 @@ Every call is asynchronous on torch's current stream; nothing is computed on the
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -26,7 +28,7 @@ from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
 from .projection import packed_bits
 
-__all__ = ["qgemv", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
+__all__ = ["qgemv", "norm_in", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
            "DecoderStack", "EPS"]
 
 EPS = 1e-6  # reference.py:27
@@ -47,32 +49,48 @@ def qgemv(x, words, scale, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: f
     return out
 
 
-def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int | None = None, out=None):
+def norm_in(a, res, w1, x_out, *, w2=None, z_out=None, q2: float = 0.0, f16: bool = False, eps: float = EPS):
+    """The residual-add + norm prologue of the fused GEMVs (struct g4a_norm_in): their input
+    becomes srq(rms(res + rms(a) * w1) * w2, q2) (f16-rounded around the srq with f16), with
+    x = res + rms(a) * w1 stored to x_out (which must not alias a, res or w1)."""
+    for t, n in ((a, "a"), (res, "res"), (w1, "w1"), (x_out, "x_out")):
+        _need(t, n, torch.float32)
+    return _lib.G4ANormIn(_ptr(a), _ptr(res), _ptr(w1), _ptr(w2) if w2 is not None else None, _ptr(x_out),
+                          _ptr(z_out) if z_out is not None else None, float(q2), int(f16), float(eps))
+
+
+def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int | None = None, out=None,
+                pro=None):
     """out = srq(gelu(qgemv(x, *gate)) * qgemv(x, *up), out_q) in one pass (gateup_74/95,
-    reference.py:176-181); gate and up are (words, scale, in_q, out_q)."""
+    reference.py:176-181); gate and up are (words, scale, in_q, out_q). pro: a norm_in(...)
+    prologue that makes x (then x may be None)."""
     (gw, gs, gi, go), (uw, us, ui, uo) = gate, up
-    _need(x, "x", torch.float32)
+    if pro is None:
+        _need(x, "x", torch.float32)
     for t, n in ((gw, "gate words"), (uw, "up words")):
         _need(t, n, _WORDS)
     bits = bits or packed_bits(gw, n_in, n_out)
     if out is None:
-        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
-    check(_lib.load().g4a_qgemv_geglu(bits, n_in, n_out, _ptr(x), _ptr(gw), _ptr(gs), float(gi), float(go), _ptr(uw),
-                                      _ptr(us), float(ui), float(uo), float(out_q), _ptr(out), _stream()))
+        out = torch.empty(n_out, dtype=torch.float32, device=gw.device)
+    check(_lib.load().g4a_qgemv_geglu(bits, n_in, n_out, _ptr(x) if x is not None else None, _ptr(gw), _ptr(gs),
+                                      float(gi), float(go), _ptr(uw), _ptr(us), float(ui), float(uo), float(out_q),
+                                      _ptr(out), ctypes.byref(pro) if pro is not None else None, _stream()))
     return out
 
 
 def qgemv_gelu_mul(x, words, scale, mul, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: float = 0.0,
-                   bits: int | None = None, out=None):
-    """out = gelu(qgemv(x)) * mul (plegate_76; reference.py:186-187)."""
-    _need(x, "x", torch.float32)
+                   bits: int | None = None, out=None, pro=None):
+    """out = gelu(qgemv(x)) * mul (plegate_76; reference.py:186-187); pro as for qgemv_geglu."""
+    if pro is None:
+        _need(x, "x", torch.float32)
     _need(words, "words", _WORDS)
     _need(mul, "mul", torch.float32)
     bits = bits or packed_bits(words, n_in, n_out)
     if out is None:
-        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
-    check(_lib.load().g4a_qgemv_gelu_mul(bits, n_in, n_out, _ptr(x), float(in_q), _ptr(words), _ptr(scale),
-                                         float(out_q), _ptr(mul), _ptr(out), _stream()))
+        out = torch.empty(n_out, dtype=torch.float32, device=words.device)
+    check(_lib.load().g4a_qgemv_gelu_mul(bits, n_in, n_out, _ptr(x) if x is not None else None, float(in_q),
+                                         _ptr(words), _ptr(scale), float(out_q), _ptr(mul), _ptr(out),
+                                         ctypes.byref(pro) if pro is not None else None, _stream()))
     return out
 
 
@@ -206,7 +224,7 @@ class DecoderStack:
         f32 = lambda *shape: torch.zeros(*shape, dtype=torch.float32, device=device)  # noqa: E731
         inter = max(s.intermediate for s in man.layers)
         self.x, self.h, self.a, self.sum_a = f32(H), f32(H), f32(H), f32(1)
-        self.o, self.y2, self.hf = f32(H), f32(H), f32(H)
+        self.o, self.y2, self.hf, self.xb = f32(H), f32(H), f32(H), f32(H)
         self.gg = f32(inter)
         self.down = f32(H)
         self.ple_tab, self.ple_proj, self.ple_in = f32(self.nL, self.d), f32(self.nL * self.d), f32(self.nL, self.d)
@@ -245,21 +263,25 @@ class DecoderStack:
         qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=0.0, out_q=sc["o_out"], bits=w["o_bits_n"],
               out=self.o)
         snap("o", self.o)
-        rms_norm(self.o, w["o_w1"], res=self.x, out=self.x, w2=w["o_w2"], q2=sc["gate_in"], f16_2=True, out2=self.y2)
-        snap("x1", self.x)
-        snap("y2", self.y2)
+        # x1 = x + rms(o) * w1 and the MLP input y2 = f16(srq(f16(rms(x1) * w2), gate_in)) are
+        # made by the gate/up kernel's prologue (x1 into the second residual buffer xb)
         gg = self.gg[:inter]
-        qgemv_geglu(self.y2, (w["gate_bits"], w["gate_scale"], sc["gate_in"], sc["gate_out"]),
+        qgemv_geglu(None, (w["gate_bits"], w["gate_scale"], sc["gate_in"], sc["gate_out"]),
                     (w["up_bits"], w["up_scale"], sc["up_in"], sc["up_out"]), H, inter, out_q=sc["down_in"],
-                    bits=w["gate_bits_n"], out=gg)
+                    bits=w["gate_bits_n"], out=gg,
+                    pro=norm_in(self.o, self.x, w["o_w1"], self.xb, w2=w["o_w2"], z_out=self.y2, q2=sc["gate_in"],
+                                f16=True))
+        snap("x1", self.xb)
+        snap("y2", self.y2)
         snap("geglu", gg)
         qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=0.0, out_q=sc["down_out"],
               bits=w["down_bits_n"], out=self.down)
         snap("down", self.down)
-        rms_norm(self.down, w["down_nw"], res=self.x, out=self.x)
+        # x2 = x1 + rms(down) * w: the per-layer-embedding gate kernel's prologue, back into x
+        qgemv_gelu_mul(None, w["plegate_codes"], w["plegate_rowscale"], self.ple_in[L], H, self.d,
+                       in_q=sc["plegate_in"], out_q=sc["plegate_out"], bits=8, out=self.pleg,
+                       pro=norm_in(self.down, self.xb, w["down_nw"], self.x))
         snap("x2", self.x)
-        qgemv_gelu_mul(self.x, w["plegate_codes"], w["plegate_rowscale"], self.ple_in[L], H, self.d,
-                       in_q=sc["plegate_in"], out_q=sc["plegate_out"], bits=8, out=self.pleg)
         snap("pleg", self.pleg)
         qgemv(self.pleg, w["pleproj_codes"], w["pleproj_rowscale"], self.d, H, in_q=sc["pleproj_in"],
               out_q=sc["pleproj_out"], bits=8, out=self.pleproj)

@@ -202,8 +202,13 @@ def test_decoder_argument_errors(lib):
     assert lib.g4a_softcap_argmax_ws_bytes(262144) == 64 * 8 and lib.g4a_softcap_argmax_ws_bytes(0) == 0
     assert lib.g4a_softcap_argmax(262144, FAKE, f(30), FAKE, FAKE, 511, None) == -3        # workspace
     # fused GEMV variants: the same checks, and their own operands
-    assert lib.g4a_qgemv_geglu(4, 48, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(0), FAKE, None) == E
-    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, None, f(0), f(0), f(0), FAKE, None) == E
-    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(-1), FAKE, None) == E
-    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), None, FAKE, None) == E
-    assert lib.g4a_qgemv_gelu_mul(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, FAKE, None) == U
+    assert lib.g4a_qgemv_geglu(4, 48, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(0), FAKE, None, None) == E
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, None, f(0), f(0), f(0), FAKE, None, None) == E
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(-1), FAKE, None,
+                               None) == E
+    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), None, FAKE, None, None) == E
+    assert lib.g4a_qgemv_gelu_mul(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, FAKE, None, None) == U
+    pro = _lib.G4ANormIn(FAKE.value, FAKE.value, None, None, FAKE.value, None, 0.0, 0, 1e-6)  # no w1
+    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
+    pro.w1 = FAKE.value
+    assert lib.g4a_qgemv_gelu_mul(4, 4096, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
