@@ -191,16 +191,19 @@ def _stage_checks(m, L, t, ple_in):
         contract_close(g["hf"], OD.rms_norm(g["x3"], m.tensor("final_norm")), what + " final norm")
 
 
-def test_decoder_steps_stage_by_stage(tmp_path):
-    """Three resident steps of a four-layer model (sliding hd 256 / global hd 512 with
-    partial RoPE, two KV-sharing layers, 4- and 2-bit MLPs): each step's token is the
-    previous step's argmax, read on the device."""
-    write_model(tmp_path, full=True, seed=11)
+@pytest.mark.parametrize("H,n_heads,ple_d,vocab,steps", [(256, 4, 32, 512, 3), (1536, 8, 256, 2048, 1)])
+def test_decoder_steps_stage_by_stage(tmp_path, H, n_heads, ple_d, vocab, steps):
+    """Resident steps of a four-layer model (sliding hd 256 / global hd 512 with partial
+    RoPE, two KV-sharing layers, 4- and 2-bit MLPs): each step's token is the previous
+    step's argmax, read on the device. The second case has E2B's widths (H 1536, 8 heads,
+    intermediate 6144, per-layer inputs 256): the norm prologues at full width, the 128-
+    and 256-thread GEMV row groups and the hd-512 o_proj rows."""
+    write_model(tmp_path, full=True, seed=11, H=H, n_heads=n_heads, ple_d=ple_d, vocab=vocab)
     m = load_manifest(tmp_path)
     st = D.DecoderStack(m, max_seq=64, device=DEV)
     st.tok.fill_(5)
     prev = 5
-    for pos in range(3):
+    for pos in range(steps):
         trace = []
         st.step(pos, trace=trace)
         torch.cuda.synchronize()
