@@ -21,9 +21,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // export.py:150-156, :200-206 lm_head). Rows are packed BITS-bit values, value i of a row at
 // bit BITS*(i % (32/BITS)) of word i / (32/BITS) (the loader's and dq_f16's order); zp =
 // 2^(BITS-1). BITS = 16: plain f16 rows (pl_model_proj), no zero point, no row scale.
-// A wave splits into 64/LPR lane groups; a group owns RPW rows and walks their 16-byte
-// chunks LPR at a time, so short rows (the 384-byte lm_head rows) keep most lanes busy and
-// each chunk of x is loaded and quantised once for RPW rows. Epilogues (EPI):
+// A workgroup splits into 256/T row groups of T threads (T = 16 .. 256, sized to the row);
+// a group owns RPW rows and walks their 16-byte chunks T at a time, so short rows (the
+// 384-byte lm_head rows) keep most threads busy and each chunk of x serves RPW rows.
+// Codes are decoded through byte lanes and the zero point comes out of the sum of x.
+// Epilogues (EPI):
 //   0  out = y
 //   1  gate/up pair (gateup_74/95): y_b from the second matrix, out = srq(gelu(y) * y_b, epi_q)
 //   2  out = gelu(y) * mul[o] (plegate_76: the gate times the layer's per-layer input)
