@@ -118,7 +118,8 @@ template <int BITS, int T, int RPW, int EPI>
 __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
     // T threads per row group (16..256, the chunks of a row spread over them), 256/T groups
     // per workgroup, RPW rows per group; groups wider than a wave reduce through LDS.
-    // With several groups per workgroup (T <= 64) x is quantised once per workgroup into LDS,
+    // With several groups per workgroup (T <= 64), or a norm prologue (which needs all of x in
+    // every workgroup anyway), x is quantised once per workgroup into LDS,
     // float4 i of chunk c at [i][c] (threads of a group read consecutive chunks: conflict-free),
     // one copy per matrix step; wider groups use each chunk of x in one thread only and load
     // it straight from memory.
@@ -126,10 +127,11 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
     constexpr int NGRP = 256 / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
     constexpr float ZP = BITS == 16 ? 0.0f : (float)(1 << (BITS - 1));
-    constexpr bool STAGE = T <= 64;
+    const bool stage = T <= 64 || g.pa != nullptr;  // workgroup-uniform
     extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
     __shared__ float red[T > 64 ? 4 : 1][NM][RPW];
     __shared__ float xsum_part[8][NM];
+    __shared__ float xsum_red[4][NM];
     const int tid = threadIdx.x;
     const int sub = tid % T, grp = tid / T;
     const int row0 = (blockIdx.x * NGRP + grp) * RPW;
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) sx[m] = 0.0f;
     float* xsf = reinterpret_cast<float*>(xs);
-    auto stage = [&](int i, float v) {
+    auto stage_x = [&](int i, float v) {
         const int c = i / VPC, e = i % VPC;
         const int at = ((e >> 2) * nch + c) * 4 + (e & 3);
 #pragma unroll
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
             sx[m] += q;
         }
     };
-    if (STAGE && g.pa) {  // workgroup-uniform; n_in <= 2048
+    if (g.pa) {  // workgroup-uniform; n_in <= 2048
         constexpr int PER = 8;
         __shared__ float pred[16];
         float av[PER], rv[PER], w1v[PER], w2v[PER];
@@ -200,19 +202,25 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
             const float zq = g.pf16 ? (float)(half_t)srq((float)(half_t)z, g.pq2) : srq(z, g.pq2);
             if (i < n_in) {
                 if (blockIdx.x == 0 && g.pzout) g.pzout[i] = zq;
-                stage(i, zq);
+                stage_x(i, zq);
             }
         }
     } else {
-        for (int i = tid; STAGE && i < n_in; i += 256) stage(i, g.x[i]);
+        for (int i = tid; stage && i < n_in; i += 256) stage_x(i, g.x[i]);
     }
-    if constexpr (STAGE) {
+    float xtot[NM];  // staged: the sum of the whole quantised x, known after the barrier
+    if (stage) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const float t = wave_sum(sx[m]);
             if ((tid & 63) == 0) xsum_part[tid >> 6][m] = t;
         }
         __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            xtot[m] = (xsum_part[0][m] + xsum_part[1][m]) + (xsum_part[2][m] + xsum_part[3][m]);
+            sx[m] = 0.0f;
+        }
     }
     const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
     float acc[NM][RPW];
@@ -222,7 +230,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
         for (int r = 0; r < RPW; ++r) acc[m][r] = 0.0f;
     for (int c = sub; c < nch; c += T) {
         if (c != sub) load_w(c);
-        if constexpr (STAGE) {
+        if (stage) {
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
     for (int m = 0; m < NM; ++m) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) acc[m][r] = group_sum<T >= 64 ? 64 : T>(acc[m][r]);
-        if constexpr (!STAGE) sx[m] = group_sum<64>(sx[m]);
+        sx[m] = group_sum<64>(sx[m]);  // direct loads only (0 when staged)
     }
     if constexpr (T > 64) {  // the group's waves through LDS (one group per 128/256 threads)
         const int wig = sub >> 6;  // wave in group
@@ -260,7 +268,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
             for (int m = 0; m < NM; ++m) {
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) red[slot][m][r] = acc[m][r];
-                xsum_part[slot][m] = sx[m];
+                xsum_red[slot][m] = sx[m];
             }
         }
         __syncthreads();
@@ -275,21 +283,14 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
             }
             float t = 0.0f;
 #pragma unroll
-            for (int k = 0; k < T / 64; ++k) t += xsum_part[(grp * (T / 64) + k) & 3][m];
+            for (int k = 0; k < T / 64; ++k) t += xsum_red[(grp * (T / 64) + k) & 3][m];
             sx[m] = t;
         }
     }
     float zsx[NM];  // zero point times the sum of the quantised x (over the whole row)
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-        float t = 0.0f;
-        if constexpr (STAGE) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) t += xsum_part[k][m];
-        } else {
-            t = sx[m];
-        }
-        zsx[m] = ZP * t;
+        zsx[m] = ZP * (stage ? xtot[m] : sx[m]);
     }
     // thread r of the group writes row r
 #pragma unroll
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(int n_part, const fl
 template <int BITS, int T, int RPW, int EPI>
 static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
     const int rows_per_wg = (256 / T) * RPW;
-    const size_t lds = T <= 64 ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
+    const size_t lds = T <= 64 || g.pa ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
     hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg),
                        dim3(256), lds, s, g);
     return hipGetLastError();
@@ -509,7 +510,6 @@ static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
 template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
-    if (g.pa) return c <= 16 ? launch_qgemv<BITS, 16, 2, EPI>(g, s) : launch_qgemv<BITS, 64, 2, EPI>(g, s);  // staged
     if (c <= 16) return launch_qgemv<BITS, 16, 2, EPI>(g, s);
     if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
     if (c <= 64) return launch_qgemv<BITS, 64, 2, EPI>(g, s);
