@@ -810,8 +810,11 @@ static prefill_fn pick_g(int G, bool kv32, bool out32, bool hilo) {
 using namespace g4a;
 
 // Key split for short prompts: when the query blocks alone give fewer than 2 workgroups
-// per CU, long causal rows are cut into pieces of split_tiles key tiles so that about one
-// piece per CU results (G4A_PREFILL_SPLIT_TILES: 0 automatic, -1 never, N tiles per piece).
+// per CU, long causal rows are cut into pieces of split_tiles key tiles, the longest block
+// into about six pieces (G4A_PREFILL_SPLIT_TILES: 0 automatic, -1 never, N tiles per piece).
+// Measured best piece sizes at 16 / 24 / 32 / 64 tiles in the longest block (S 1024, 1536,
+// 2048, 4096 global): 3 / 3-4 / 5 / 10-13 tiles; one piece per CU (3 / 5 / 9 / 33) was up
+// to 24 % slower beyond S 1024.
 struct PrefillSplit {
     int split_tiles, max_pieces, n_qblocks, total_pieces;
     size_t o_bytes, ml_bytes, q16_bytes, total;
@@ -832,18 +835,15 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     // preparation and merge only while the unsplit grid leaves most CUs idle (S 2048,
     // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27)
     if (mode == 0 && W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
-    long total = 0;
     int max_tiles = 0;
     for (int qb = 0; qb < p.n_qblocks; ++qb) {
         const int p0 = start_pos + qb * BQ;
         const int hi = p0 + BQ < start_pos + S ? p0 + BQ : start_pos + S;
         const int lo = W > 0 && p0 + 1 - W > 0 ? p0 + 1 - W : 0;
         const int nt = (hi - lo + KT - 1) / KT;
-        total += nt;
         if (nt > max_tiles) max_tiles = nt;
     }
-    total *= kvH;
-    int st = mode > 0 ? mode : (int)((total + 255) / 256);
+    int st = mode > 0 ? mode : (max_tiles * 5 + 31) / 32;
     if (st < 2) st = 2;
     if (st < (max_tiles + 7) / 8) st = (max_tiles + 7) / 8;  // the merge takes <= 8 pieces
     const int pieces = (max_tiles + st - 1) / st;
