@@ -13,8 +13,9 @@ prefill (S 1024, global and W 512, TFLOP/s of 4*hd*nH*attended-pairs), config 4
 (16 sequences, KV ~ U[1024, 32768]), the q/k/v producer in front of the path (decode
 4-bit GEMV at the config-2 layer shape, prefill projection GEMMs at config 3) and the
 config-5 35-layer stack. Times come from HIP events on the stream the
-kernels run on. `cpu_baseline` is the numpy oracle on this host for the headline
-workload (a bounded sample).
+kernels run on; the MALL is flushed before every timed replay. `cpu_baseline` is the
+numpy oracle on this host for the headline decode and the config-3 global prefill,
+min-of-5 at the BLAS default thread count and at one thread.
 """
 from __future__ import annotations
 
@@ -35,11 +36,27 @@ NH, KVH, HD = 8, 2, 256
 EAGER = False                 # --eager: time plain back-to-back launches instead of a HIP graph
 
 
-def graph_time_ms(fn_list, steps, warmup):
+_FLUSH = None
+
+
+def flush_mall():
+    """Evict the 256 MB MALL (Infinity Cache) and the L2s: read and write 1 GiB that no timed
+    call touches, so the first calls of a timed region find nothing of theirs cached."""
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = torch.empty(256 << 20, dtype=torch.float32, device="cuda")
+        _FLUSH.fill_(0.0)
+    _FLUSH.add_(1.0)
+
+
+def graph_time_ms(fn_list, steps, warmup, flush=True):
     """Capture `steps` calls (cycling fn_list) in one HIP graph; return mean ms per call.
 
-    With --eager the same calls are launched one by one on the stream (for profilers
-    that count per dispatch); the figure then includes host launch gaps.
+    The MALL is flushed before the timed replay (flush_mall), so a call whose operands are
+    distinct from those of the previous len(fn_list) - 1 calls streams them from HBM: with
+    len(fn_list) rotated sets of >= 512 MiB in total, no set is revisited before the MALL has
+    been overwritten. With --eager the same calls are launched one by one on the stream
+    (for profilers that count per dispatch); the figure then includes host launch gaps.
     """
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -48,6 +65,9 @@ def graph_time_ms(fn_list, steps, warmup):
             fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
     if EAGER:
+        if flush:
+            flush_mall()
+            torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
@@ -64,6 +84,9 @@ def graph_time_ms(fn_list, steps, warmup):
     torch.cuda.synchronize()
     g.replay()                      # warm replay (untimed)
     torch.cuda.synchronize()
+    if flush:
+        flush_mall()
+        torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
@@ -140,7 +163,8 @@ def prefill_case(sa, S, window, theta, steps, warmup, gen):
     ms = graph_time_ms([fn], steps, warmup)
     pairs = sum(min(p + 1, window) if window else p + 1 for p in range(S))
     flops = 4 * HD * NH * pairs
-    return ms, flops
+    host = tuple(x.cpu().numpy() for x in (q, qg, kc, vc, cos, sin)) + (flops,)
+    return ms, flops, host
 
 
 def batched_decode_case(sa, steps, warmup, gen):
@@ -398,39 +422,80 @@ def load_traffic():
         return None
 
 
-def cpu_baseline(case, seconds):
-    """The numpy oracle (oracle/attention.py) on this host for the headline decode call."""
-    import oracle.attention as O
+def _blas_info():
+    """The BLAS numpy is built against (numpy.show_config) and its thread pools right now."""
+    blas = "unknown"
     try:
-        from threadpoolctl import threadpool_limits
+        cfg = np.show_config(mode="dicts")
+        dep = cfg.get("Build Dependencies", {}).get("blas", {})
+        blas = f"{dep.get('name', '?')} {dep.get('version', '')}".strip()
+    except Exception:  # pragma: no cover - older numpy
+        pass
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"),
+                      default=1)
     except ImportError:  # pragma: no cover
-        threadpool_limits = None
+        threads = None
+    return blas, threads
+
+
+def _min_of(fn, reps=5, min_s=2.5):
+    """min and median of at least `reps` timed calls (and at least `min_s` seconds of them)
+    after one warm-up call (time.perf_counter)."""
+    fn()
+    ts = []
+    while len(ts) < reps or sum(ts) < min_s:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return min(ts), float(np.median(ts))
+
+
+def cpu_baseline(case, prefill_inputs):
+    """The numpy oracle (oracle/attention.py) on this host, timed as the build's CPU baseline
+    protocol asks: min-of-5 after a warm-up, at the BLAS library's default thread count (this
+    host's share of cores) and at one thread, for the headline decode call and for the
+    config-3 global prefill (S 1024). `value` is the headline decode at the default threads."""
+    import oracle.attention as O
+    from threadpoolctl import threadpool_limits
     q, qg, cos, sin, (kc, vc), cfg = case
     qn, qgn = q.cpu().numpy(), qg.cpu().numpy()
     c, s = cos.cpu().numpy()[0], sin.cpu().numpy()[0]
     k, v = kc.cpu().numpy(), vc.cpu().numpy()
     T = k.shape[0]
-    threads = min(16, os.cpu_count() or 1)
-    ctx = threadpool_limits(limits=threads) if threadpool_limits else None
-    try:
-        O.decode_attention(qn, k, v, T, KVH, q_gain=qgn, cos=c, sin=s, window=cfg.window)
-        n, t0 = 0, time.perf_counter()
-        while True:
-            O.decode_attention(qn, k, v, T, KVH, q_gain=qgn, cos=c, sin=s, window=cfg.window)
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or n >= 100000:
-                break
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
-    per = el / n
     nbytes = 2 * T * KVH * HD * 2
-    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_call": round(per * 1e6, 1),
-            "sample": f"{n} calls of oracle.decode_attention on the headline workload "
-                      f"(T {T}, nH {NH}/kvH {KVH}, hd {HD}, f16 cache) over {el:.1f} s, numpy BLAS "
-                      f"limited to {threads} threads"}
+    pq, pqg, pk, pv, pcos, psin, pflops = prefill_inputs
+    blas, default_threads = _blas_info()
+
+    def dec():
+        O.decode_attention(qn, k, v, T, KVH, q_gain=qgn, cos=c, sin=s, window=cfg.window)
+
+    def pre():
+        O.prefill_attention(pq, pk, pv, 0, KVH, q_gain=pqg, cos=pcos, sin=psin)
+
+    res = {}
+    for tag, limit in (("default", None), ("one_thread", 1)):
+        ctx = threadpool_limits(limits=limit) if limit else None
+        try:
+            dmin, dmed = _min_of(dec)
+            pmin, pmed = _min_of(pre)
+        finally:
+            if ctx is not None:
+                ctx.__exit__(None, None, None)
+        res[tag] = {"threads": limit or default_threads,
+                    "decode_2g_us_min": round(dmin * 1e6, 1), "decode_2g_us_median": round(dmed * 1e6, 1),
+                    "decode_2g_GB/s": round(nbytes / dmin / 1e9, 3),
+                    "prefill_3g_ms_min": round(pmin * 1e3, 2), "prefill_3g_ms_median": round(pmed * 1e3, 2),
+                    "prefill_3g_GFLOP/s": round(pflops / pmin / 1e9, 2)}
+    d = res["default"]
+    return {"value": d["decode_2g_GB/s"], "unit": "GB/s", "cores": d["threads"], "kind": "port",
+            "us_per_call": d["decode_2g_us_min"], "cpu_count": os.cpu_count(), "blas": blas,
+            "one_thread": res["one_thread"], "default_threads": d,
+            "sample": f"oracle.decode_attention on the headline workload (T {T}, nH {NH}/kvH {KVH}, hd {HD}, f16 "
+                      f"cache) and oracle.prefill_attention on config 3 global (S 1024), each the minimum of >= 5 "
+                      f"calls (>= 2.5 s) after a warm-up, at the BLAS default of {d['threads']} threads ({blas}; os.cpu_count() "
+                      f"{os.cpu_count()}) and at 1 thread"}
 
 
 def main():
@@ -439,7 +504,6 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 35-layer config 5 stack")
     ap.add_argument("--no-decoder", action="store_true", help="skip the E2B-shaped whole-decoder step")
@@ -472,7 +536,7 @@ def main():
         out = {}
         cfgn = "3" if args.prefill_seq == 1024 else f"S{args.prefill_seq}"
         for tag, win, th in ((f"prefill_{cfgn}g", 0, 1e6), (f"prefill_{cfgn}s", 512, 1e4)):
-            msp, fl = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen)
+            msp, fl, _ = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen)
             out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
         print(json.dumps(out), flush=True)
         return
@@ -495,34 +559,48 @@ def main():
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "decode_2g: BASELINE config 2 global layer, 1 query, nH 8/kvH 2, hd 256, "
                                "KV 4096 f16 cache, q/k RMSNorm+RoPE theta 1e6, 64 rotated caches",
-                   "accumulate": "f32", "kv_bytes_per_call": nbytes},
+                   "accumulate": "f32", "kv_bytes_per_call": nbytes,
+                   "timing": {"graph_calls": args.steps, "distinct_caches_timed": min(args.steps, 64),
+                              "rotation_bytes": 64 * nbytes, "mall_flushed_before_timing": True,
+                              "note": "one HIP graph of exactly `steps` calls over 64 rotated caches (512 MiB); "
+                                      "1 GiB is read and written before the timed replay, so every timed call "
+                                      "streams a cache that is not in the 256 MB MALL"}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "kernels": "decode_kernel + decode_merge_kernel (one g4a_decode call)"},
     }
+    prefill_host = None
     if not args.only_headline:
         sec = {}
-        ms2, nb2, _ = decode_case(sa, 4096, 512, 1e4, args.steps, args.warmup, 64, gen)
-        msd, _, _ = decode_case(sa, 4096, 0, 1e6, args.steps, args.warmup, 64, gen, device_len=False)
+        # HBM-bound rows: at least one call per rotated set in the timed graph, whatever --steps
+        hs = max(args.steps, 64)
+        ms2, nb2, _ = decode_case(sa, 4096, 512, 1e4, hs, args.warmup, 64, gen)
+        msd, _, _ = decode_case(sa, 4096, 0, 1e6, hs, args.warmup, 64, gen, device_len=False)
         sec["decode_2g_host_len"] = {"us_per_call": round(msd * 1e3, 3), "GB/s": round(nbytes / msd / 1e6, 2),
                                      "note": "the headline call with the key length given on the host "
                                              "(key_len NULL at the C ABI)"}
-        ms1, nb1 = config1_case(sa, args.steps, args.warmup, gen)
+        ms1, nb1 = config1_case(sa, max(args.steps, 256), args.warmup, gen)
         sec["decode_1"] = {"us_per_call": round(ms1 * 1e3, 3), "GB/s": round(nb1 / ms1 / 1e6, 2),
                            "hbm_frac": round(nb1 / ms1 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb1,
                            "note": "config 1 on the GPU: f32 caches, nH 4/kvH 1, T 1024, scale 1/16"}
         sec["decode_2s"] = {"us_per_call": round(ms2 * 1e3, 3), "GB/s": round(nb2 / ms2 / 1e6, 2),
-                            "hbm_frac": round(nb2 / ms2 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb2}
+                            "hbm_frac": round(nb2 / ms2 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb2,
+                            "note": f"{hs} calls over 64 rotated 8 MiB caches, MALL flushed first"}
+        sec["decode_1"]["note"] += f"; {max(args.steps, 256)} calls over 256 rotated 2 MiB caches, MALL flushed first"
         for tag, win, th in (("prefill_3g", 0, 1e6), ("prefill_3s", 512, 1e4)):
-            msp, fl = prefill_case(sa, 1024, win, th, max(8, args.steps // 8), args.warmup, gen)
+            msp, fl, host = prefill_case(sa, 1024, win, th, max(8, args.steps // 8), args.warmup, gen)
+            if tag == "prefill_3g":
+                prefill_host = host
             tf = fl / (msp * 1e-3) / 1e12
             sec[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(tf, 2),
-                        "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl}
+                        "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl,
+                        "note": "one 8 MiB cache re-read by every call (MFMA-bound; the cache of a "
+                                "prefill layer was just written by its kv_write)"}
         ms4, nb4, toks = batched_decode_case(sa, max(8, args.steps // 16), args.warmup, gen)
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
                            "hbm_frac": round(nb4 / ms4 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb4,
                            "sum_kv_len": toks}
-        msg, nbg = qkv_gemv_case(sa, args.steps, args.warmup, gen)
+        msg, nbg = qkv_gemv_case(sa, max(args.steps, 128), args.warmup, gen)
         sec["qkv_gemv_2"] = {"us_per_call": round(msg * 1e3, 3), "GB/s": round(nbg / msg / 1e6, 2),
                              "hbm_frac": round(nbg / msg / 1e6 / HBM_PEAK_GBS, 4), "weight_bytes": nbg,
                              "note": "decode q/k/v projections (qkv_70), 4-bit weights, 128 rotated sets"}
@@ -543,7 +621,9 @@ def main():
                                           "32 steps at KV ~4096 in one HIP graph"}
         rec["secondary"] = sec
     if not args.no_cpu_baseline:
-        rec["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds)
+        if prefill_host is None:
+            prefill_host = prefill_case(sa, 1024, 0, 1e6, 8, 2, gen)[2]
+        rec["cpu_baseline"] = cpu_baseline(case, prefill_host)
     print(json.dumps(rec), flush=True)
 
 

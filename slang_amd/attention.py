@@ -190,14 +190,16 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
 
 def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
             rope_sin=None, out=None, out_dtype=torch.float16, q_hilo: bool = False,
-            workspace: DecodeWorkspace | None = None):
+            workspace: DecodeWorkspace | None = None, split: bool = True):
     """Causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
 
     q [S][nH][hd] f32 raw; caches [>= start_pos+S][kvH][hd] f16/f32; rope_cos/sin
     [S][hd/2] rows for those positions. Returns out [S][nH][hd] (f16 by default).
     q_hilo keeps the normalised, rotated q at f32 accuracy (two f16 MFMA operands)
     instead of rounding it to f16 as qprep_b does. Short prompts split long causal rows
-    over workgroups through `workspace` (allocated here when not given).
+    over workgroups through `workspace` (allocated here when not given); split=False
+    passes no workspace, which the C ABI defines as the unsplit call (one kernel, the
+    q prologue fused in).
     """
     S = q.shape[0]
     if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
@@ -221,7 +223,7 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None
             (_lib.OUT_F32 if out.dtype == torch.float32 else 0) | (_lib.Q_HILO if q_hilo else 0)
     c = cfg.c(flags)
     lib = _lib.load()
-    ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos))
+    ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos)) if split else 0
     ws = (workspace or DecodeWorkspace(q.device)).get(ws_bytes) if ws_bytes else None
     check(lib.g4a_prefill(ctypes.byref(c), S, int(start_pos), _ptr(q), _ptr(q_gain), _ptr(rope_cos),
                           _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(ws),

@@ -122,11 +122,22 @@ __device__ __forceinline__ float8v bload_f8(rsrc_t r, int off) {
 }
 
 // ---------------------------------------------------------------- numerics
+// Pin a value in a register, so the compiler can no longer fold the arithmetic that made it
+// into a later conversion. A fused multiply-add-convert (v_fma_mix*_f16) rounds once, from the
+// exact result, where the f32 value converted afterwards is rounded twice; near an f16 rounding
+// tie the two differ by one f16 ulp. Once pinned, every conversion of x starts from the same
+// f32 value: a hi/lo split sums back to x, and every kernel that rounds the same value to f16
+// gets the reference's f16(f32 value) (qprep_b, kernels_dsl.py:1872-1873).
+__device__ __forceinline__ float pin(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // Static-range quantisation, identity when s == 0 (gemma4_150/reference.py:30-31).
 // x / s is the IEEE quotient and rintf rounds half to even, as numpy's round does.
 __device__ __forceinline__ float srq(float x, float s) {
     if (s == 0.0f) return x;
-    return fminf(fmaxf(rintf(x / s), -128.0f), 127.0f) * s;
+    return pin(fminf(fmaxf(rintf(x / s), -128.0f), 127.0f) * s);  // an f32 product, as the reference's
 }
 
 // 8 consecutive cache elements as f32, from f16 (one 16 B load) or f32 (two 16 B loads).
@@ -212,8 +223,9 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float x0 = x[s][i], x1 = x[s + KSTEPS / 2][i];
-            x[s][i] = __builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i]));  // explicit fma: every
-            x[s + KSTEPS / 2][i] = __builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]);  // user rounds alike
+            // explicit fma, and the result pinned: every user rounds the same f32 value
+            x[s][i] = pin(__builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i])));
+            x[s + KSTEPS / 2][i] = pin(__builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]));
         }
 }
 
@@ -257,6 +269,11 @@ __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, fl
         v0 = v0 * rs;
         v1 = v1 * rs;
     }
+    // the rows are rounded to the cache type by the caller: from these f32 values
+    k0 = pin(k0);
+    k1 = pin(k1);
+    v0 = pin(v0);
+    v1 = pin(v1);
 }
 
 }  // namespace g4a

@@ -33,9 +33,6 @@
 //    agent-scope release has to write back the XCD's L2 and the merger then walks every
 //    partial serially.)
 // Scores are in the log2 domain (q carries scale*log2 e), so the softmax uses exp2.
-#include <stdio.h>
-#include <stdlib.h>
-
 #include "common.hpp"
 
 namespace g4a {
@@ -404,8 +401,9 @@ void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < QP; ++e) {
             const float x0 = x[0][e], x1 = x[1][e];
-            const float r0 = (x0 * qcv[e] - x1 * qsv[e]) * a.scale_log2;
-            const float r1 = (x1 * qcv[e] + x0 * qsv[e]) * a.scale_log2;
+            // pinned: the high part and the low part's subtrahend are one rounding of one value
+            const float r0 = pin((x0 * qcv[e] - x1 * qsv[e]) * a.scale_log2);
+            const float r1 = pin((x1 * qcv[e] + x0 * qsv[e]) * a.scale_log2);
             const half_t h0 = (half_t)r0, h1 = (half_t)r1;
             sQ[hh * QSTR + d0 + e] = h0;
             sQ[hh * QSTR + HD / 2 + d0 + e] = h1;
@@ -657,21 +655,21 @@ __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------- host side
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
+// Split policy (measured on MI355X: workgroup targets of 128-1024 and minimum chunks of
+// 16-512 keys were swept on configs 2 and 4 and on the whole decode step; these won or tied)
+constexpr long kDecodeTargetWgs = 512;  // workgroups the worst-case sequence is spread over
+constexpr long kDecodeMinChunk = 16;    // keys per split at least (one 16-key block)
 
 // Keys per split: spread the worst-case work (every sequence at max_key_len) over about
-// G4A_DECODE_TARGET_WGS workgroups, never below G4A_DECODE_MIN_CHUNK keys; a chunk of 64 keys
+// kDecodeTargetWgs workgroups, never below kDecodeMinChunk keys; a chunk of 64 keys
 // (every wave of the workgroup busy) is preferred as long as it still yields 128 or more
 // workgroups. At most 256 splits per sequence, chunk a multiple of the 16-key block.
 static int decode_chunk(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     const long pairs = (long)n_seq * cfg->n_kv_heads;
     long max_active = max_key_len;
     if (cfg->window > 0 && (long)cfg->window < max_active) max_active = cfg->window;
-    const long target = env_int("G4A_DECODE_TARGET_WGS", 512);
-    const long min_chunk = env_int("G4A_DECODE_MIN_CHUNK", 16);
+    const long target = kDecodeTargetWgs;
+    const long min_chunk = kDecodeMinChunk;
     const long kp = max_active * pairs;
     long chunk = (kp + target - 1) / target;
     if (chunk < min_chunk) chunk = min_chunk;
@@ -699,7 +697,7 @@ static ListPlan list_plan(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     ListPlan p{0, 0};
     if (n_seq <= 1 || decode_splits(cfg, n_seq, max_key_len) <= 1) return p;
     const bool f32 = (cfg->flags & G4A_KV_F32) != 0;
-    const int resident = env_int("G4A_DECODE_RESIDENT", cfg->head_dim == 256 && !f32 ? 512 : 256);
+    const int resident = cfg->head_dim == 256 && !f32 ? 512 : 256;
     const long pairs = (long)n_seq * cfg->n_kv_heads;
     p.target = resident - pairs > resident / 2 ? (int)(resident - pairs) : resident / 2;
     p.grid = (int)(p.target + pairs);
@@ -939,3 +937,4 @@ extern "C" int g4a_decode_kv(const g4a_cfg* cfg, int n_seq, int max_key_len, con
     return decode_impl(cfg, n_seq, max_key_len, key_len, q, q_gain, rope_cos, rope_sin, k_cache, v_cache,
                             seq_stride, out, ws, ws_bytes, stream, &kvn);
 }
+

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
         for (int k = 0; k < PER; ++k) {
             const int i = tid + 256 * k;
             const float z = g.pw2 ? av[k] / d2 * w2v[k] : av[k];
-            const float zq = g.pf16 ? (float)(half_t)srq((float)(half_t)z, g.pq2) : srq(z, g.pq2);
+            const float zq = g.pf16 ? (float)(half_t)srq((float)(half_t)pin(z), g.pq2) : srq(z, g.pq2);
             if (i < n_in) {
                 if (blockIdx.x == 0 && g.pzout) g.pzout[i] = zq;
                 stage_x(i, zq);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(1024) void rms_kernel(RmsArgs a) {
     for (int k = 0; k < PER; ++k) {
         const int i = threadIdx.x + k * nt;
         const float z = a.w2 ? xv[k] / d2 * w2v[k] : xv[k];
-        const float y2 = a.f16_2 ? (float)(half_t)srq((float)(half_t)z, a.q2) : srq(z, a.q2);
+        const float y2 = a.f16_2 ? (float)(half_t)srq((float)(half_t)pin(z), a.q2) : srq(z, a.q2);
         if (i < n) {
             a.out2[(size_t)r * n + i] = y2;
             s2 += y2;

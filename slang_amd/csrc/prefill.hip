@@ -19,8 +19,6 @@
 // is computed. Scores stay f32 in the MFMA accumulators; P is rounded to f16 only as
 // the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last] are skipped;
 // boundary tiles are masked per element. Work-groups are launched longest-causal-row first.
-#include <stdlib.h>
-
 #include "common.hpp"
 
 namespace g4a {
@@ -47,19 +45,13 @@ struct PrefillArgs {
 };
 
 // LDS operand reads issued ahead of their MFMAs in prefill_kernel_w32: score product
-// (one K read per MFMA) and P.V product (two transposed V reads per MFMA)
-#ifndef G4A_QK_AHEAD
-#define G4A_QK_AHEAD 4
-#endif
-#ifndef G4A_PV_AHEAD
-#define G4A_PV_AHEAD 3
-#endif
-#ifndef G4A_PREFILL_KT256
-#define G4A_PREFILL_KT256 64
-#endif
+// (one K read per MFMA) and P.V product (two transposed V reads per MFMA); 2-8 and 3-7
+// measured within +-2 % at S 1024 and S 8192
+constexpr int kQkAhead = 4;
+constexpr int kPvAhead = 3;
 template <int HD>
 struct PrefillShape {
-    static constexpr int KT = HD == 512 ? 32 : G4A_PREFILL_KT256;  // keys per LDS tile
+    static constexpr int KT = HD == 512 ? 32 : 64;  // keys per LDS tile
     static constexpr int KSTEPS = HD / 32;           // MFMA k-steps of the score product
     static constexpr int NKT = KT / 16;              // 16-key sub-tiles of S^T
     static constexpr int NU = KT / 32;               // 32-key k-steps of the P.V product
@@ -533,8 +525,8 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float x0 = x[s][i], x1 = x[s + 8][i];
-                x[s][i] = __builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i]));
-                x[s + 8][i] = __builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]);
+                x[s][i] = pin(__builtin_fmaf(x0, cv[s][i], -(x1 * sv[s][i])));
+                x[s + 8][i] = pin(__builtin_fmaf(x1, cv[s][i], x0 * sv[s][i]));
             }
 #pragma unroll
         for (int s = 0; s < 16; ++s)
@@ -595,14 +587,14 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
                 sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
             }
         }
-        // keep G4A_QK_AHEAD LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
-        __builtin_amdgcn_sched_group_barrier(0x100, G4A_QK_AHEAD, 0);
+        // keep kQkAhead LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
+        __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);
 #pragma unroll
-        for (int i = 0; i < 32 - G4A_QK_AHEAD; ++i) {
+        for (int i = 0; i < 32 - kQkAhead; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, G4A_QK_AHEAD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
 
         // scores of this lane: key kb + 4h + 32kt + 8(r/4) + r%4 of its column, log2 domain;
         // tiles inside every column's range skip the per-element mask
@@ -665,14 +657,14 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) oacc[dt] = mfma32(av[dt], pb[u], oacc[dt]);
         }
-        // transposed V reads kept G4A_PV_AHEAD MFMAs ahead of the P.V MFMAs, two reads per MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * G4A_PV_AHEAD, 0);
+        // transposed V reads kept kPvAhead MFMAs ahead of the P.V MFMAs, two reads per MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPvAhead, 0);
 #pragma unroll
-        for (int i = 0; i < 32 - G4A_PV_AHEAD; ++i) {
+        for (int i = 0; i < 32 - kPvAhead; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, G4A_PV_AHEAD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kPvAhead, 0);
     }
 
     // ---- epilogue: column sum over both halves, normalise, srq, store 4 dims at a time
@@ -777,11 +769,6 @@ static void (*pick_w32(bool out32))(PrefillArgs) {
 
 typedef void (*prefill_fn)(PrefillArgs);
 
-static int getenv_flag(const char* name) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : 0;
-}
-
 template <int HD, int G, typename KVT, typename OUTT>
 static prefill_fn pick_hilo(bool hilo) {
     return hilo ? prefill_kernel<HD, G, KVT, OUTT, true> : prefill_kernel<HD, G, KVT, OUTT, false>;
@@ -811,16 +798,15 @@ using namespace g4a;
 
 // Key split for short prompts: when the query blocks alone give fewer than 2 workgroups
 // per CU, long causal rows are cut into pieces of split_tiles key tiles, the longest block
-// into about six pieces (G4A_PREFILL_SPLIT_TILES: 0 automatic, -1 never, N tiles per piece).
-// Measured best piece sizes at 16 / 24 / 32 / 64 tiles in the longest block (S 1024, 1536,
-// 2048, 4096 global): 3 / 3-4 / 5 / 10-13 tiles; one piece per CU (3 / 5 / 9 / 33) was up
-// to 24 % slower beyond S 1024.
+// into about six pieces. Measured best piece sizes at 16 / 24 / 32 / 64 tiles in the
+// longest block (S 1024, 1536, 2048, 4096 global): 3 / 3-4 / 5 / 10-13 tiles; one piece
+// per CU (3 / 5 / 9 / 33) was up to 24 % slower beyond S 1024.
 struct PrefillSplit {
     int split_tiles, max_pieces, n_qblocks, total_pieces;
     size_t o_bytes, ml_bytes, q16_bytes, total;
 };
 static bool use_w32(const g4a_cfg* cfg) {
-    return cfg->head_dim == 256 && !(cfg->flags & (G4A_KV_F32 | G4A_Q_HILO)) && getenv_flag("G4A_PREFILL_W16") == 0;
+    return cfg->head_dim == 256 && !(cfg->flags & (G4A_KV_F32 | G4A_Q_HILO));
 }
 static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0};
@@ -829,12 +815,11 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     if (G < 1 || 128 % G) return p;
     const int BQ = 128 / G, KT = 64, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
     p.n_qblocks = (S + BQ - 1) / BQ;
-    const int mode = getenv_flag("G4A_PREFILL_SPLIT_TILES");
-    if (mode < 0 || (mode == 0 && (long)p.n_qblocks * kvH >= 512)) return p;
+    if ((long)p.n_qblocks * kvH >= 512) return p;
     // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
     // preparation and merge only while the unsplit grid leaves most CUs idle (S 2048,
     // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27)
-    if (mode == 0 && W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
+    if (W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
     int max_tiles = 0;
     for (int qb = 0; qb < p.n_qblocks; ++qb) {
         const int p0 = start_pos + qb * BQ;
@@ -843,7 +828,7 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
         const int nt = (hi - lo + KT - 1) / KT;
         if (nt > max_tiles) max_tiles = nt;
     }
-    int st = mode > 0 ? mode : (max_tiles * 5 + 31) / 32;
+    int st = (max_tiles * 5 + 31) / 32;
     if (st < 2) st = 2;
     if (st < (max_tiles + 7) / 8) st = (max_tiles + 7) / 8;  // the merge takes <= 8 pieces
     const int pieces = (max_tiles + st - 1) / st;
@@ -964,7 +949,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
         a.q16 = q16;
     }
-    a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0 && getenv_flag("G4A_PREFILL_XCD_RUNS") >= 0;
+    a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0;
     const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
                       : a.xcd_runs      ? dim3(a.n_qblocks * cfg->n_kv_heads)
                                         : dim3(a.n_qblocks, cfg->n_kv_heads);

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
             const int bit = 32 * (v / (32 / BITS)) + 8 * ((v % (32 / BITS)) / (8 / BITS)) +
                             BITS * (v % (8 / BITS));      // word, byte, then low bits first
             const uint32_t q = (w[bit / 32] >> (bit % 32)) & MASK;
-            h[j] = (half_t)(s * ((float)q - zp));
+            h[j] = (half_t)pin(s * ((float)q - zp));  // f16 of the f32 product, as dq_f16 rounds
         }
         *reinterpret_cast<half8*>(dst + 8 * g) = h;
     }
@@ -334,11 +334,7 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
         g.out_q[i] = m ? m->out_q : 0.0f;
         g.tile_end[i] = tiles;
     }
-    const char* bkv = getenv("G4A_GEMM_BK");
-    if (bkv && atoi(bkv) == 32)
-        hipLaunchKernelGGL(gemm16_kernel<32>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
-    else
-        hipLaunchKernelGGL(gemm16_kernel<64>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    hipLaunchKernelGGL(gemm16_kernel<64>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "gemm16 launch");
     return G4A_OK;

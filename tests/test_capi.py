@@ -212,3 +212,4 @@ def test_decoder_argument_errors(lib):
     assert lib.g4a_qgemv_gelu_mul(4, 64, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
     pro.w1 = FAKE.value
     assert lib.g4a_qgemv_gelu_mul(4, 4096, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
+

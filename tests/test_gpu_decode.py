@@ -5,6 +5,8 @@ Cases follow the reference's own decode tests (tests/test_gemma3_kernels_gpu.py:
 tests/test_gemma4_kernels_gpu.py:63-80, tests/test_kernels_dsl_parity.py:726-782) and
 BASELINE configs 1, 2 (global and sliding) and 4.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -368,3 +370,42 @@ def test_host_key_len_matches_device_key_len(B, window, fused):
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+# ---------------------------------------------------------------- f32-accurate scores
+def test_decode_scores_are_f32_accurate():
+    """The decode keeps q at f32 accuracy as an f16 high part plus an f16 low part. Both parts
+    must come from one f32 value: a high part rounded from a different evaluation of q (a fused
+    multiply-convert rounds once, a multiply then a convert twice) leaves hi + lo one f16 ulp
+    off wherever q sits on an f16 rounding tie (about one element in 4096), a score error of up
+    to ~1e-2 and an output error of several 1e-3 when such a key dominates.
+
+    White-box: with every key of split d equal to e_d (a unit row), split d's score maximum,
+    which the decode leaves in its workspace ((m, l) pairs [pair][split][G], m in log2 units),
+    is exactly the kernel's q_d. 16 q rows with gain and RoPE (32,768 q elements): each must
+    match the oracle's f32 q to a few f32 ulps."""
+    T, nH, kvH, hd = 16384, 8, 2, 256        # 64 keys per split, 256 splits per kv head
+    kc = torch.zeros(T, kvH, hd, device=DEV, dtype=torch.float16)
+    for d in range(hd):
+        kc[64 * d:64 * d + 64, :, d] = 1.0
+    vc = torch.zeros_like(kc)
+    cfg = sa.AttnConfig(nH, kvH, hd)
+    rng = np.random.default_rng(77)
+    lib = sa._lib.load()
+    c = cfg.c(0)
+    assert lib.g4a_decode_ws_bytes(ctypes.byref(c), 1, T) >= 2 * 256 * 4 * 8
+    worst = 0.0
+    for r in range(16):
+        q = rng.standard_normal((nH, hd)).astype(np.float32)
+        qg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+        cos, sin = O.rope_tables([int(rng.integers(0, 1 << 20))], hd, 1e6 if r % 2 else 1e4)
+        ws = sa.DecodeWorkspace(DEV)
+        sa.decode(t(q), kc, vc, [T], cfg, q_gain=t(qg), rope_cos=t(cos), rope_sin=t(sin), workspace=ws)
+        torch.cuda.synchronize()
+        ml = ws.buf[:2 * 256 * 4 * 8].view(torch.float32).view(kvH, 256, nH // kvH, 2).cpu().numpy()
+        q_kernel = (ml[..., 0].astype(np.float64) / np.log2(np.e)).transpose(0, 2, 1).reshape(nH, hd)
+        q_ref = O._prep_q(q, qg, cos, sin, 1e-6).astype(np.float64)
+        err = np.abs(q_kernel - q_ref) / np.maximum(np.abs(q_ref), 1.0)
+        worst = max(worst, float(err.max()))
+        assert err.max() < 2e-6, f"row {r}: kernel q off by {err.max():.2e} (relative) at {np.unravel_index(err.argmax(), err.shape)}"
+    print(f"decode q vs oracle q: worst relative difference {worst:.2e}")
