@@ -115,6 +115,25 @@ int g4a_decode_kv(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t*
                   void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * g4a_decode without a workspace: no counterpart in the reference (whose runners own a
+ * persistent `partials` buffer). It is for callers that cannot allocate device memory --
+ * code under HIP graph capture, serving loops or harnesses that forbid hipMalloc. The
+ * split partials live in a device array inside the library, G4A_DECODE_SCRATCH_BYTES per
+ * GPU, held from the library's load until the process ends; the call allocates nothing.
+ * Arguments, kernels and results are those of g4a_decode (bit-identical for the same
+ * inputs). A call whose partials need more than the array holds (g4a_decode_ws_bytes >
+ * G4A_DECODE_SCRATCH_BYTES: roughly n_seq * n_kv_heads * splits * G * head_dim * 4 bytes)
+ * returns G4A_EWORKSPACE before launching. The stream must belong to the current device.
+ * Every call on one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams, two threads) race: serialise them, or use g4a_decode with distinct workspaces.
+ */
+#define G4A_DECODE_SCRATCH_BYTES (8u << 20)
+int g4a_decode_noalloc(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                       const float* q, const float* q_gain, const float* rope_cos, const float* rope_sin,
+                       const void* k_cache, const void* v_cache, int64_t seq_stride, float* out,
+                       void* stream);
+
+/*
  * Batched causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
  * Replaces PrefillGPU._attn_gemm (prefill_gpu.py:259-313: qprep_b -> QK^T GEMM ->
  * smax_b -> PV GEMM -> attnout_b) and the fused attn_prefill dispatch

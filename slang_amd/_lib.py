@@ -12,6 +12,9 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libg4attn.so")
 
+# the allocation-free decode's device array (G4A_DECODE_SCRATCH_BYTES, g4attn.h)
+DECODE_SCRATCH_BYTES = 8 << 20
+
 # flags (g4attn.h)
 KV_F32 = 0x1
 IN_F16 = 0x2
@@ -22,7 +25,7 @@ Q_HILO = 0x10
 # every function include/g4attn.h declares
 EXPORTS = (
     "g4a_strerror", "g4a_last_error", "g4a_version",
-    "g4a_decode_ws_bytes", "g4a_decode", "g4a_decode_kv",
+    "g4a_decode_ws_bytes", "g4a_decode", "g4a_decode_kv", "g4a_decode_noalloc",
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
     "g4a_dequant", "g4a_qkv_gemv", "g4a_srqh", "g4a_gemm16",
@@ -106,6 +109,9 @@ def load() -> ctypes.CDLL:
     lib.g4a_decode_kv.restype = ctypes.c_int
     lib.g4a_decode_kv.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_float,
                                   ctypes.c_float, P, P, P, ctypes.c_int64, P, P, ctypes.c_size_t, P]
+    lib.g4a_decode_noalloc.restype = ctypes.c_int
+    lib.g4a_decode_noalloc.argtypes = [cfgp, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P,
+                                       ctypes.c_int64, P, P]
     lib.g4a_prefill_ws_bytes.restype = ctypes.c_size_t
     lib.g4a_prefill_ws_bytes.argtypes = [cfgp, ctypes.c_int, ctypes.c_int]
     lib.g4a_prefill.restype = ctypes.c_int

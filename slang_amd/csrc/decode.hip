@@ -33,6 +33,8 @@
 //    agent-scope release has to write back the XCD's L2 and the merger then walks every
 //    partial serially.)
 // Scores are in the log2 domain (q carries scale*log2 e), so the softmax uses exp2.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace g4a {
@@ -938,3 +940,66 @@ extern "C" int g4a_decode_kv(const g4a_cfg* cfg, int n_seq, int max_key_len, con
                             seq_stride, out, ws, ws_bytes, stream, &kvn);
 }
 
+// ---------------------------------------------------------------- allocation-free variant
+// g4a_decode_noalloc: g4a_decode with the split partials in a file-scope device array
+// instead of a caller workspace, for callers that cannot allocate (code under HIP graph
+// capture, serving loops that forbid hipMalloc). Each GPU holds its own copy of the array
+// from the library's load until the process ends; the host reaches it only through the
+// address hipGetSymbolAddress returns on that device (the array's name in host code is a
+// host-side stand-in, not a device address). The partials need no initialisation (every
+// slot the merge reads is written by the same call), so nothing is cleared between calls.
+// Calls that overlap on one GPU share the array and race.
+namespace g4a {
+constexpr size_t kDecodeScratchBytes = G4A_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_dev[kMaxScratchDevices];  // per device: the array's device address
+static std::mutex g_scratch_mu;
+
+// The device address of this device's scratch array, resolved once per device with that
+// device current (the device of the caller's stream must be the current device).
+static int decode_scratch(void** p) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        set_error("device %d beyond the %d devices the scratch table holds", dev, kMaxScratchDevices);
+        return G4A_EINVAL;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* a = nullptr;
+        e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+        if (!a) {
+            set_error("hipGetSymbolAddress(scratch) returned NULL");
+            return G4A_EHIP;
+        }
+        g_scratch_dev[dev] = a;
+    }
+    *p = g_scratch_dev[dev];
+    return G4A_OK;
+}
+}  // namespace g4a
+
+extern "C" int g4a_decode_noalloc(const g4a_cfg* cfg, int n_seq, int max_key_len, const int32_t* key_len,
+                                  const float* q, const float* q_gain, const float* rope_cos,
+                                  const float* rope_sin, const void* k_cache, const void* v_cache,
+                                  int64_t seq_stride, float* out, void* stream) {
+    if (!check_cfg(cfg, true)) return G4A_EINVAL;
+    if (n_seq <= 0 || max_key_len <= 0) {
+        set_error("n_seq (%d) and max_key_len (%d) must be positive", n_seq, max_key_len);
+        return G4A_EINVAL;
+    }
+    const size_t need = g4a_decode_ws_bytes(cfg, n_seq, max_key_len);
+    if (need == 0 || need > kDecodeScratchBytes) {
+        set_error("decode partials need %zu bytes; g4a_decode_noalloc holds at most %zu "
+                  "(use g4a_decode with a workspace)", need, kDecodeScratchBytes);
+        return G4A_EWORKSPACE;
+    }
+    void* ws = nullptr;
+    const int rc = decode_scratch(&ws);
+    if (rc != G4A_OK) return rc;
+    return decode_impl(cfg, n_seq, max_key_len, key_len, q, q_gain, rope_cos, rope_sin, k_cache, v_cache,
+                       seq_stride, out, ws, kDecodeScratchBytes, stream, nullptr);
+}

@@ -213,3 +213,16 @@ def test_decoder_argument_errors(lib):
     pro.w1 = FAKE.value
     assert lib.g4a_qgemv_gelu_mul(4, 4096, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
 
+
+def test_decode_noalloc_limit(lib):
+    """The allocation-free decode states its array size in the header and rejects calls whose
+    partials exceed it before touching the device."""
+    src = open(HEADER).read()
+    m = re.search(r"#define G4A_DECODE_SCRATCH_BYTES \((\d+)u << (\d+)\)", src)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.DECODE_SCRATCH_BYTES
+    c = cfg(n_q_heads=64, n_kv_heads=8, head_dim=512)  # 256 splits x 64 heads x 512 dims of partials
+    need = lib.g4a_decode_ws_bytes(ctypes.byref(c), 1, 1 << 20)
+    assert need > _lib.DECODE_SCRATCH_BYTES
+    rc = lib.g4a_decode_noalloc(ctypes.byref(c), 1, 1 << 20, FAKE, FAKE, None, None, None, FAKE, FAKE,
+                                0, FAKE, None)
+    assert rc == -3 and b"at most" in lib.g4a_last_error()
