@@ -269,11 +269,13 @@ def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, int
     Packed rows are uniform random bytes, i.e. uniform codes of any width."""
     from slang_amd.manifest import Manifest
     rng = np.random.default_rng(seed)
-    parts, tensors, pos = [], {}, 0
+    parts, tensors, pos, keep = [], {}, 0, {}
 
     def put(name, arr, dt):
         nonlocal pos
-        b = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+        arr = np.ascontiguousarray(arr)
+        keep[name] = arr  # the bytes below are a view: contents may still be set until the end
+        b = arr.view(np.uint8).reshape(-1)
         tensors[name] = {"off": pos, "len": int(b.size), "dtype": dt, "shape": list(arr.shape)}
         parts.append(b)
         pos += b.size
@@ -328,6 +330,8 @@ def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, int
         layers.append({"index": L, "sliding": not glob, "head_dim": hd, "q_dim": q_dim, "intermediate": inter,
                        "shared": shared, "kv_source": src, "rope_theta": 1e6 if glob else 1e4,
                        "rope_cutoff": 64 if glob else hd // 2, "scales": sc})
+    for L in range(n_layers):  # export.py:110, 119-122: the next layer's input norm (the final norm last)
+        keep[f"L{L}.pleproj_w12s"][H:2 * H] = keep[f"L{L + 1}.in_norm"] if L + 1 < n_layers else keep["final_norm"]
     meta = {"config": {"H": H, "nL": n_layers, "nH": nH, "vocab": vocab, "window": window, "softcap": 30.0,
                        "ple_d": ple_d, "embed_scale": float(np.sqrt(H)), "ple_scale": float(np.sqrt(ple_d)),
                        "bos": 2, "eos": 1},
@@ -355,7 +359,30 @@ def decoder_case(steps=32, T=4096):
         rows = T + steps // 2 + 1  # the middle step's key count
         rows = min(rows, st.man.window) if s.sliding else rows
         kv += 2 * rows * st.man.n_kv_heads(s.index) * s.head_dim * 2
-    return ms, wbytes + kv, wbytes, kv
+    pre = decoder_prefill_case(st)
+    return ms, wbytes + kv, wbytes, kv, pre
+
+
+def decoder_prefill_case(st, S=1024, reps=4):
+    """The layers-outer batched prefill of the same model (DecoderStack.prefill, the reference's
+    PrefillGPU.prefill): an S-token prompt through all 35 layers, the token ids on the device,
+    one prompt per step of a HIP graph. Returns ms per prompt and the FLOPs of its GEMMs
+    (every linear over S rows) and of its attention (4*hd*nH*attended pairs per layer)."""
+    man = st.man
+    H, nL, d = st.H, st.nL, st.d
+    ids = torch.randint(0, st.vocab, (S,), dtype=torch.int32, device="cuda")
+    st.prefill(ids, 0)  # dequantises every layer's weights once (kept resident), sizes the buffers
+    torch.cuda.synchronize()
+    ms = graph_time_ms([lambda: st.prefill(ids, 0)], reps, 1)
+    gemm = 2 * S * H * nL * d
+    att = 0
+    for s in man.layers:
+        kv = 0 if s.shared else man.kv_dim(s.index)
+        gemm += 2 * S * H * (s.q_dim + 2 * kv) + 2 * S * s.q_dim * H + 3 * 2 * S * H * s.intermediate + 2 * 2 * S * H * d
+        W = man.window if s.sliding else 0
+        pairs = sum(min(p + 1, W) if W else p + 1 for p in range(S))
+        att += 4 * s.head_dim * s.n_q_heads * pairs
+    return ms, gemm, att
 
 
 def qkv_gemv_case(sa, steps, warmup, gen, n_sets=128):
@@ -396,6 +423,17 @@ def proj_case(sa, steps, warmup, gen, S=1024):
         sa.gemm16(a16, [(wq, oq, 0.02), (wk, ok, None), (wv, ov, None)])
     ms = graph_time_ms([fn], steps, warmup)
     return ms, 2 * S * H * (NH * HD + 2 * KVH * HD)
+
+
+def prefill_row(pre, S=1024):
+    ms, gemm, att = pre
+    return {"ms_per_prompt": round(ms, 3), "prompt_tokens": S, "tokens/s": round(S / ms * 1e3, 1),
+            "gemm_TFLOP/s": round(gemm / ms / 1e9, 2), "attention_TFLOP/s": round(att / ms / 1e9, 2),
+            "mfma_frac": round((gemm + att) / ms / 1e9 / F16_PEAK_TFLOPS, 4), "gemm_flops": gemm,
+            "attention_flops": att,
+            "note": "layers-outer batched prefill of the E2B-shaped synthetic model (35 layers): every "
+                    "linear one f16 GEMM over the prompt (weights dequantised once, kept resident), "
+                    "batched causal attention, the row tails between them; a HIP graph of whole prompts"}
 
 
 def copy_calibration(steps):
@@ -541,9 +579,10 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.decoder_only:
-        msd, nbd, wb, kvb = decoder_case()
+        msd, nbd, wb, kvb, pre = decoder_case()
         print(json.dumps({"decoder_e2b": {"ms_per_token": round(msd, 4), "GB/s": round(nbd / msd / 1e6, 2),
-                                          "weight_bytes": wb, "kv_bytes": kvb}}), flush=True)
+                                          "weight_bytes": wb, "kv_bytes": kvb},
+                          "decoder_e2b_prefill": prefill_row(pre)}), flush=True)
         return
     if args.batched_only:
         ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
@@ -612,7 +651,8 @@ def main():
         if not args.no_stack:
             sec["stack_5"] = stack_case(sa, gen)
         if not args.no_decoder:
-            msd, nbd, wb, kvb = decoder_case()
+            msd, nbd, wb, kvb, pre = decoder_case()
+            sec["decoder_e2b_prefill"] = prefill_row(pre)
             sec["decoder_e2b"] = {"ms_per_token": round(msd, 4), "tokens/s": round(1e3 / msd, 1),
                                   "GB/s": round(nbd / msd / 1e6, 2), "hbm_frac": round(nbd / msd / 1e6 / HBM_PEAK_GBS, 4),
                                   "bytes_per_token": nbd, "weight_bytes": wb, "kv_bytes": kvb,

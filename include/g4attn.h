@@ -229,6 +229,8 @@ typedef struct {
     int n;        /* rows of w = output columns, a multiple of 128 */
     int out_f32;
     float out_q;
+    float alpha;  /* the f16 result is f16(alpha * sum), gemm_tiled's alpha (kernels_dsl.py:96-103;
+                     the down projection's down_in, prefill_gpu.py:377); 0 means 1 */
 } g4a_gemm_mat;
 
 /*
@@ -324,6 +326,10 @@ int g4a_geglu(int n, const float* a, const float* b, float out_q, float* out, vo
  */
 int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok,
               const float* row_scale, int group, float mult, float* out, void* stream);
+/* g4a_embed for n_tok tokens tok[0..n_tok) into out [n_tok][n]: embed_00 and plegather_01 over
+ * the S tokens of a batched prefill (kernels_dsl.py:433-479; prefill_gpu.py:412-420). */
+int g4a_embed_rows(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok, int n_tok,
+                   const float* row_scale, int group, float mult, float* out, void* stream);
 /* logits <- cap * tanh(logits / cap) in place (cap 0: unchanged) and tok[0] = the first
  * index of the maximum (reference.py:207; runner.py:501-505 argmax1_34 -> argmax2_35 on the
  * GPU). ws: g4a_softcap_argmax_ws_bytes(n) bytes for the per-workgroup candidates; logits
@@ -331,6 +337,44 @@ int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t*
 size_t g4a_softcap_argmax_ws_bytes(int n);
 int g4a_softcap_argmax(int n, float* logits, float cap, int32_t* tok, void* ws, size_t ws_bytes,
                        void* stream);
+
+/*
+ * ---- The layers-outer batched prefill around the attention block ----------------------
+ * PrefillGPU._layer (gemma4_150/prefill_gpu.py:316-395) over S token rows: the f16 GEMMs are
+ * g4a_gemm16 on dequantised weights (g4a_dequant), the attention g4a_prefill, and the tails
+ * between them these three.
+ */
+/* g4a_rows_tail modes: the next GEMM's f16 operand y16 made from the updated row */
+#define G4A_TAIL_NONE   0 /* no y16 */
+#define G4A_TAIL_SRQ    1 /* y16 = f16(srq(hidden, q2))                          srqh_b */
+#define G4A_TAIL_NORM   2 /* y16 = f16(srq(rms(hidden) * w2, q2))                rmssrq_69 + srqh_b */
+#define G4A_TAIL_NORM16 3 /* y16 = f16(srq(f32(f16(rms(hidden) * w2)), q2))      rmssrqh_b */
+/*
+ * Per row r of n values (n <= 4096): when x16 is given, the residual add + RMSNorm of rmsadd_b
+ * (kernels_dsl.py:622-657; prefill_gpu.py:364, 378, 389):
+ *   d = srq(f32(x16[r]), x_q);  hidden[r] = (hidden[r] + d / sqrt(mean(d^2) + eps) * w1) * mult
+ * then y16[r] by mode, rms(h) = h / sqrt(mean(h^2) + eps) (rmssrqh_b :660-710, srqh_b :233-242,
+ * rmssrq_69 :158-206). x16 NULL: no add, y16 from hidden as it is (the input norm of layer 0,
+ * prefill_gpu.py:430-431). hidden f32 [n_rows][n], x16/y16 f16 [n_rows][n].
+ */
+int g4a_rows_tail(int n_rows, int n, const void* x16, float x_q, const float* w1, float mult, float eps,
+                  float* hidden, int mode, const float* w2, float q2, void* y16, void* stream);
+/*
+ * geglu_b (kernels_dsl.py:259-290; prefill_gpu.py:373-375) over n values (a multiple of 8):
+ *   y = gelu_tanh(srq(f32(gate16), gate_q)) * srq(f32(up16), up_q)
+ *   out16 = f16(clamp(round(y / out_q), -128, 127)) -- the code on out_q's grid, which the down
+ *   GEMM scales back with alpha = out_q --, or f16(y) when out_q is 0.
+ */
+int g4a_geglu16(int n, const void* gate16, const void* up16, float gate_q, float up_q, float out_q,
+                void* out16, void* stream);
+/*
+ * plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242; prefill_gpu.py:381-384) over n_rows
+ * rows of d values (a multiple of 8):
+ *   out16[s][o] = f16(srq(gelu_tanh(srq(f32(lin16[s][o]), lin_q)) * ple[s * ple_stride + o], out_q))
+ * ple: the layer's slice of the per-layer inputs [S][nL][d] (ple_stride = nL * d).
+ */
+int g4a_plegate16(int n_rows, int d, const void* lin16, float lin_q, const float* ple, int ple_stride,
+                  float out_q, void* out16, void* stream);
 
 #ifdef __cplusplus
 }

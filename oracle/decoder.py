@@ -21,6 +21,9 @@ It restates gemma4_150/reference.py's ReferenceSRQ over the exported model forma
                                                        reference.py:141-191
   * forward's tail (final norm, 2-bit lm_head, softcap)  reference.py:193-207
   * lm_head rows from export.py's blocked [24][vocab][4] words  export.py:91-93
+  * the layers-outer batched prefill's rounding points (f16 GEMM operands and products, the
+    row tails rmsadd_b / rmssrqh_b / rmssrq_69 / srqh_b, geglu_b's codes, plegate_b,
+    combine_b) ..................................... prefill_gpu.py:316-436
 
 The attention block itself is oracle.attention's (q/k/v from oracle.projection).
 `post_attention` and `ple_block` return every intermediate of a layer after its
@@ -32,7 +35,11 @@ Pinning (tests/test_oracle_decoder.py): gelu_tanh against the erf form of GELU a
 limits; rms_norm against a float64 loop and its scale invariance; qlin against a
 pure-Python triple loop over unpacked codes, and against the zero-point closed form;
 hand-packed embedding words; the lm_head block order against a row-major re-pack;
-argmax ties.
+argmax ties. The batched prefill's stages: gemm16 against a float64 triple loop (with alpha,
+and a transposed operand caught), rmsadd's closed forms (a constant row normalises to its
+sign, a zero row adds nothing), a known answer where rmssrqh_b's double rounding and a single
+rounding land on different srq codes, geglu_b's codes and clamp, and prefill_inputs against
+the decode step's token row (exact) and per-layer inputs.
 """
 from __future__ import annotations
 
@@ -157,3 +164,71 @@ def final_logits(man, x):
     rows = lmhead_rows(man.tensor("lmhead_blk"))
     W = dequant_rows(rows, man.tensor("lmhead_scale"), H, 2)
     return softcap_argmax(W @ xn, float(c["softcap"]))
+
+
+# --------------------------------------------------------------------------
+# the layers-outer batched prefill (prefill_gpu.py:316-436)
+# --------------------------------------------------------------------------
+# The same layer with the GPU runner's rounding points: every linear one f16 GEMM over the
+# S rows (weights dq_f16'd, activations f16(srq(..)), products f16), the tails between them
+# per row. `prefill_inputs` is the prompt's start (:412-431); the rest are the stages of
+# _layer (:356-395), each from the previous stage's value so a test can feed the GPU's own.
+def gemm16(a16, w16, alpha=1.0):
+    """gemm_tiled (kernels_dsl.py:34-136, tr = 1): f16(alpha * (a16 . w16^T)); the product of the
+    f16 operands accumulated in float64 (f32 on the GPU), scaled in f32 and rounded to f16."""
+    c = np.asarray(a16, np.float16).astype(np.float64) @ np.asarray(w16, np.float16).astype(np.float64).T
+    return (np.float32(alpha) * c.astype(np.float32)).astype(np.float16)
+
+
+def rmsadd(hidden, x16, x_q, w1, mult=1.0):
+    """rmsadd_b (kernels_dsl.py:622-657): hidden + rms(srq(f32(x16), x_q)) * w1, times mult."""
+    d = srq(np.asarray(x16, np.float16).astype(np.float32), x_q)
+    return ((np.asarray(hidden, np.float32) + rms_norm(d, w1)) * np.float32(mult)).astype(np.float32)
+
+
+def tail_operand(hidden, mode, w2=None, q2=0.0):
+    """The next GEMM's f16 operand from updated rows: "srq" = srqh_b (kernels_dsl.py:233-242),
+    "norm" = rmssrq_69 then srqh_b (:158-206), "norm16" = rmssrqh_b's f16(srq(f32(f16(n)), q2))
+    (:660-710: the normed value is narrowed to f16 before the srq as well as after)."""
+    h = np.asarray(hidden, np.float32)
+    z = h if mode == "srq" else rms_norm(h, w2)
+    if mode == "norm16":
+        z = z.astype(np.float16).astype(np.float32)
+    return srq(z, q2).astype(np.float16)
+
+
+def geglu_codes(g16, u16, gate_q, up_q, out_q):
+    """geglu_b (kernels_dsl.py:259-290): y = gelu(srq(f32(gate), gate_q)) * srq(f32(up), up_q),
+    stored as its code on out_q's grid, f16(clamp(round(y / out_q), -128, 127)) (f16(y) when
+    out_q is 0); the down GEMM scales it back with alpha = out_q (prefill_gpu.py:376-377)."""
+    y = (gelu_tanh(srq(np.asarray(g16, np.float16).astype(np.float32), gate_q))
+         * srq(np.asarray(u16, np.float16).astype(np.float32), up_q)).astype(np.float32)
+    if out_q == 0.0:
+        return y.astype(np.float16)
+    return np.clip(np.round(y / np.float32(out_q)), -128.0, 127.0).astype(np.float16)
+
+
+def plegate_operand(lin16, lin_q, ple_L, out_q):
+    """plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242; prefill_gpu.py:381-384):
+    f16(srq(gelu(srq(f32(lin), lin_q)) * ple, out_q)), ple the layer's per-layer inputs [S][d]."""
+    g = gelu_tanh(srq(np.asarray(lin16, np.float16).astype(np.float32), lin_q))
+    return srq((g * np.asarray(ple_L, np.float32)).astype(np.float32), out_q).astype(np.float16)
+
+
+def prefill_inputs(man, toks):
+    """The prompt's start (prefill_gpu.py:412-431): token rows (embed_00), the per-layer
+    model projection as one GEMM over f16(h) with an f16 product (srqh_b, _gemm, srq_b with
+    step 0), the per-layer table rows (plegather_01) and combine_b's
+    ple = (rms(ctx * H^-1/2, pl_proj_norm) + table) / sqrt 2. Returns (hidden [S][H],
+    ctx [S][nL*d], table [S][nL*d], ple [S][nL][d])."""
+    c = man.config
+    H, nL, d = int(c["H"]), int(c["nL"]), int(c["ple_d"])
+    toks = [int(t) for t in toks]
+    hidden = np.stack([embed_row(man.tensor("embed_q"), t, man.tensor("embed_scale"), H, 2, H,
+                                 float(c["embed_scale"])) for t in toks])
+    ctx = gemm16(hidden.astype(np.float16), man.tensor("pl_model_proj")).astype(np.float32)
+    table = np.stack([embed_row(man.tensor("ple_q"), t, man.tensor("ple_scale"), nL * d, 4, d,
+                                float(c["ple_scale"])) for t in toks])
+    ple = ((rms_norm(ctx.reshape(-1, nL, d) * np.float32(H ** -0.5), man.tensor("pl_proj_norm"))
+            + table.reshape(-1, nL, d)) * np.float32(2.0 ** -0.5)).astype(np.float32)
+    return hidden, ctx, table, ple

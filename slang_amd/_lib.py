@@ -30,8 +30,12 @@ EXPORTS = (
     "g4a_kv_write",
     "g4a_dequant", "g4a_qkv_gemv", "g4a_srqh", "g4a_gemm16",
     "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
-    "g4a_embed", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
+    "g4a_embed", "g4a_embed_rows", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
+    "g4a_rows_tail", "g4a_geglu16", "g4a_plegate16",
 )
+
+# g4a_rows_tail modes (g4attn.h)
+TAIL_NONE, TAIL_SRQ, TAIL_NORM, TAIL_NORM16 = 0, 1, 2, 3
 
 
 class G4ACfg(ctypes.Structure):
@@ -55,6 +59,7 @@ class G4AGemmMat(ctypes.Structure):
         ("n", ctypes.c_int),
         ("out_f32", ctypes.c_int),
         ("out_q", ctypes.c_float),
+        ("alpha", ctypes.c_float),
     ]
 
 
@@ -146,6 +151,14 @@ def load() -> ctypes.CDLL:
     lib.g4a_geglu.argtypes = [i, P, P, f, P, P]
     lib.g4a_embed.restype = ctypes.c_int
     lib.g4a_embed.argtypes = [i, i, P, ctypes.c_int64, P, P, i, f, P, P]
+    lib.g4a_embed_rows.restype = ctypes.c_int
+    lib.g4a_embed_rows.argtypes = [i, i, P, ctypes.c_int64, P, i, P, i, f, P, P]
+    lib.g4a_rows_tail.restype = ctypes.c_int
+    lib.g4a_rows_tail.argtypes = [i, i, P, f, P, f, f, P, i, P, f, P, P]
+    lib.g4a_geglu16.restype = ctypes.c_int
+    lib.g4a_geglu16.argtypes = [i, P, P, f, f, f, P, P]
+    lib.g4a_plegate16.restype = ctypes.c_int
+    lib.g4a_plegate16.argtypes = [i, i, P, f, P, i, f, P, P]
     lib.g4a_softcap_argmax.restype = ctypes.c_int
     lib.g4a_softcap_argmax_ws_bytes.restype = ctypes.c_size_t
     lib.g4a_softcap_argmax_ws_bytes.argtypes = [i]

@@ -395,13 +395,15 @@ __global__ __launch_bounds__(256) void geglu_kernel(int n, const float* a, const
 // out[j] = mult * row_scale[tok * (n / group) + j / group] * (code_j - 2^(bits-1)) for the
 // packed row tok of the table (reference.py:116-124 embed, 2-bit; :126-133 ple_table,
 // 4-bit with one scale per layer slice). The token id is read on the device, so a step can
-// start from the argmax of the previous one; an id past the table reads zeros.
+// start from the argmax of the previous one; an id past the table reads zeros. Grid row y
+// gathers token tok[y] into out + y*n (embed_00 / plegather_01 over S tokens).
 __global__ __launch_bounds__(256) void embed_kernel(int bits, int n, const uint32_t* table, uint32_t table_bytes,
                                                     int row_words, const int32_t* tok, const float* row_scale,
                                                     uint32_t scale_bytes, int group, float mult, float* out) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= n) return;
-    const int t = tok[0];
+    const int t = tok[blockIdx.y];
+    out += (size_t)blockIdx.y * n;
     const rsrc_t rt = make_rsrc(table, table_bytes);
     const rsrc_t rs = make_rsrc(row_scale, scale_bytes);
     const int vpw = 32 / bits;
@@ -727,8 +729,12 @@ extern "C" int g4a_geglu(int n, const float* a, const float* b, float out_q, flo
     return G4A_OK;
 }
 
-extern "C" int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok,
-                         const float* row_scale, int group, float mult, float* out, void* stream) {
+extern "C" int g4a_embed_rows(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok, int n_tok,
+                              const float* row_scale, int group, float mult, float* out, void* stream) {
+    if (n_tok <= 0 || n_tok > 65535) {
+        set_error("n_tok (%d) must be in [1, 65535]", n_tok);
+        return G4A_EINVAL;
+    }
     if (bits != 2 && bits != 4 && bits != 8) {
         set_error("bits %d not supported (2, 4 or 8)", bits);
         return G4A_EUNSUPPORTED;
@@ -746,12 +752,17 @@ extern "C" int g4a_embed(int bits, int n, const void* table, int64_t n_rows, con
         set_error("table, tok, row_scale and out must be non-NULL");
         return G4A_EINVAL;
     }
-    hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, bits, n,
+    hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256, n_tok), dim3(256), 0, (hipStream_t)stream, bits, n,
                        (const uint32_t*)table, (uint32_t)(n_rows * row_words * 4), row_words, tok, row_scale,
                        (uint32_t)(n_rows * (n / group) * 4), group, mult, out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "embed launch");
     return G4A_OK;
+}
+
+extern "C" int g4a_embed(int bits, int n, const void* table, int64_t n_rows, const int32_t* tok,
+                         const float* row_scale, int group, float mult, float* out, void* stream) {
+    return g4a_embed_rows(bits, n, table, n_rows, tok, 1, row_scale, group, mult, out, stream);
 }
 
 extern "C" size_t g4a_softcap_argmax_ws_bytes(int n) {

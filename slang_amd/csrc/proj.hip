@@ -163,7 +163,7 @@ struct Gemm16Args {
     const half_t* w[3];  // [N_p][K] f16
     void* out[3];        // [M][N_p] f16, or f32 (srq'd with out_q) when out_f32
     int n[3], out_f32[3];
-    float out_q[3];
+    float out_q[3], alpha[3];
     int tile_end[3];  // cumulative tiles (n_p / 128) * mtiles
 };
 
@@ -247,10 +247,11 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     }
 
     // D^T[n][m]: acc[r] is output n = 8(r/4) + 4h + r%4, token m = l32 of the 32x32 block;
-    // the product rounds to f16 (gemm_tiled), the q path then applies srq_b
+    // the product, times alpha, rounds to f16 (gemm_tiled's f16(alpha * acc)), the q path then
+    // applies srq_b
     const int N = g.n[p];
     const bool f32 = g.out_f32[p] != 0;
-    const float oq = g.out_q[p];
+    const float oq = g.out_q[p], alpha = g.alpha[p];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
         const int m = m0 + 64 * wm + 32 * mb + l32;
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
                 const int n = n0 + 64 * wn + 32 * nb + 8 * q + 4 * h;
                 float4v v;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = (float)(half_t)acc[nb][mb][4 * q + i];
+                for (int i = 0; i < 4; ++i) v[i] = (float)(half_t)pin(alpha * acc[nb][mb][4 * q + i]);
                 if (f32)
                     store4(reinterpret_cast<float*>(g.out[p]) + (size_t)m * N + n, srq4(v, oq));
                 else
@@ -332,6 +333,7 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
         g.n[i] = m ? m->n : 128;
         g.out_f32[i] = m ? m->out_f32 : 0;
         g.out_q[i] = m ? m->out_q : 0.0f;
+        g.alpha[i] = m && m->alpha != 0.0f ? m->alpha : 1.0f;
         g.tile_end[i] = tiles;
     }
     hipLaunchKernelGGL(gemm16_kernel<64>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);

@@ -26,10 +26,10 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
-from .projection import packed_bits
+from .projection import dequant, gemm16, packed_bits, srqh
 
 __all__ = ["qgemv", "norm_in", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
-           "DecoderStack", "EPS"]
+           "embed_rows", "rows_tail", "geglu16", "plegate16", "DecoderStack", "EPS"]
 
 EPS = 1e-6  # reference.py:27
 _WORDS = (torch.int32, torch.uint32)
@@ -147,6 +147,63 @@ def embed(table_u8, tok, row_scale, n: int, bits: int, group: int, mult: float, 
     return out
 
 
+def embed_rows(table_u8, tok, row_scale, n: int, bits: int, group: int, mult: float, out=None):
+    """embed for every id of tok (device int32 [S]): out [S][n] (embed_00 / plegather_01 over S
+    tokens, kernels_dsl.py:433-479)."""
+    _need(table_u8, "table", torch.uint8)
+    _need(tok, "tok", torch.int32)
+    _need(row_scale, "row_scale", torch.float32)
+    S = tok.numel()
+    if out is None:
+        out = torch.empty(S, n, dtype=torch.float32, device=table_u8.device)
+    _need(out, "out", torch.float32)
+    check(_lib.load().g4a_embed_rows(bits, n, _ptr(table_u8), table_u8.shape[0], _ptr(tok), S, _ptr(row_scale),
+                                     group, float(mult), _ptr(out), _stream()))
+    return out
+
+
+def rows_tail(hidden, x16=None, *, x_q: float = 0.0, w1=None, mult: float = 1.0, mode: int = _lib.TAIL_NONE,
+              w2=None, q2: float = 0.0, y16=None, eps: float = EPS):
+    """Per row of hidden f32 [S][n]: with x16 (f16 [S][n], a GEMM output) the residual add
+    hidden = (hidden + rms(srq(x16, x_q)) * w1) * mult (rmsadd_b), then the next GEMM operand
+    y16 f16 by mode: TAIL_SRQ f16(srq(hidden, q2)) (srqh_b), TAIL_NORM f16(srq(rms(hidden) * w2,
+    q2)) (rmssrq_69), TAIL_NORM16 f16(srq(f32(f16(rms(hidden) * w2)), q2)) (rmssrqh_b)
+    (kernels_dsl.py:158-206, 233-242, 622-710). Returns y16."""
+    _need(hidden, "hidden", torch.float32)
+    _need(x16, "x16", torch.float16)
+    S, n = hidden.shape
+    if mode != _lib.TAIL_NONE and y16 is None:
+        y16 = torch.empty(S, n, dtype=torch.float16, device=hidden.device)
+    _need(y16, "y16", torch.float16)
+    check(_lib.load().g4a_rows_tail(S, n, _ptr(x16), float(x_q), _ptr(w1), float(mult), float(eps), _ptr(hidden),
+                                    int(mode), _ptr(w2), float(q2), _ptr(y16), _stream()))
+    return y16
+
+
+def geglu16(gate16, up16, gate_q: float, up_q: float, out_q: float, out=None):
+    """geglu_b (kernels_dsl.py:259-290): f16 code round(gelu(srq(g, gate_q)) * srq(u, up_q) / out_q)."""
+    _need(gate16, "gate", torch.float16)
+    _need(up16, "up", torch.float16)
+    if out is None:
+        out = torch.empty_like(gate16)
+    check(_lib.load().g4a_geglu16(gate16.numel(), _ptr(gate16), _ptr(up16), float(gate_q), float(up_q),
+                                  float(out_q), _ptr(out), _stream()))
+    return out
+
+
+def plegate16(lin16, lin_q: float, ple, ple_stride: int, out_q: float, out=None):
+    """plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242): f16(srq(gelu(srq(lin, lin_q)) *
+    ple, out_q)) over lin16 f16 [S][d]; ple points at the layer's slice of [S][nL][d] (row stride
+    ple_stride values)."""
+    _need(lin16, "lin", torch.float16)
+    S, d = lin16.shape
+    if out is None:
+        out = torch.empty_like(lin16)
+    check(_lib.load().g4a_plegate16(S, d, _ptr(lin16), float(lin_q), _ptr(ple), int(ple_stride), float(out_q),
+                                    _ptr(out), _stream()))
+    return out
+
+
 def softcap_argmax(logits, cap: float, tok=None, ws=None):
     """logits <- cap * tanh(logits / cap) in place; tok[0] = first argmax (reference.py:207).
     ws: a byte tensor of at least g4a_softcap_argmax_ws_bytes(n) (allocated when absent)."""
@@ -233,6 +290,7 @@ class DecoderStack:
         self.arg_ws = torch.empty(_lib.load().g4a_softcap_argmax_ws_bytes(self.vocab), dtype=torch.uint8,
                                   device=device)
         self.tok = torch.zeros(1, dtype=torch.int32, device=device)
+        self.dq16, self._pb = {}, None  # batched prefill: f16 weights and activation buffers
 
     def embed_token(self):
         """x = embed(tok), ple_in = ple_input(tok, x), and layer 0's srq'd input norm
@@ -297,6 +355,135 @@ class DecoderStack:
                      w2=self.final_norm, out2=self.hf)
             snap("x3", self.x)
             snap("hf", self.hf)
+
+    # ---------------------------------------------------------------- batched prefill
+    def _prefill_weights(self, L: int) -> dict:
+        """Layer L's o_proj, MLP and per-layer-embedding linears dequantised to f16 once and kept
+        resident (PrefillGPU._dq dequantises them into scratch on every prefill,
+        prefill_gpu.py:186-200; one GPU's HBM holds every layer's f16 copy many times over)."""
+        if L not in self.dq16:
+            s, w, H, d = self.man.layers[L], self.w[L], self.H, self.d
+            it = s.intermediate
+            self.dq16[L] = {
+                "o": dequant(w["o_bits"], w["o_scale"], s.q_dim, H, bits=w["o_bits_n"]),
+                "gate": dequant(w["gate_bits"], w["gate_scale"], H, it, bits=w["gate_bits_n"]),
+                "up": dequant(w["up_bits"], w["up_scale"], H, it, bits=w["gate_bits_n"]),
+                "down": dequant(w["down_bits"], w["down_scale"], it, H, bits=w["down_bits_n"]),
+                "plegate": dequant(w["plegate_codes"], w["plegate_rowscale"], H, d, bits=8),
+                "pleproj": dequant(w["pleproj_codes"], w["pleproj_rowscale"], d, H, bits=8)}
+        return self.dq16[L]
+
+    def _prefill_buffers(self, S: int):
+        """Activations of an S-token prefill (flat, kept for later prompts of at most S tokens);
+        returns take(name, *shape), a contiguous view of the first prod(shape) values."""
+        if self._pb is None or self._pb["S"] < S:
+            H, nL, d = self.H, self.nL, self.d
+            it = max(s.intermediate for s in self.man.layers)
+            qd = max(s.q_dim for s in self.man.layers)
+            f32 = lambda n: torch.empty(S * n, dtype=torch.float32, device=self.device)  # noqa: E731
+            f16 = lambda n: torch.empty(S * n, dtype=torch.float16, device=self.device)  # noqa: E731
+            self._pb = {"S": S, "hidden": f32(H), "ctx": f32(nL * d), "plegath": f32(nL * d), "ple": f32(nL * d),
+                        "a16": f16(H), "attn": f16(qd), "o16": f16(H), "y2": f16(H), "g16": f16(it),
+                        "u16": f16(it), "gg16": f16(it), "d16": f16(H), "hh": f16(H), "plin": f16(d),
+                        "gph": f16(d), "pp16": f16(H), "ids": torch.empty(S, dtype=torch.int32, device=self.device)}
+        pb = self._pb
+        return lambda name, *shape: pb[name][:int(np.prod(shape))].view(*shape)
+
+    def prefill(self, toks, start_pos: int = 0, trace: list | None = None) -> int:
+        """Run S prompt tokens through every layer at positions start_pos.., layers outer and
+        tokens inner, leaving the K/V caches filled (PrefillGPU.prefill, prefill_gpu.py:398-436;
+        the layer is _layer, :316-395). Each linear is one f16 GEMM over all S rows (weights
+        dequantised once, activations f16(srq(..)) as srqh_b makes them, products f16 as
+        gemm_tiled rounds them), the attention one batched causal prefill. Like the reference
+        it makes no logits: decoding continues from the next token. toks: host ints or a device
+        int32 tensor [S]. Returns start_pos + S. trace: gets one dict per layer of its stages."""
+        ids = toks if torch.is_tensor(toks) else torch.tensor(list(toks), dtype=torch.int32)
+        S = int(ids.numel())
+        if S <= 0:
+            return start_pos
+        if start_pos < 0 or start_pos + S > self.attn.max_seq:
+            raise ValueError(f"positions [{start_pos}, {start_pos + S}) outside the {self.attn.max_seq}-row caches")
+        take = self._prefill_buffers(S)
+        H, nL, d = self.H, self.nL, self.d
+        tid = take("ids", S)
+        tid.copy_(ids.to(device=self.device, dtype=torch.int32), non_blocking=True)
+        hid, ple, ctx, plegath = take("hidden", S, H), take("ple", S, nL, d), take("ctx", S, nL * d), \
+            take("plegath", S, nL * d)
+        snap = (lambda t, k, v: t.__setitem__(k, v.clone())) if trace is not None else (lambda t, k, v: None)
+        # token embeddings and the per-layer inputs (prefill_gpu.py:412-429)
+        embed_rows(self.embed_q, tid, self.embed_sc, H, 2, H, self.embed_scale, out=hid)
+        a16 = take("a16", S, H)
+        srqh(hid, 0.0, out=a16)
+        gemm16(a16, [(self.pl_proj, ctx, 0.0)])       # f32(f16(h . P^T)): srq_b with step 0
+        embed_rows(self.ple_q, tid, self.ple_sc, nL * d, 4, d, self.ple_scale, out=plegath)
+        rms_norm(ctx.view(S * nL, d), self.pl_norm, res=plegath.view(S * nL, d), pre=H ** -0.5,
+                 mult=2.0 ** -0.5, out=ple.view(S * nL, d))    # combine_b
+        if trace is not None:
+            trace.append({"hidden": hid.clone(), "ctx": ctx.clone(), "plegath": plegath.clone(), "ple": ple.clone()})
+        rows_tail(hid, mode=_lib.TAIL_NORM, w2=self.w[0]["in_norm"], q2=self.man.layers[0].scales["qkv_in"], y16=a16)
+        for L in range(nL):
+            s, w, wd = self.man.layers[L], self.w[L], self._prefill_weights(L)
+            sc, it = s.scales, s.intermediate
+            t = {} if trace is not None else None
+            snap(t, "a16", a16)
+            snap(t, "x0", hid)
+            attn = self.attn.prefill_layer(L, start_pos, a16, out=take("attn", S, s.q_dim // s.head_dim, s.head_dim),
+                                           trace=t).view(S, s.q_dim)
+            snap(t, "attn", attn)
+            o16, y2 = take("o16", S, H), take("y2", S, H)
+            gemm16(attn, [(wd["o"], o16, None)])
+            rows_tail(hid, o16, x_q=sc["o_out"], w1=w["o_w1"], mode=_lib.TAIL_NORM16, w2=w["o_w2"],
+                      q2=sc["gate_in"], y16=y2)
+            snap(t, "o16", o16)
+            snap(t, "x1", hid)
+            snap(t, "y2", y2)
+            g16, u16, gg = take("g16", S, it), take("u16", S, it), take("gg16", S, it)
+            gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)])
+            geglu16(g16, u16, sc["gate_out"], sc["up_out"], sc["down_in"], out=gg)
+            snap(t, "g16", g16)
+            snap(t, "u16", u16)
+            snap(t, "gg16", gg)
+            d16, hh = take("d16", S, H), take("hh", S, H)
+            gemm16(gg, [(wd["down"], d16, None, sc["down_in"])])
+            rows_tail(hid, d16, x_q=sc["down_out"], w1=w["down_nw"], mode=_lib.TAIL_SRQ, q2=sc["plegate_in"], y16=hh)
+            snap(t, "d16", d16)
+            snap(t, "x2", hid)
+            snap(t, "hh", hh)
+            plin, gph, pp = take("plin", S, d), take("gph", S, d), take("pp16", S, H)
+            gemm16(hh, [(wd["plegate"], plin, None)])
+            plegate16(plin, sc["plegate_out"], ple[:, L], nL * d, sc["pleproj_in"], out=gph)
+            gemm16(gph, [(wd["pleproj"], pp, None)])
+            snap(t, "plin", plin)
+            snap(t, "gph", gph)
+            snap(t, "pp16", pp)
+            if L + 1 < nL:  # the next layer's srq'd input norm as its GEMM operand (rmssrq_69 + srqh_b)
+                rows_tail(hid, pp, x_q=sc["pleproj_out"], w1=w["post_ple"], mult=w["layer_scalar"],
+                          mode=_lib.TAIL_NORM, w2=self.w[L + 1]["in_norm"],
+                          q2=self.man.layers[L + 1].scales["qkv_in"], y16=a16)
+            else:
+                rows_tail(hid, pp, x_q=sc["pleproj_out"], w1=w["post_ple"], mult=w["layer_scalar"])
+            snap(t, "x3", hid)
+            if trace is not None:
+                trace.append(t)
+        return start_pos + S
+
+    def generate(self, ids, n_new: int, start_pos: int = 0) -> torch.Tensor:
+        """Greedy generation kept on the GPU (G4Runner.generate_resident, runner.py:542-569):
+        prefill every prompt token but the last, then n_new decode steps from the last one, each
+        step's argmax feeding the next step's embedding on the device. Returns the n_new tokens
+        (device int32); the caller reads them back when it wants them."""
+        ids = list(ids)
+        if not ids or n_new <= 0:
+            return torch.empty(0, dtype=torch.int32, device=self.device)
+        pos = self.prefill(ids[:-1], start_pos) if len(ids) > 1 else start_pos
+        if pos + n_new > self.attn.max_seq:
+            raise ValueError(f"{pos + n_new} positions exceed the {self.attn.max_seq}-row caches")
+        self.tok.fill_(int(ids[-1]))
+        out = torch.empty(n_new, dtype=torch.int32, device=self.device)
+        for i in range(n_new):
+            self.step(pos + i)
+            out[i:i + 1].copy_(self.tok)
+        return out
 
     def head(self):
         """2-bit lm_head over the final norm, softcap and argmax into self.tok (reference.py:200-207)."""

@@ -294,11 +294,12 @@ class AttentionStack:
                 self.dq[L] = (wq, wk, wv)
         return self.dq[L]
 
-    def prefill_layer(self, L: int, start_pos: int, a: torch.Tensor, out=None):
+    def prefill_layer(self, L: int, start_pos: int, a: torch.Tensor, out=None, trace: dict | None = None):
         """Layer L's attention for S tokens at positions start_pos.. from their normed inputs
-        a f32 [S][H]: dequantised q/k/v GEMMs (q srq'd with q_out, k/v f16), kvnorm_b with
-        srq(k_out / v_out) on non-shared layers, then causal prefill attention. Returns the
-        attention output f16 [S][nH][hd] (prefill_gpu.py:327-354)."""
+        a f32 [S][H] (or already the GEMM operand f16(srq(a, qkv_in)) [S][H]): dequantised
+        q/k/v GEMMs (q srq'd with q_out, k/v f16), kvnorm_b with srq(k_out / v_out) on
+        non-shared layers, then causal prefill attention. Returns the attention output f16
+        [S][nH][hd] (prefill_gpu.py:327-354). trace: gets q, kraw and vraw."""
         s, man = self.man.layers[L], self.man
         S = a.shape[0]
         if start_pos < 0 or start_pos + S > self.max_seq:
@@ -306,7 +307,20 @@ class AttentionStack:
         cfg = man.attn_config(L)
         sc = s.scales
         wq, wk, wv = self._dequant(L)
-        q, kraw, vraw = P.prefill_qkv(a, wq, wk, wv, a_in_q=sc.get("qkv_in", 0.0), q_out=sc.get("q_out", 0.0))
+        if a.dtype == torch.float16:  # the operand is made: the three GEMMs straight from it
+            q = torch.empty(S, wq.shape[0], device=a.device, dtype=torch.float32)
+            mats = [(wq, q, sc.get("q_out", 0.0))]
+            kraw = vraw = None
+            if wk is not None:
+                kraw = torch.empty(S, wk.shape[0], device=a.device, dtype=torch.float16)
+                vraw = torch.empty(S, wv.shape[0], device=a.device, dtype=torch.float16)
+                mats += [(wk, kraw, None), (wv, vraw, None)]
+            P.gemm16(a, mats)
+        else:
+            q, kraw, vraw = P.prefill_qkv(a, wq, wk, wv, a_in_q=sc.get("qkv_in", 0.0), q_out=sc.get("q_out", 0.0))
+        if trace is not None:
+            trace.update(q=q.clone(), kraw=None if kraw is None else kraw.clone(),
+                         vraw=None if vraw is None else vraw.clone())
         kc, vc = self.caches(L)
         cos, sin = self._rows(L, start_pos, start_pos + S)
         if not s.shared:

@@ -139,14 +139,16 @@ def srqh(a, a_in_q: float = 0.0, out=None):
 def gemm16(a16, mats):
     """Up to three products sharing the f16 activation a16 [M][K], one launch (g4a_gemm16).
 
-    mats: sequence of (w_f16 [N][K], out, out_q or None); out f16 [M][N] gets the f16 GEMM
-    result (gemm_tiled), out f32 [M][N] gets srq(f32(f16 result), out_q) (srq_b)."""
+    mats: sequence of (w_f16 [N][K], out, out_q or None[, alpha]); out f16 [M][N] gets the f16
+    GEMM result f16(alpha * sum) (gemm_tiled), out f32 [M][N] gets srq(f32(that), out_q) (srq_b)."""
     _need(a16, "a16", torch.float16)
     M, K = a16.shape
     if not 1 <= len(mats) <= 3:
         raise ValueError("gemm16 takes 1 to 3 matrices")
     tab = (_lib.G4AGemmMat * len(mats))()
-    for i, (w, out, oq) in enumerate(mats):
+    for i, m in enumerate(mats):
+        w, out, oq = m[:3]
+        alpha = float(m[3]) if len(m) > 3 else 1.0
         _need(w, "w_f16", torch.float16)
         _need(out, "out", (torch.float16, torch.float32))
         if w.dim() != 2 or w.shape[1] != K:
@@ -154,7 +156,7 @@ def gemm16(a16, mats):
         if out.numel() != M * w.shape[0]:
             raise ValueError("out must hold M*N values")
         tab[i] = _lib.G4AGemmMat(w.data_ptr(), out.data_ptr(), w.shape[0], int(out.dtype == torch.float32),
-                                 float(oq or 0.0))
+                                 float(oq or 0.0), alpha)
     check(_lib.load().g4a_gemm16(M, K, _ptr(a16), len(mats), tab, _stream()))
 
 

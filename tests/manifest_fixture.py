@@ -20,23 +20,27 @@ SCHEDULE = [(True, 256, 128, False, 0), (False, 512, 64, False, 1),
 
 
 class _Writer:
+    """Lays tensors out as export.py's Writer does; the bytes go to the file at close(), so a
+    tensor's contents may still be set after later tensors were put (its size may not)."""
+
     def __init__(self, path):
-        self.f = open(path, "wb")
+        self.path = path
         self.pos = 0
         self.tensors = {}
+        self.arrays = []
 
     def put(self, name, arr, dtype):
-        b = np.ascontiguousarray(arr).tobytes()
-        self.f.write(b)
-        self.tensors[name] = {"off": self.pos, "len": len(b), "dtype": dtype, "shape": list(arr.shape)}
-        self.pos += len(b)
-        pad = (-len(b)) % 4
-        if pad:
-            self.f.write(b"\0" * pad)
-            self.pos += pad
+        a = np.ascontiguousarray(arr)
+        self.tensors[name] = {"off": self.pos, "len": a.nbytes, "dtype": dtype, "shape": list(a.shape)}
+        self.arrays.append((self.pos, a))
+        self.pos += a.nbytes + (-a.nbytes) % 4
 
     def close(self):
-        self.f.close()
+        with open(self.path, "wb") as f:
+            for off, a in self.arrays:
+                f.seek(off)
+                f.write(a.tobytes())
+            f.truncate(self.pos)
 
 
 def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHEDULE, seed=0,
@@ -110,6 +114,10 @@ def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHED
         layers.append({"index": L, "sliding": sliding, "head_dim": hd, "q_dim": q_dim,
                        "intermediate": 4 * H, "shared": shared, "kv_source": src,
                        "rope_theta": 1e4 if sliding else 1e6, "rope_cutoff": cutoff, "scales": sc})
+    if full:  # export.py:110, 119-122: the middle third of pleproj_w12s is the next layer's
+        for L in range(nL):  # input norm, the final norm after the last layer
+            nxt = arrays[f"L{L + 1}.in_norm"] if L + 1 < nL else arrays["final_norm"]
+            arrays[f"L{L}.pleproj_w12s"][H:2 * H] = nxt
     w.close()
     man = {"config": {"H": H, "nL": nL, "nH": n_heads, "vocab": vocab if full else 16, "window": window,
                       "softcap": 30.0, "ple_d": ple_d if full else 8, "embed_scale": float(np.sqrt(H)),

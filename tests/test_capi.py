@@ -161,9 +161,10 @@ def test_projection_argument_errors(lib):
 
 
 def test_gemm_mat_struct_layout():
-    """struct g4a_gemm_mat: two pointers, two ints, a float (8-byte aligned, 32 bytes)."""
-    assert [f[0] for f in _lib.G4AGemmMat._fields_] == ["w_f16", "out", "n", "out_f32", "out_q"]
+    """struct g4a_gemm_mat: two pointers, two ints, two floats (8-byte aligned, 32 bytes)."""
+    assert [f[0] for f in _lib.G4AGemmMat._fields_] == ["w_f16", "out", "n", "out_f32", "out_q", "alpha"]
     assert _lib.G4AGemmMat.n.offset == 16 and _lib.G4AGemmMat.out_q.offset == 24
+    assert _lib.G4AGemmMat.alpha.offset == 28
     assert ctypes.sizeof(_lib.G4AGemmMat) == 32
 
 

@@ -103,3 +103,76 @@ def test_stage_functions_compose_to_reference_layer(tmp_path):
     assert s.intermediate == 4 * H and OD.bits_of(m, f"L{L}.gate_bits", 4 * H, H) == 2
     assert abs(pb["x3"] - (st["x2"] + OD.rms_norm(pb["pleproj"], t("pleproj_w12s")[:H])) * t("pleproj_w12s")[2 * H]
                ).max() < 1e-5
+
+
+# ---------------------------------------------------------------- the batched prefill's stages
+def test_prefill_gemm16_against_a_loop_and_alpha():
+    """gemm_tiled's f16(alpha * A . W^T) against a pure-Python float64 loop on a tiny case."""
+    rng = np.random.default_rng(21)
+    a = rng.standard_normal((3, 5)).astype(np.float16)
+    w = rng.standard_normal((4, 5)).astype(np.float16)
+    for alpha in (1.0, 0.01):
+        ref = np.empty((3, 4), np.float16)
+        for m in range(3):
+            for n in range(4):
+                acc = sum(float(a[m, k]) * float(w[n, k]) for k in range(5))
+                ref[m, n] = np.float16(np.float32(alpha) * np.float32(acc))
+        np.testing.assert_array_equal(OD.gemm16(a, w, alpha), ref)
+    # a transposed operand (A . W instead of A . W^T) is caught
+    sq = rng.standard_normal((4, 4)).astype(np.float16)
+    assert not np.array_equal(OD.gemm16(sq, sq.T.copy()), OD.gemm16(sq, sq))
+
+
+def test_prefill_row_tails_closed_forms():
+    """rmsadd_b: a constant row normalises to its sign times w1; a zero row adds nothing. The
+    tail operands: srq grid codes; rmssrqh_b's double rounding differs from one rounding
+    exactly where the f16 narrowing crosses an srq midpoint (kernels_dsl.py:667-671)."""
+    H = 8
+    hid = np.arange(H, dtype=np.float32)
+    w1 = np.linspace(0.5, 1.5, H).astype(np.float32)
+    x = np.full(H, -3.0, np.float16)
+    np.testing.assert_allclose(OD.rmsadd(hid, x, 0.0, w1, 2.0), (hid - w1) * 2, rtol=1e-6)
+    np.testing.assert_array_equal(OD.rmsadd(hid, np.zeros(H, np.float16), 0.0, w1), hid)
+    # srq mode: codes of hidden on q2's grid
+    h = np.array([[0.014, 0.016, -0.5, 2.0]], np.float32)
+    np.testing.assert_array_equal(OD.tail_operand(h, "srq", q2=0.01), np.array([[0.01, 0.02, -0.5, 1.27]], np.float16))
+    # norm vs norm16: z = 0.0150001 on a 0.01 grid: f16(z) = 0.0149994 rounds down, z itself up
+    z = np.float32(0.0150001)
+    w2 = np.full(4, z, np.float32)
+    ones = np.ones((1, 4), np.float32)            # rms(ones) = 1, so the normed value is w2
+    assert float(OD.tail_operand(ones, "norm", w2, 0.01)[0, 0]) == np.float16(0.02)
+    assert float(OD.tail_operand(ones, "norm16", w2, 0.01)[0, 0]) == np.float16(0.01)
+
+
+def test_geglu_codes_and_plegate_operand():
+    """geglu_b stores the code of y on out_q's grid (gelu(0) = 0 gives code 0; y at k * out_q
+    gives k; codes clamp to [-128, 127]); plegate_b + srqh_b is srq(gelu(srq(lin)) * ple)."""
+    g = np.array([0.0, 0.5, 0.25, 40.0], np.float16)
+    u = np.array([5.0, 1.0, 2.0, 1.0], np.float16)
+    y = OD.gelu_tanh(g.astype(np.float32)) * u.astype(np.float32)
+    codes = OD.geglu_codes(g, u, 0.0, 0.0, 0.01)
+    assert codes[0] == 0 and codes[3] == 127
+    np.testing.assert_array_equal(codes[1:3], np.round(y[1:3] / np.float32(0.01)).astype(np.float16))
+    np.testing.assert_array_equal(OD.geglu_codes(g, u, 0.0, 0.0, 0.0), y.astype(np.float16))
+    lin = np.array([[0.031, -0.2]], np.float16)
+    ple = np.array([[2.0, -1.0]], np.float32)
+    ref = OD.srq(OD.gelu_tanh(OD.srq(lin.astype(np.float32), 0.03)) * ple, 0.05).astype(np.float16)
+    np.testing.assert_array_equal(OD.plegate_operand(lin, 0.03, ple, 0.05), ref)
+
+
+def test_prefill_inputs_match_the_decode_step_inputs(tmp_path):
+    """The batched start (embed_00, the per-layer projection as an f16 GEMM, combine_b) gives the
+    decode step's token row exactly and its per-layer inputs (reference.py:133-139) up to the
+    f16 rounding of the projection's operands and product."""
+    from slang_amd.manifest import load_manifest
+    write_model(tmp_path, full=True, seed=2, H=256, ple_d=128, vocab=64)
+    m = load_manifest(tmp_path)
+    toks = [3, 17, 63]
+    hidden, ctx, table, ple = OD.prefill_inputs(m, toks)
+    for i, t in enumerate(toks):
+        x = OD.embed_row(m.tensor("embed_q"), t, m.tensor("embed_scale"), m.hidden, 2, m.hidden,
+                         float(m.config["embed_scale"]))
+        np.testing.assert_array_equal(hidden[i], x)
+        ref = OD.ple_input(m, t, x)
+        assert np.abs(ple[i] - ref).max() < 2e-2 * np.abs(ref).max()
+        assert np.abs(ple[i] - ref).mean() < 2e-3 * np.abs(ref).mean()
