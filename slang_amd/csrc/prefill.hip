@@ -39,6 +39,8 @@ struct PrefillArgs {
     int split_tiles, max_pieces, pieces_per_head;
     int xcd_runs;  // prefill_kernel_w32 unsplit: 1-D grid, query blocks in contiguous runs per XCD
     const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
+    const half_t* q16lo;  // ... and with G4A_Q_HILO its f16 low parts (q - f32(q16))
+    int kv_row0;  // prefill_kernel_w32: first row held in kc/vc (rows below it are never read)
     half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
                       // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
     float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
@@ -80,7 +82,7 @@ __device__ __forceinline__ half4 lds_tr16(const half_t* p) {
 template <int HD>
 __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float* gain, const float* rcos,
                                                     const float* rsin, half_t* out, int rows, int n_q_heads,
-                                                    float eps) {
+                                                    float eps, half_t* out_lo) {
     constexpr int KSTEPS = HD / 32;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 16 + n;
@@ -93,10 +95,14 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
     if (!ok) return;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-        half8 hv;
+        half8 hv, lv;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) hv[i] = (half_t)x[s][i];
+        for (int i = 0; i < 8; ++i) {
+            hv[i] = (half_t)x[s][i];
+            lv[i] = (half_t)(x[s][i] - (float)hv[i]);  // the f32-accurate split of G4A_Q_HILO
+        }
         *reinterpret_cast<half8*>(out + (size_t)row * HD + 32 * s + 8 * g) = hv;
+        if (out_lo) *reinterpret_cast<half8*>(out_lo + (size_t)row * HD + 32 * s + 8 * g) = lv;
     }
 }
 
@@ -291,9 +297,10 @@ __device__ __forceinline__ int xcd_run_index() {
     return x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
 }
 
-template <int G, typename OUTT>
+template <int G, typename OUTT, bool HILO>
 __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
+    constexpr int QMF = HILO ? 2 : 1;  // score MFMAs per K operand (q high, then low parts)
     constexpr int ROWB = HD * 2;      // bytes per LDS tile row
     constexpr int TILEB = KT * ROWB;  // one K or V tile
     __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
@@ -371,11 +378,12 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 
     // K/V of this kv head through buffer resources: rows >= kv_hi read as zeros
     const int rowg = a.n_kv_heads * HD * 2;  // global bytes per cache row
-    const rsrc_t rk = make_rsrc(reinterpret_cast<const half_t*>(a.kc) + (size_t)kh * HD, (uint32_t)kv_hi * rowg);
-    const rsrc_t rv = make_rsrc(reinterpret_cast<const half_t*>(a.vc) + (size_t)kh * HD, (uint32_t)kv_hi * rowg);
+    // (rows from kv_row0: a cache converted to f16 for this call holds only the attended rows)
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const half_t*>(a.kc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const half_t*>(a.vc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
     // wave w fills tile rows 16w .. 16w+15, two rows (1 KiB) per instruction
     auto issue = [&](int t, int buf) {
-        const int kb = wg_lo + t * KT;
+        const int kb = wg_lo + t * KT - a.kv_row0;
         char* kdst = lds + buf * 2 * TILEB;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     // operand layout of the 32x32x16 MFMA. The arithmetic, including the order of the
     // sum of squares, is that of prep_q_column (qprep_kernel), so both round q to the
     // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
-    half8 qf[16];
+    half8 qf[16], ql[HILO ? 16 : 1];
     if (a.q16) {  // q prepared by qprep_kernel for every piece of the call at once
         // Wave w DMAs the f16 q rows of its own 32 columns (two 512-byte rows per
         // instruction, chunk n32 of a row from logical chunk n32 ^ (row % 32)) into the LDS
@@ -416,12 +424,22 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
         for (int s = 0; s < 16; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage free for tile t0 + 1's DMA
+        if constexpr (HILO) {  // the low parts straight into the operand layout
+            const rsrc_t rql = make_rsrc(a.q16lo, (uint32_t)a.S * a.n_q_heads * HD * 2);
+            const int qo = (s_idx * a.n_q_heads + kh * G + hh) * ROWB + 16 * h;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) ql[s] = bload_h8(rql, qo + 32 * s);
+        }
         if (!col_ok) {
 #pragma unroll
-            for (int s = 0; s < 16; ++s) qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            for (int s = 0; s < 16; ++s) qf[s] = ql[HILO ? s : 0] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+        if constexpr (HILO) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(ql[s]));
+        }
     } else {
         // workgroup-uniform resources (a per-lane base would make the compiler loop over
         // lanes); the row of this lane's column is in the offset
@@ -531,11 +549,18 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
         for (int s = 0; s < 16; ++s)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+            for (int i = 0; i < 8; ++i) {
+                qf[s][i] = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
+                if constexpr (HILO) ql[s][i] = col_ok ? (half_t)(x[s][i] - (float)qf[s][i]) : (half_t)0.0f;
+            }
         // q is only ever an MFMA B operand, which may sit in AGPRs: that leaves the VGPRs to
         // the O^T accumulators, the scores and the LDS operand batches
 #pragma unroll
         for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+        if constexpr (HILO) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(ql[s]));
+        }
     }
 
     // ---- key ranges: this wave [w_lo, wp1], this column [col_lo, pos]
@@ -584,17 +609,19 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 sacc[0] = mfma32(kv0[s], qf[s0 + s], sacc[0]);
+                if constexpr (HILO) sacc[0] = mfma32(kv0[s], ql[s0 + s], sacc[0]);
                 sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
+                if constexpr (HILO) sacc[1] = mfma32(kv1[s], ql[s0 + s], sacc[1]);
             }
         }
         // keep kQkAhead LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
         __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);
 #pragma unroll
         for (int i = 0; i < 32 - kQkAhead; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, QMF, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, QMF * kQkAhead, 0);
 
         // scores of this lane: key kb + 4h + 32kt + 8(r/4) + r%4 of its column, log2 domain;
         // tiles inside every column's range skip the per-element mask
@@ -763,8 +790,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 }
 
 template <int G>
-static void (*pick_w32(bool out32))(PrefillArgs) {
-    return out32 ? prefill_kernel_w32<G, float> : prefill_kernel_w32<G, half_t>;
+static void (*pick_w32(bool out32, bool hilo))(PrefillArgs) {
+    if (hilo) return out32 ? prefill_kernel_w32<G, float, true> : prefill_kernel_w32<G, half_t, true>;
+    return out32 ? prefill_kernel_w32<G, float, false> : prefill_kernel_w32<G, half_t, false>;
 }
 
 typedef void (*prefill_fn)(PrefillArgs);
@@ -803,17 +831,27 @@ using namespace g4a;
 // per CU (3 / 5 / 9 / 33) was up to 24 % slower beyond S 1024.
 struct PrefillSplit {
     int split_tiles, max_pieces, n_qblocks, total_pieces;
-    size_t o_bytes, ml_bytes, q16_bytes, total;
+    int kv_row0, kv_rows;  // f32 caches: the attended rows copied to f16
+    size_t kv16_bytes, o_bytes, ml_bytes, q16_bytes, q16lo_bytes, total;
 };
-static bool use_w32(const g4a_cfg* cfg) {
-    return cfg->head_dim == 256 && !(cfg->flags & (G4A_KV_F32 | G4A_Q_HILO));
-}
+// hd 256 runs the 32-column kernel in every mode. f32 caches go through an f16 copy of the
+// attended rows in the workspace (the 16-column kernel rounds them to f16 as it stages
+// them, so the operands are the same values); G4A_Q_HILO adds q's f16 low parts as a second
+// score operand. Without the workspace an f32-cache call runs the 16-column kernel.
+static bool use_w32(const g4a_cfg* cfg) { return cfg->head_dim == 256; }
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
-    PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0};
+    PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (!use_w32(cfg) || S <= 0 || cfg->n_kv_heads == 0) return p;
     const int G = (int)(cfg->n_q_heads / cfg->n_kv_heads);
     if (G < 1 || 128 % G) return p;
     const int BQ = 128 / G, KT = 64, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
+    if (cfg->flags & G4A_KV_F32) {
+        p.kv_row0 = W > 0 && start_pos + 1 - W > 0 ? start_pos + 1 - W : 0;
+        p.kv_rows = start_pos + S - p.kv_row0;
+        p.kv16_bytes = 2 * align256((size_t)p.kv_rows * kvH * 256 * sizeof(half_t));
+    }
+    p.total = p.kv16_bytes;
     p.n_qblocks = (S + BQ - 1) / BQ;
     if ((long)p.n_qblocks * kvH >= 512) return p;
     // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
@@ -845,10 +883,25 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     }
     const size_t slots = (size_t)kvH * p.n_qblocks * pieces * 128;
     p.o_bytes = slots * 256 * sizeof(half_t);
-    p.ml_bytes = (slots * sizeof(float2) + 255) & ~(size_t)255;
-    p.q16_bytes = ((size_t)S * cfg->n_q_heads * 256 * sizeof(half_t) + 255) & ~(size_t)255;
-    p.total = p.o_bytes + p.ml_bytes + p.q16_bytes;
+    p.ml_bytes = align256(slots * sizeof(float2));
+    p.q16_bytes = align256((size_t)S * cfg->n_q_heads * 256 * sizeof(half_t));
+    p.q16lo_bytes = (cfg->flags & G4A_Q_HILO) ? p.q16_bytes : 0;
+    p.total = p.kv16_bytes + p.o_bytes + p.ml_bytes + p.q16_bytes + p.q16lo_bytes;
     return p;
+}
+
+// f32 -> f16 copy (round to nearest even) of n8 groups of 8 cache values, K and V
+__global__ __launch_bounds__(256) void kv16_kernel(const float* kc, const float* vc, half_t* ko, half_t* vo,
+                                                   size_t n8) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const float4v* k4 = reinterpret_cast<const float4v*>(kc) + 2 * i;
+    const float4v* v4 = reinterpret_cast<const float4v*>(vc) + 2 * i;
+    const float4v k0 = k4[0], k1 = k4[1], v0 = v4[0], v1 = v4[1];
+    reinterpret_cast<half8*>(ko)[i] = half8{(half_t)k0[0], (half_t)k0[1], (half_t)k0[2], (half_t)k0[3],
+                                            (half_t)k1[0], (half_t)k1[1], (half_t)k1[2], (half_t)k1[3]};
+    reinterpret_cast<half8*>(vo)[i] = half8{(half_t)v0[0], (half_t)v0[1], (half_t)v0[2], (half_t)v0[3],
+                                            (half_t)v1[0], (half_t)v1[1], (half_t)v1[2], (half_t)v1[3]};
 }
 
 extern "C" size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos) {
@@ -885,15 +938,18 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     }
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
     const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
-    // hd 256 with f16 caches and f16 q: the 32-column kernel; other modes the 16-column one
-    const bool w32 = use_w32(cfg);
+    // hd 256: the 32-column kernel (f32 caches only with the workspace for their f16 copy);
+    // hd 512 and f32 caches without a workspace: the 16-column one
+    const PrefillSplit sp = prefill_split(cfg, S, start_pos);
+    const bool ws_ok = ws && (uintptr_t)ws % 256 == 0;
+    const bool w32 = use_w32(cfg) && (!kv32 || (ws_ok && ws_bytes >= sp.kv16_bytes));
     prefill_fn fn = nullptr;
     if (w32) {
         switch (G) {
-            case 1: fn = pick_w32<1>(out32); break;
-            case 2: fn = pick_w32<2>(out32); break;
-            case 4: fn = pick_w32<4>(out32); break;
-            case 8: fn = pick_w32<8>(out32); break;
+            case 1: fn = pick_w32<1>(out32, hilo); break;
+            case 2: fn = pick_w32<2>(out32, hilo); break;
+            case 4: fn = pick_w32<4>(out32, hilo); break;
+            case 8: fn = pick_w32<8>(out32, hilo); break;
         }
     } else {
         fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
@@ -925,29 +981,46 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.scale_log2 = cfg->scale * kLog2e;
     a.eps = cfg->eps;
     a.out_q = cfg->out_q;
-    // key split when a large enough workspace is given (without one the call runs unsplit)
-    const PrefillSplit sp = prefill_split(cfg, S, start_pos);
     a.split_tiles = 0;
     a.max_pieces = 1;
     a.pieces_per_head = 0;
     a.part_o = nullptr;
     a.part_ml = nullptr;
     a.q16 = nullptr;
-    if (sp.split_tiles > 0 && ws && ws_bytes >= sp.total && (uintptr_t)ws % 256 == 0) {
+    a.q16lo = nullptr;
+    a.kv_row0 = 0;
+    char* wsp = (char*)ws;  // workspace layout: [K16][V16][partials][(m, l)][q16][q16 low]
+    if (w32 && kv32) {
+        const size_t half_bytes = sp.kv16_bytes / 2, skip = (size_t)sp.kv_row0 * cfg->n_kv_heads * 256;
+        const size_t n8 = (size_t)sp.kv_rows * cfg->n_kv_heads * 256 / 8;
+        hipLaunchKernelGGL(kv16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                           reinterpret_cast<const float*>(k_cache) + skip, reinterpret_cast<const float*>(v_cache) + skip,
+                           (half_t*)wsp, (half_t*)(wsp + half_bytes), n8);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return hip_error(e0, "prefill cache conversion launch");
+        a.kc = wsp;
+        a.vc = wsp + half_bytes;
+        a.kv_row0 = sp.kv_row0;
+        wsp += sp.kv16_bytes;
+    }
+    // key split when a large enough workspace is given (without one the call runs unsplit)
+    if (w32 && sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total) {
         a.split_tiles = sp.split_tiles;
         a.max_pieces = sp.max_pieces;
         a.pieces_per_head = sp.total_pieces;
-        a.part_o = (half_t*)ws;
-        a.part_ml = (float2*)((char*)ws + sp.o_bytes);
+        a.part_o = (half_t*)wsp;
+        a.part_ml = (float2*)(wsp + sp.o_bytes);
         // the pieces of a query block share its q: prepare it once (qprep_b's kernel, whose
         // f16 values are those of the fused prologue), then every piece loads f16 q
-        half_t* q16 = (half_t*)((char*)ws + sp.o_bytes + sp.ml_bytes);
+        half_t* q16 = (half_t*)(wsp + sp.o_bytes + sp.ml_bytes);
+        half_t* q16lo = hilo ? (half_t*)(wsp + sp.o_bytes + sp.ml_bytes + sp.q16_bytes) : nullptr;
         const int rows = S * (int)cfg->n_q_heads;
         hipLaunchKernelGGL(qprep_kernel<256>, dim3((rows + 15) / 16), dim3(64), 0, (hipStream_t)stream, q, q_gain,
-                           rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads, cfg->eps);
+                           rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads, cfg->eps, q16lo);
         hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
         a.q16 = q16;
+        a.q16lo = q16lo;
     }
     a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0;
     const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
@@ -995,7 +1068,7 @@ extern "C" int g4a_qprep(const g4a_cfg* cfg, int S, const float* q, const float*
     const int blocks = (int)((rows + 15) / 16);
     auto fn = HD == 256 ? qprep_kernel<256> : qprep_kernel<512>;
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64), 0, (hipStream_t)stream, q, q_gain, rope_cos, rope_sin,
-                       (half_t*)q16, (int)rows, (int)cfg->n_q_heads, cfg->eps);
+                       (half_t*)q16, (int)rows, (int)cfg->n_q_heads, cfg->eps, (half_t*)nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "qprep launch");
     return G4A_OK;

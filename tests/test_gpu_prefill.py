@@ -242,6 +242,35 @@ def test_f32_cache_and_mirror():
     contract_close(out16.float().cpu().numpy().reshape(S, nH, hd), z["expected_q16_w16"], "attn_gemm mirror")
 
 
+@pytest.mark.parametrize("S,start,window", [(1024, 0, 0), (1024, 0, 512), (700, 900, 512), (300, 50, 0)])
+def test_f32_caches_on_the_32_column_kernel(S, start, window):
+    """With a workspace, f32 caches run the 32-column kernel on an f16 copy of the attended
+    rows (from max(0, start+1-W)): the copy rounds as the 16-column kernel's staging does, so
+    the output equals the f16-cache call's bit for bit, in both q modes. Without a workspace
+    (the 16-column kernel on the f32 rows) the output meets the contract against the oracle
+    on the f16-rounded caches."""
+    hd, nH, kvH, T = 256, 8, 2, start + S
+    rng = np.random.default_rng(S + start + window)
+    q = rng.standard_normal((S, nH, hd)).astype(np.float32)
+    qg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    k32 = rng.standard_normal((T + 2, kvH, hd)).astype(np.float32)  # not f16-representable
+    v32 = rng.standard_normal((T + 2, kvH, hd)).astype(np.float32)
+    k16, v16 = k32.astype(np.float16), v32.astype(np.float16)
+    cos, sin = O.rope_tables(np.arange(start, T), hd, 1e4 if window else 1e6)
+    cfg = sa.AttnConfig(nH, kvH, hd, window)
+    kw = dict(q_gain=qg, rope_cos=cos, rope_sin=sin)
+    for hilo in (False, True):
+        a = run(q, k32, v32, start, cfg, out_dtype=torch.float32, q_hilo=hilo, **kw)
+        b = run(q, k16, v16, start, cfg, out_dtype=torch.float32, q_hilo=hilo, **kw)
+        assert np.array_equal(a, b), f"f32 vs f16 caches, hilo={hilo}: max |d| {np.abs(a - b).max()}"
+    q16 = kernel_q16(q, cfg, qg, cos, sin).astype(np.float32)
+    ref = O.prefill_attention(q16, k16.astype(np.float32), v16.astype(np.float32), start, kvH, window=window)
+    contract_close(run(q, k32, v32, start, cfg, out_dtype=torch.float32, split=False, **kw),
+                   ref, f"f32 caches unsplit S={S} start={start} W={window}")
+    contract_close(run(q, k32, v32, start, cfg, out_dtype=torch.float32, **kw), ref,
+                   f"f32 caches S={S} start={start} W={window}")
+
+
 @pytest.mark.parametrize("S", [512, 1024, 2048])
 @pytest.mark.parametrize("window", [0, 512])
 def test_key_split_matches_unsplit(S, window):
