@@ -297,18 +297,21 @@ __device__ __forceinline__ int xcd_run_index() {
     return x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
 }
 
-template <int G, typename OUTT, bool HILO>
-__global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
-    constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
-    constexpr int QMF = HILO ? 2 : 1;  // score MFMAs per K operand (q high, then low parts)
-    constexpr int ROWB = HD * 2;      // bytes per LDS tile row
-    constexpr int TILEB = KT * ROWB;  // one K or V tile
-    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n32 = lane & 31, h = lane >> 5;
-    int kh = blockIdx.y;
+// ---- the workgroup's query block (longest causal rows first) and, with a key split, its
+// piece: the work lists of the 32-column kernels (query blocks of BQ positions, KT-key tiles).
+// The split grid is 1-D: the work list (kv head, block from the longest, piece) is cut into
+// 8 contiguous runs, one per XCD (the dispatcher deals workgroup L to XCD L % 8), so the
+// pieces of a block share one L2 for the block's q rows and each kv head's K/V is read by as
+// few XCDs as the split allows: every kernel starts with cold L2s, and the first tiles of all
+// workgroups arrive together. Within its kv head, piece i is found by counting through the
+// blocks from the longest, each holding ceil(tiles / split_tiles) pieces: the lanes take 64
+// blocks at a time (one division each, in parallel) and a prefix sum over the wave finds the
+// block holding piece i; a scalar loop over the blocks would cost microseconds of issue slots.
+struct PrefillUnit {
+    int kh, qb, piece, n_pieces;
+};
+template <int BQ, int KT>
+__device__ __forceinline__ PrefillUnit prefill_unit(const PrefillArgs& a, int lane) {
     const int T_total = a.start_pos + a.S;
     // key tiles of query block b: [lo(b), hi(b)) in tiles of KT keys
     auto block_tiles = [&](int b) {
@@ -316,17 +319,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         const int hi = min(b0 + BQ, T_total), lo = a.window > 0 ? max(0, b0 + 1 - a.window) : 0;
         return (hi - lo + KT - 1) / KT;
     };
-    // ---- this workgroup's query block (longest causal rows first) and, with a key split,
-    // its piece. The split grid is 1-D: the work list (kv head, block from the longest,
-    // piece) is cut into 8 contiguous runs, one per XCD (the dispatcher deals workgroup
-    // L to XCD L % 8), so the pieces of a block share one L2 for the block's q rows and
-    // each kv head's K/V is read by as few XCDs as the split allows: every kernel starts
-    // with cold L2s, and the first tiles of all workgroups arrive together. Within its
-    // kv head, piece i is found by counting through the blocks from the longest, each
-    // holding ceil(tiles / split_tiles) pieces: the lanes take 64 blocks at a time (one
-    // division each, in parallel) and a prefix sum over the wave finds the block holding
-    // piece i; a scalar loop over the blocks would cost microseconds of issue slots.
-    int qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
+    int kh = blockIdx.y, qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
     if (a.xcd_runs) {
         // sliding window, unsplit: a 1-D grid over (kv head, query block) in contiguous runs
         // per XCD, so neighbouring blocks -- which share most of their window's K/V tiles --
@@ -355,6 +348,23 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
             base += __builtin_amdgcn_readlane(incl, 63);
         }
     }
+    return PrefillUnit{kh, qb, piece, n_pieces};
+}
+
+template <int G, typename OUTT, bool HILO>
+__global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
+    constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
+    constexpr int QMF = HILO ? 2 : 1;  // score MFMAs per K operand (q high, then low parts)
+    constexpr int ROWB = HD * 2;      // bytes per LDS tile row
+    constexpr int TILEB = KT * ROWB;  // one K or V tile
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n32 = lane & 31, h = lane >> 5;
+    const int T_total = a.start_pos + a.S;
+    const PrefillUnit wu = prefill_unit<BQ, KT>(a, lane);
+    const int kh = wu.kh, qb = wu.qb, piece = wu.piece, n_pieces = wu.n_pieces;
 
     // ---- key range of the workgroup [wg_lo, kv_hi) in tiles; with a key split this
     // workgroup takes tiles [t0, t1) of its query block
@@ -725,18 +735,271 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- hd 512
+// prefill_kernel_w32d: hd 512 (the global layers of Gemma 4 E2B) on the 32-column scheme.
+// 32 columns x 512 dims would take 256 accumulator and 128 q registers a wave, so the dims
+// are split over a pair of waves: wave d of pair p holds the 32 columns 32p .. 32p + 31 (64
+// per workgroup: G heads x 64/G positions) over dims 256d .. 256d + 255. Each wave forms the
+// partial scores of its dims (S_d^T = K_d . Q_d^T, 16 MFMAs a 32-key tile), the pair adds
+// them through LDS (both waves then hold S_0 + S_1 and run the same softmax), and each wave
+// accumulates O^T for its own dims -- per wave the registers and the LDS bytes per MFMA of
+// the hd-256 kernel. Tiles of 32 keys (1 KiB rows: K and V 32 KiB each, double buffered:
+// 128 KiB of LDS, plus 16 KiB for the score exchange) are DMA'd as in prefill_kernel_w32.
+// q comes prepared in f16 (qprep_kernel; the RoPE pairs (i, i + 256) would span both waves).
+template <int G, typename OUTT, bool HILO>
+__global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
+    constexpr int HD = 512, KT = 32, NCOL = 64, BQ = NCOL / G;
+    constexpr int QMF = HILO ? 2 : 1;
+    constexpr int ROWB = HD * 2;      // 1 KiB rows
+    constexpr int TILEB = KT * ROWB;  // one K or V tile: 32 KiB
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB + 4 * 4096];  // [buffer][K, V], exchange
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pr = wave >> 1, dh = wave & 1;  // pair (columns), dim half
+    const int n32 = lane & 31, h = lane >> 5;
+    const int T_total = a.start_pos + a.S;
+    const PrefillUnit wu = prefill_unit<BQ, KT>(a, lane);
+    const int kh = wu.kh, qb = wu.qb, piece = wu.piece, n_pieces = wu.n_pieces;
+
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, T_total);
+    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
+    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
+    int t0 = 0, t1 = n_tiles;
+    if (a.split_tiles > 0) {
+        t0 = piece * a.split_tiles;
+        t1 = min(t0 + a.split_tiles, n_tiles);
+    }
+
+    // ---- this lane's query column (head hh, position offset pl) and 8-dim half h
+    const int c = 32 * pr + n32;
+    const int hh = c % G, pl = c / G;
+    const int s_raw = qb * BQ + pl;
+    const bool col_ok = s_raw < a.S;
+    const int s_idx = col_ok ? s_raw : a.S - 1;
+    const int pos = a.start_pos + s_idx;
+
+    // K/V rows through buffer resources (rows >= kv_hi read as zeros); row r of a tile holds
+    // chunk x at place x ^ (r % 32) (K) or x ^ vswz(r) (V): wave w moves rows 8w .. 8w + 7
+    const int rowg = a.n_kv_heads * HD * 2;
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const half_t*>(a.kc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const half_t*>(a.vc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
+    auto issue = [&](int t, int buf) {
+        const int kb = wg_lo + t * KT - a.kv_row0;
+        char* kdst = lds + buf * 2 * TILEB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * wave + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kdst + r * ROWB), 16,
+                                                     (kb + r) * rowg + 16 * (lane ^ (r & 31)), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(kdst + TILEB + r * ROWB),
+                                                     16, (kb + r) * rowg + 16 * (lane ^ vswz(r)), 0, 0, 0);
+        }
+    };
+
+    // ---- q: lane (column c, half h) holds dims 256 dh + 16s + 8h .. +7 (s < 16), the B
+    // operand layout; the loads go out before the first tile's
+    half8 qf[16], ql[HILO ? 16 : 1];
+    {
+        const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
+        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * ROWB + 512 * dh + 16 * h;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qf[s] = bload_h8(rq, qo + 32 * s);
+        if constexpr (HILO) {
+            const rsrc_t rql = make_rsrc(a.q16lo, (uint32_t)a.S * a.n_q_heads * HD * 2);
+#pragma unroll
+            for (int s = 0; s < 16; ++s) ql[s] = bload_h8(rql, qo + 32 * s);
+        }
+        if (t0 < t1) issue(t0, t0 & 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (!col_ok) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) qf[s] = ql[HILO ? s : 0] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(qf[s]));
+        if constexpr (HILO) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) asm volatile("" : "+a"(ql[s]));
+        }
+    }
+
+    // ---- key ranges: this pair [w_lo, wp1], this column [col_lo, pos]
+    const int wp0 = p0 + (32 * pr) / G;
+    const int wp1 = min(p0 + (32 * pr + 31) / G, T_total - 1);
+    const int w_lo = a.window > 0 ? max(0, wp0 + 1 - a.window) : 0;
+    const int col_lo = a.window > 0 ? pos + 1 - a.window : 0;
+
+    // transposed V reads, as prefill_kernel_w32's, in this wave's dim half
+    const int m16 = lane & 15, half16 = (lane >> 4) & 1;
+    const int vr0 = 4 * h + (m16 >> 2);
+    const int vc0 = 2 * half16 + ((m16 & 3) >> 1);
+    const int vb0 = 8 * (m16 & 1);
+    const int vsw = vswz(vr0);
+    float* xme = reinterpret_cast<float*>(lds + 4 * TILEB) + wave * 1024;  // [r/4][lane][4]
+    const float* xother = reinterpret_cast<const float*>(lds + 4 * TILEB) + (wave ^ 1) * 1024;
+
+    float16v oacc[8];  // O^T[256 dh + 32dt + 8(r/4) + 4h + r%4][column]
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[dt] = float16v{};
+    float m_use = kNegInf, l_run = 0.0f;
+    bool started = false;
+    for (int t = t0; t < t1; ++t) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's rows of tile t are in LDS
+        __syncthreads();                                    // all rows; tile t-1 and the exchange consumed
+        if (t + 1 < t1) issue(t + 1, (t + 1) & 1);
+        const int kb = wg_lo + t * KT;
+        const bool live = !(kb > wp1 || kb + KT - 1 < w_lo);  // pair-uniform: a key of the tile for the pair
+        const char* K = lds + (t & 1) * 2 * TILEB;
+        const char* V = K + TILEB;
+        float16v sacc = float16v{};
+        if (live) {
+            // S_dh^T = K_dh . Q_dh^T over 16 k-steps of 16 dims
+            const char* krow = K + n32 * ROWB;
+#pragma unroll
+            for (int s0 = 0; s0 < 16; s0 += 4) {
+                half8 kv[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    kv[s] = *reinterpret_cast<const half8*>(krow + 16 * ((32 * dh + 2 * (s0 + s) + h) ^ n32));
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    sacc = mfma32(kv[s], qf[s0 + s], sacc);
+                    if constexpr (HILO) sacc = mfma32(kv[s], ql[s0 + s], sacc);
+                }
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 14; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, QMF, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * QMF, 0);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *reinterpret_cast<float4v*>(xme + (r4 * 64 + lane) * 4) =
+                    float4v{sacc[4 * r4], sacc[4 * r4 + 1], sacc[4 * r4 + 2], sacc[4 * r4 + 3]};
+        }
+        __syncthreads();  // the partner's partial scores
+        if (!live) continue;
+        // S = S_0 + S_1 in both waves of the pair (the same sums in the same order)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const float4v o = *reinterpret_cast<const float4v*>(xother + (r4 * 64 + lane) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sacc[4 * r4 + i] = dh == 0 ? sacc[4 * r4 + i] + o[i] : o[i] + sacc[4 * r4 + i];
+        }
+        // scores of this lane: key kb + 4h + 8(r/4) + r%4 of its column, log2 domain
+        const bool masked = (kb + KT - 1 > wp0) || (a.window > 0 && kb < wp1 + 1 - a.window);
+        if (masked) {
+            const int rel_hi = pos - (kb + 4 * h), rel_lo = col_lo - (kb + 4 * h);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int o = 8 * (r >> 2) + (r & 3);
+                sacc[r] = (o <= rel_hi && o >= rel_lo) ? sacc[r] : kNegInf;
+            }
+        }
+        float mloc = kNegInf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[r]);
+        mloc = max32(mloc) * a.scale_log2;
+        const bool bump = mloc > m_use + 8.0f;  // the running max moves only past 2^8
+        if (__any(bump)) {
+            const float m_new = bump ? mloc : m_use;
+            const float corr = m_use == kNegInf ? 0.0f : fexp2(m_use - m_new);
+            l_run *= corr;
+            if (started) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) oacc[dt] *= corr;
+            }
+            m_use = m_new;
+        }
+        started = true;
+        const float msub = m_use == kNegInf ? 0.0f : m_use;
+        half8 pb[2];
+        float ps = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float pv = fexp2(__builtin_fmaf(sacc[8 * u + i], a.scale_log2, -msub));
+                ps += pv;
+                pb[u][i] = (half_t)pv;
+            }
+        l_run += ps;
+
+        // O^T_dh += V_dh^T . P^T over two 16-key steps
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int ra = 16 * u + vr0, rb = ra + 8;
+#pragma unroll
+            for (int d0 = 0; d0 < 8; d0 += 4) {
+                half8 av[4];
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    const int ch = 32 * dh + 4 * (d0 + dd) + vc0;
+                    const half4 lo = lds_tr16(reinterpret_cast<const half_t*>(V + ra * ROWB + 16 * (ch ^ vsw) + vb0));
+                    const half4 hi = lds_tr16(reinterpret_cast<const half_t*>(V + rb * ROWB + 16 * (ch ^ vsw) + vb0));
+                    av[dd] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) oacc[d0 + dd] = mfma32(av[dd], pb[u], oacc[d0 + dd]);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 14; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+
+    // ---- epilogue: this wave's 256 dims of its 32 columns
+    const float l_tot = add32(l_run);
+    if (n_pieces > 1) {  // a piece of a split query block: O / l in f16, (m, l) from wave dh 0
+        const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
+        const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * 256) + 4 * lane;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
+                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
+                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+        if (h == 0 && dh == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
+        return;
+    }
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (col_ok) {
+        OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD + 256 * dh;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(orow + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
+            }
+    }
+}
+
 // Merge of the pieces of split query blocks (the decode merge identity per column): with
 // each piece holding o_p = O_p / l_p, out = sum_p o_p l_p 2^(m_p - M) / sum_p l_p 2^(m_p - M),
-// M = max_p m_p, then srq and the output type. One workgroup per (query block, 32-column
-// wave block, kv head), laid out like the partials: thread (k, lane) owns the lane's
-// 4-dim runs k, k+4, .. (k < 4) of all 32 dims tiles, so every load instruction reads a
-// contiguous 512-byte run. At most 8 pieces.
-template <typename OUTT>
+// M = max_p m_p, then srq and the output type. One workgroup per (query block, wave block of
+// 32 columns x 256 dims, kv head), laid out like the partials: thread (k, lane) owns the
+// lane's 4-dim runs k, k+4, .. (k < 4) of all 32 dims tiles, so every load instruction reads
+// a contiguous 512-byte run. At most 8 pieces. HD 256: wave block w = columns 32w..; HD 512
+// (prefill_kernel_w32d): columns 32(w/2).., dims 256(w%2)..
+template <typename OUTT, int HD>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-    constexpr int HD = 256, KT = 64, NCOL = 128, MAXP = 8;
+    constexpr int KT = HD == 256 ? 64 : 32, NCOL = HD == 256 ? 128 : 64, MAXP = 8;
     const int qb = blockIdx.x, w = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, k0 = tid >> 6;
-    const int c = 32 * w + (lane & 31), h = lane >> 5;
+    const int c = (HD == 256 ? 32 * w : 32 * (w >> 1)) + (lane & 31), h = lane >> 5;
+    const int dbase = HD == 256 ? 0 : 256 * (w & 1);
     const int G = a.n_q_heads / a.n_kv_heads, BQ = NCOL / G;
     const int p0 = a.start_pos + qb * BQ;
     const int kv_hi = min(p0 + BQ, a.start_pos + a.S);
@@ -749,7 +1012,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     // buffer ranges end at the block's last piece: the loads of absent pieces read zeros,
     // so all of them issue at once with no branch
     const rsrc_t rml = make_rsrc(a.part_ml + blk0 * NCOL, (uint32_t)n_pieces * NCOL * 8);
-    const rsrc_t ro = make_rsrc(a.part_o + blk0 * (NCOL * HD) + (size_t)w * (32 * HD), (uint32_t)n_pieces * NCOL * HD * 2);
+    const rsrc_t ro = make_rsrc(a.part_o + blk0 * (NCOL * HD) + (size_t)w * (32 * 256), (uint32_t)n_pieces * NCOL * HD * 2);
     float2 ml[MAXP];
     half4 ov[MAXP][8];
 #pragma unroll
@@ -781,7 +1044,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     }
     if (s_idx >= a.S) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + c % G) * HD;
+    OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + c % G) * HD + dbase;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int k = k0 + 4 * i, d = 32 * (k >> 2) + 8 * (k & 3) + 4 * h;
@@ -789,10 +1052,15 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     }
 }
 
-template <int G>
+template <int HD, int G>
 static void (*pick_w32(bool out32, bool hilo))(PrefillArgs) {
-    if (hilo) return out32 ? prefill_kernel_w32<G, float, true> : prefill_kernel_w32<G, half_t, true>;
-    return out32 ? prefill_kernel_w32<G, float, false> : prefill_kernel_w32<G, half_t, false>;
+    if constexpr (HD == 256) {
+        if (hilo) return out32 ? prefill_kernel_w32<G, float, true> : prefill_kernel_w32<G, half_t, true>;
+        return out32 ? prefill_kernel_w32<G, float, false> : prefill_kernel_w32<G, half_t, false>;
+    } else {
+        if (hilo) return out32 ? prefill_kernel_w32d<G, float, true> : prefill_kernel_w32d<G, half_t, true>;
+        return out32 ? prefill_kernel_w32d<G, float, false> : prefill_kernel_w32d<G, half_t, false>;
+    }
 }
 
 typedef void (*prefill_fn)(PrefillArgs);
@@ -832,30 +1100,38 @@ using namespace g4a;
 struct PrefillSplit {
     int split_tiles, max_pieces, n_qblocks, total_pieces;
     int kv_row0, kv_rows;  // f32 caches: the attended rows copied to f16
-    size_t kv16_bytes, o_bytes, ml_bytes, q16_bytes, q16lo_bytes, total;
+    // workspace layout [K16][V16][q16][q16 low][partials][(m, l)]; base: the bytes the
+    // unsplit call needs, total: with the split
+    size_t kv16_bytes, q16_bytes, q16lo_bytes, o_bytes, ml_bytes, base, total;
 };
-// hd 256 runs the 32-column kernel in every mode. f32 caches go through an f16 copy of the
-// attended rows in the workspace (the 16-column kernel rounds them to f16 as it stages
-// them, so the operands are the same values); G4A_Q_HILO adds q's f16 low parts as a second
-// score operand. Without the workspace an f32-cache call runs the 16-column kernel.
-static bool use_w32(const g4a_cfg* cfg) { return cfg->head_dim == 256; }
+// Every mode runs the 32-column kernels (hd 256: prefill_kernel_w32, hd 512:
+// prefill_kernel_w32d) when the workspace holds what they need: f32 caches an f16 copy of
+// the attended rows (the 16-column kernel rounds them to f16 as it stages them, so the
+// operands are the same values); hd 512 its q in f16 (qprep_kernel; with G4A_Q_HILO the low
+// parts too). hd 256 runs unsplit without a workspace (its q prologue fused in); the rest
+// falls back to the 16-column kernel.
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
-    PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    if (!use_w32(cfg) || S <= 0 || cfg->n_kv_heads == 0) return p;
+    PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const int HD = (int)cfg->head_dim;
+    if ((HD != 256 && HD != 512) || S <= 0 || cfg->n_kv_heads == 0) return p;
     const int G = (int)(cfg->n_q_heads / cfg->n_kv_heads);
-    if (G < 1 || 128 % G) return p;
-    const int BQ = 128 / G, KT = 64, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
+    const int NCOL = HD == 256 ? 128 : 64, KT = HD == 256 ? 64 : 32;
+    if (G < 1 || NCOL % G) return p;
+    const int BQ = NCOL / G, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
+    const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
     if (cfg->flags & G4A_KV_F32) {
         p.kv_row0 = W > 0 && start_pos + 1 - W > 0 ? start_pos + 1 - W : 0;
         p.kv_rows = start_pos + S - p.kv_row0;
-        p.kv16_bytes = 2 * align256((size_t)p.kv_rows * kvH * 256 * sizeof(half_t));
+        p.kv16_bytes = 2 * align256((size_t)p.kv_rows * kvH * HD * sizeof(half_t));
     }
-    p.total = p.kv16_bytes;
+    const size_t q16 = align256((size_t)S * cfg->n_q_heads * HD * sizeof(half_t));
+    p.base = p.kv16_bytes + (HD == 512 ? q16 * (hilo ? 2 : 1) : 0);
+    p.total = p.base;
     p.n_qblocks = (S + BQ - 1) / BQ;
     if ((long)p.n_qblocks * kvH >= 512) return p;
     // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
-    // preparation and merge only while the unsplit grid leaves most CUs idle (S 2048,
+    // preparation and merge only while the unsplit grid leaves most CUs idle (hd 256, S 2048,
     // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27)
     if (W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
     int max_tiles = 0;
@@ -881,12 +1157,12 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
         const int nt = (hi - lo + KT - 1) / KT;
         p.total_pieces += nt > st ? (nt + st - 1) / st : 1;
     }
-    const size_t slots = (size_t)kvH * p.n_qblocks * pieces * 128;
-    p.o_bytes = slots * 256 * sizeof(half_t);
+    const size_t slots = (size_t)kvH * p.n_qblocks * pieces * NCOL;
+    p.q16_bytes = q16;
+    p.q16lo_bytes = hilo ? q16 : 0;
+    p.o_bytes = slots * HD * sizeof(half_t);
     p.ml_bytes = align256(slots * sizeof(float2));
-    p.q16_bytes = align256((size_t)S * cfg->n_q_heads * 256 * sizeof(half_t));
-    p.q16lo_bytes = (cfg->flags & G4A_Q_HILO) ? p.q16_bytes : 0;
-    p.total = p.kv16_bytes + p.o_bytes + p.ml_bytes + p.q16_bytes + p.q16lo_bytes;
+    p.total = p.kv16_bytes + p.q16_bytes + p.q16lo_bytes + p.o_bytes + p.ml_bytes;
     return p;
 }
 
@@ -906,7 +1182,7 @@ __global__ __launch_bounds__(256) void kv16_kernel(const float* kc, const float*
 
 extern "C" size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos) {
     if (!cfg) return 0;
-    return prefill_split(cfg, S, start_pos).total;
+    return prefill_split(cfg, S, start_pos).total;  // the split's when the call splits
 }
 
 extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float* q,
@@ -938,18 +1214,20 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     }
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
     const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
-    // hd 256: the 32-column kernel (f32 caches only with the workspace for their f16 copy);
-    // hd 512 and f32 caches without a workspace: the 16-column one
+    // the 32-column kernels when the workspace holds what they need (prefill_split), else
+    // the 16-column one
     const PrefillSplit sp = prefill_split(cfg, S, start_pos);
     const bool ws_ok = ws && (uintptr_t)ws % 256 == 0;
-    const bool w32 = use_w32(cfg) && (!kv32 || (ws_ok && ws_bytes >= sp.kv16_bytes));
+    const bool need_ws = kv32 || HD == 512;
+    const bool w32 = !need_ws || (ws_ok && ws_bytes >= sp.base);
+    const bool split = w32 && sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total;
     prefill_fn fn = nullptr;
     if (w32) {
         switch (G) {
-            case 1: fn = pick_w32<1>(out32, hilo); break;
-            case 2: fn = pick_w32<2>(out32, hilo); break;
-            case 4: fn = pick_w32<4>(out32, hilo); break;
-            case 8: fn = pick_w32<8>(out32, hilo); break;
+            case 1: fn = HD == 256 ? pick_w32<256, 1>(out32, hilo) : pick_w32<512, 1>(out32, hilo); break;
+            case 2: fn = HD == 256 ? pick_w32<256, 2>(out32, hilo) : pick_w32<512, 2>(out32, hilo); break;
+            case 4: fn = HD == 256 ? pick_w32<256, 4>(out32, hilo) : pick_w32<512, 4>(out32, hilo); break;
+            case 8: fn = HD == 256 ? pick_w32<256, 8>(out32, hilo) : pick_w32<512, 8>(out32, hilo); break;
         }
     } else {
         fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
@@ -971,7 +1249,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
-    const int BQ = (w32 ? 128 : 64) / G;
+    const int BQ = (w32 ? (HD == 256 ? 128 : 64) : 64) / G;
     a.n_qblocks = (S + BQ - 1) / BQ;
     if (w32 && ((int64_t)(start_pos + S) * cfg->n_kv_heads * HD * 2 > 0x7fffffff ||
                 (int64_t)S * cfg->n_q_heads * HD * 4 > 0x7fffffff)) {
@@ -989,10 +1267,10 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.q16 = nullptr;
     a.q16lo = nullptr;
     a.kv_row0 = 0;
-    char* wsp = (char*)ws;  // workspace layout: [K16][V16][partials][(m, l)][q16][q16 low]
+    char* wsp = (char*)ws;  // workspace layout: [K16][V16][q16][q16 low][partials][(m, l)]
     if (w32 && kv32) {
-        const size_t half_bytes = sp.kv16_bytes / 2, skip = (size_t)sp.kv_row0 * cfg->n_kv_heads * 256;
-        const size_t n8 = (size_t)sp.kv_rows * cfg->n_kv_heads * 256 / 8;
+        const size_t half_bytes = sp.kv16_bytes / 2, skip = (size_t)sp.kv_row0 * cfg->n_kv_heads * HD;
+        const size_t n8 = (size_t)sp.kv_rows * cfg->n_kv_heads * HD / 8;
         hipLaunchKernelGGL(kv16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                            reinterpret_cast<const float*>(k_cache) + skip, reinterpret_cast<const float*>(v_cache) + skip,
                            (half_t*)wsp, (half_t*)(wsp + half_bytes), n8);
@@ -1001,26 +1279,31 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         a.kc = wsp;
         a.vc = wsp + half_bytes;
         a.kv_row0 = sp.kv_row0;
-        wsp += sp.kv16_bytes;
     }
-    // key split when a large enough workspace is given (without one the call runs unsplit)
-    if (w32 && sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total) {
+    wsp += sp.kv16_bytes;
+    // q in f16 for hd 512 always, for hd 256 when the pieces of a split query block share it
+    // (qprep_b's kernel, whose f16 values are those of the hd-256 fused prologue)
+    if (w32 && (HD == 512 || split)) {
+        const size_t q16b = align256((size_t)S * cfg->n_q_heads * HD * sizeof(half_t));
+        half_t* q16 = (half_t*)wsp;
+        half_t* q16lo = hilo ? (half_t*)(wsp + q16b) : nullptr;
+        const int rows = S * (int)cfg->n_q_heads;
+        hipLaunchKernelGGL(HD == 256 ? qprep_kernel<256> : qprep_kernel<512>, dim3((rows + 15) / 16), dim3(64), 0,
+                           (hipStream_t)stream, q, q_gain, rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads,
+                           cfg->eps, q16lo);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
+        a.q16 = q16;
+        a.q16lo = q16lo;
+        wsp += q16b * (hilo ? 2 : 1);
+    }
+    // key split (short prompts): pieces of long causal rows, merged by a second kernel
+    if (split) {
         a.split_tiles = sp.split_tiles;
         a.max_pieces = sp.max_pieces;
         a.pieces_per_head = sp.total_pieces;
         a.part_o = (half_t*)wsp;
         a.part_ml = (float2*)(wsp + sp.o_bytes);
-        // the pieces of a query block share its q: prepare it once (qprep_b's kernel, whose
-        // f16 values are those of the fused prologue), then every piece loads f16 q
-        half_t* q16 = (half_t*)(wsp + sp.o_bytes + sp.ml_bytes);
-        half_t* q16lo = hilo ? (half_t*)(wsp + sp.o_bytes + sp.ml_bytes + sp.q16_bytes) : nullptr;
-        const int rows = S * (int)cfg->n_q_heads;
-        hipLaunchKernelGGL(qprep_kernel<256>, dim3((rows + 15) / 16), dim3(64), 0, (hipStream_t)stream, q, q_gain,
-                           rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads, cfg->eps, q16lo);
-        hipError_t e0 = hipGetLastError();
-        if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
-        a.q16 = q16;
-        a.q16lo = q16lo;
     }
     a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0;
     const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
@@ -1030,7 +1313,8 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
     if (a.split_tiles > 0) {
-        auto mf = out32 ? prefill_merge_kernel<float> : prefill_merge_kernel<half_t>;
+        auto mf = HD == 256 ? (out32 ? prefill_merge_kernel<float, 256> : prefill_merge_kernel<half_t, 256>)
+                            : (out32 ? prefill_merge_kernel<float, 512> : prefill_merge_kernel<half_t, 512>);
         hipLaunchKernelGGL(mf, dim3(a.n_qblocks, 4, cfg->n_kv_heads), dim3(256), 0, (hipStream_t)stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return hip_error(e, "prefill merge launch");
