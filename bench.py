@@ -150,21 +150,34 @@ def config1_case(sa, steps, warmup, gen, n_caches=256):
     return ms, 2 * T * kvh * hd * 4
 
 
-def prefill_case(sa, S, window, theta, steps, warmup, gen):
-    q = torch.randn(S, NH, HD, device="cuda", generator=gen)
-    qg = 1 + 0.1 * torch.randn(HD, device="cuda", generator=gen)
-    cos, sin = sa.rope_tables(np.arange(S), HD, theta)
-    kc, vc = make_caches(sa, 1, S, theta, gen)[0]
-    cfg = sa.AttnConfig(NH, KVH, HD, window)
-    out = torch.empty(S, NH, HD, device="cuda", dtype=torch.float16)
+def prefill_case(sa, S, window, theta, steps, warmup, gen, nH=NH, kvH=KVH, hd=HD, kv32=False, hilo=False):
+    """One layer's prefill attention over S tokens (config 3 by default). The other modes:
+    kv32 f32 caches (the reference's own cache type), hilo the f32-q attn_prefill form, hd
+    512 with nH 8 / kvH 1 the global layers of Gemma 4 E2B; their caches hold N(0,1) rows."""
+    q = torch.randn(S, nH, hd, device="cuda", generator=gen)
+    qg = 1 + 0.1 * torch.randn(hd, device="cuda", generator=gen)
+    cos, sin = sa.rope_tables(np.arange(S), hd, theta)
+    if (nH, kvH, hd, kv32) == (NH, KVH, HD, False):
+        kc, vc = make_caches(sa, 1, S, theta, gen)[0]
+    else:
+        kc = torch.randn(S, kvH, hd, device="cuda", generator=gen)
+        vc = torch.randn(S, kvH, hd, device="cuda", generator=gen)
+        if not kv32:
+            kc, vc = kc.half(), vc.half()
+    cfg = sa.AttnConfig(nH, kvH, hd, window)
+    out = torch.empty(S, nH, hd, device="cuda", dtype=torch.float16)
     ws = sa.DecodeWorkspace("cuda")
     fn = lambda: sa.prefill(q, kc, vc, 0, cfg, q_gain=qg, rope_cos=cos, rope_sin=sin, out=out,  # noqa: E731
-                            workspace=ws)
+                            q_hilo=hilo, workspace=ws)
     ms = graph_time_ms([fn], steps, warmup)
     pairs = sum(min(p + 1, window) if window else p + 1 for p in range(S))
-    flops = 4 * HD * NH * pairs
+    flops = 4 * hd * nH * pairs
     host = tuple(x.cpu().numpy() for x in (q, qg, kc, vc, cos, sin)) + (flops,)
     return ms, flops, host
+
+
+# the prefill modes beside config 3's default (tag: prefill_case keywords)
+PREFILL_MODES = {"hilo": dict(hilo=True), "f32kv": dict(kv32=True), "hd512": dict(nH=8, kvH=1, hd=512)}
 
 
 def batched_decode_case(sa, steps, warmup, gen):
@@ -554,6 +567,9 @@ def main():
                     help="only the config 3 prefill rows (for profiling the prefill kernel)")
     ap.add_argument("--prefill-seq", type=int, default=1024,
                     help="prompt length of the --prefill-only rows (1024 = config 3, 8192 = config 5's layer)")
+    ap.add_argument("--prefill-mode", default="f16", choices=["f16"] + list(PREFILL_MODES),
+                    help="the --prefill-only rows' mode: config 3 as is, its f32-q (hilo) form, f32 caches, "
+                         "or hd 512 (nH 8 / kvH 1, the E2B global layers)")
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config 4 batched decode row (for profiling its kernels)")
     args = ap.parse_args()
@@ -573,8 +589,10 @@ def main():
     if args.prefill_only:
         out = {}
         cfgn = "3" if args.prefill_seq == 1024 else f"S{args.prefill_seq}"
-        for tag, win, th in ((f"prefill_{cfgn}g", 0, 1e6), (f"prefill_{cfgn}s", 512, 1e4)):
-            msp, fl, _ = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen)
+        mkw = PREFILL_MODES.get(args.prefill_mode, {})
+        sfx = "" if args.prefill_mode == "f16" else f"_{args.prefill_mode}"
+        for tag, win, th in ((f"prefill_{cfgn}g{sfx}", 0, 1e6), (f"prefill_{cfgn}s{sfx}", 512, 1e4)):
+            msp, fl, _ = prefill_case(sa, args.prefill_seq, win, th, args.steps, args.warmup, gen, **mkw)
             out[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(fl / msp / 1e9, 2)}
         print(json.dumps(out), flush=True)
         return
@@ -635,6 +653,17 @@ def main():
                         "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl,
                         "note": "one 8 MiB cache re-read by every call (MFMA-bound; the cache of a "
                                 "prefill layer was just written by its kv_write)"}
+        for mode, mkw in PREFILL_MODES.items():
+            cases = (((f"prefill_3g_{mode}", 0, 1e6), (f"prefill_3s_{mode}", 512, 1e4)) if mode != "hd512"
+                     else (("prefill_hd512g", 0, 1e6),))  # E2B's hd-512 layers are its global ones
+            for tag, win, th in cases:
+                msp, fl, _ = prefill_case(sa, 1024, win, th, max(8, args.steps // 8), args.warmup, gen, **mkw)
+                tf = fl / (msp * 1e-3) / 1e12
+                sec[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(tf, 2),
+                            "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl,
+                            "note": {"hilo": "config 3 in the f32-q attn_prefill form (G4A_Q_HILO)",
+                                     "f32kv": "config 3 on f32 caches",
+                                     "hd512": "S 1024 at hd 512, nH 8 / kvH 1 (E2B global layer shape)"}[mode]}
         ms4, nb4, toks = batched_decode_case(sa, max(8, args.steps // 16), args.warmup, gen)
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
                            "hbm_frac": round(nb4 / ms4 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb4,

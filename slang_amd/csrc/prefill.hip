@@ -1132,7 +1132,8 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     if ((long)p.n_qblocks * kvH >= 512) return p;
     // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
     // preparation and merge only while the unsplit grid leaves most CUs idle (hd 256, S 2048,
-    // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27)
+    // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27; hd 512, S 1024, W 512,
+    // 128 workgroups: 49.9 unsplit against 52.7)
     if (W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
     int max_tiles = 0;
     for (int qb = 0; qb < p.n_qblocks; ++qb) {
@@ -1166,6 +1167,7 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     return p;
 }
 
+namespace g4a {
 // f32 -> f16 copy (round to nearest even) of n8 groups of 8 cache values, K and V
 __global__ __launch_bounds__(256) void kv16_kernel(const float* kc, const float* vc, half_t* ko, half_t* vo,
                                                    size_t n8) {
@@ -1179,6 +1181,7 @@ __global__ __launch_bounds__(256) void kv16_kernel(const float* kc, const float*
     reinterpret_cast<half8*>(vo)[i] = half8{(half_t)v0[0], (half_t)v0[1], (half_t)v0[2], (half_t)v0[3],
                                             (half_t)v1[0], (half_t)v1[1], (half_t)v1[2], (half_t)v1[3]};
 }
+}  // namespace g4a
 
 extern "C" size_t g4a_prefill_ws_bytes(const g4a_cfg* cfg, int S, int start_pos) {
     if (!cfg) return 0;
