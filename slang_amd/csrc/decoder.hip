@@ -205,8 +205,25 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
                 stage_x(i, zq);
             }
         }
-    } else {
-        for (int i = tid; stage && i < n_in; i += 256) stage_x(i, g.x[i]);
+    } else if (stage) {
+        // every load of x first, in batches of 4096 values (4 float4 a thread), then the
+        // staging: one L2 round trip per batch instead of one per element
+        for (int b0 = 0; b0 < n_in; b0 += 4096) {
+            float4v xv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = b0 + 4 * (tid + 256 * k);
+                xv[k] = i < n_in ? *reinterpret_cast<const float4v*>(g.x + i) : float4v{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = b0 + 4 * (tid + 256 * k);
+                if (i < n_in) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) stage_x(i + e, xv[k][e]);
+                }
+            }
+        }
     }
     float xtot[NM];  // staged: the sum of the whole quantised x, known after the barrier
     if (stage) {
