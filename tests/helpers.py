@@ -1,4 +1,5 @@
 """Shared test helpers: the parity bar and input builders."""
+import itertools
 import os
 
 import numpy as np
@@ -83,3 +84,57 @@ def tie_aware_e2e(got, ref_own, ref_kernel_q, q16, q_f32, what):
     if bad_rows.any():
         contract_close(got[bad_rows], ref_kernel_q[bad_rows], f"{what}: tie rows on the kernel's q")
     return int(bad_rows.sum())
+
+
+def qlin_codes(x, words, scale, n_in, bits, in_q, out_q, lam=4.0):
+    """The values srq(qlin(x)) may take when the GEMV sums in f32 (oracle.decoder.qlin is
+    W @ srq(x, in_q), then srq(., out_q)). Returns (code, alt): code is the oracle's value
+    computed in float64, alt the grid value on the other side of the rounding midpoint where
+    the exact sum lies within the f32 sum's error of that midpoint (else alt == code).
+
+    The error allowed is lam * 2^-24 * m, m the sum of |terms| the kernels add (the raw codes
+    times x, and the zero point times the sum of x, subtracted once per row), plus 2^-21
+    |value| for the scale product and the division by out_q. Terms of random sign make an f32
+    sum's error grow like 2^-24 m, not n 2^-24 m (the probabilistic analyses of Higham and
+    Mary, SIAM J. Sci. Comput. 2019 and 2020); a sequential f32 sum of these tests' data
+    reaches 0.37 of 2^-24 m, so lam 4 leaves a factor ten."""
+    from oracle.projection import unpack_values
+    from oracle.attention import srq
+    codes = unpack_values(words, n_in, bits).astype(np.float64)
+    zp = float(1 << (bits - 1))
+    xs = srq(np.asarray(x, np.float32), in_q).astype(np.float64)
+    sc = np.abs(np.asarray(scale, np.float64))
+    v = np.asarray(scale, np.float64) * ((codes - zp) @ xs)
+    mag = sc * (codes @ np.abs(xs) + zp * np.abs(xs).sum())
+    err = lam * 2.0 ** -24 * mag + 2.0 ** -21 * np.abs(v)
+    k = v / out_q
+    base = np.clip(np.round(k), -128, 127)
+    other = np.clip(base + np.where(k >= base, 1.0, -1.0), -128, 127)
+    near = np.abs(np.abs(k - base) - 0.5) * out_q <= err
+    return (base * out_q).astype(np.float32), (np.where(near, other, base) * out_q).astype(np.float32)
+
+
+def chain_close(got, fn, operands, what="", step=None, max_flip_frac=0.05):
+    """got = fn(*operands), each operand a (code, alt) pair from qlin_codes: every element must
+    match fn for SOME choice of its operands' codes -- within one grid step of srq(fn, step)
+    (at most max_flip_frac of them a step off: a midpoint of the last rounding), or with
+    step None within 2e-3 + 1e-2 |fn|. An operand code only has a second choice where its own
+    sum sits on a rounding midpoint, so a wrong term, sign or index fails."""
+    from oracle.attention import srq
+    got = np.asarray(got, np.float64)
+    if step is not None:
+        assert np.abs(got / step - np.round(got / step)).max() < 1e-3, f"{what}: off the SRQ grid"
+    best = np.full(got.shape, np.inf)
+    n_alt = [int((a != c).sum()) for c, a in operands]
+    for choice in itertools.product(*[(0, 1)] * len(operands)):
+        ref = fn(*[operands[i][ch] for i, ch in enumerate(choice)]).astype(np.float32)
+        if step is not None:
+            d = np.abs(got - srq(ref, step)) / (step * 1.001)
+        else:
+            d = np.abs(got - ref) / (ATOL + RTOL * np.abs(ref.astype(np.float64)))
+        best = np.minimum(best, d)
+    bad = best > 1.0
+    assert not bad.any(), (f"{what}: {int(bad.sum())}/{bad.size} elements match no choice of operand codes "
+                           f"(worst {best.max():.2f}x the bound; operands with a second code: {n_alt})")
+    if step is not None:
+        assert (best > 0).mean() <= max_flip_frac, f"{what}: {(best > 0).mean():.2%} of elements a step off"

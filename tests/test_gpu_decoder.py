@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle.decoder as OD
-from helpers import contract_close, srq_close
+from helpers import chain_close, contract_close, qlin_codes, srq_close
 from manifest_fixture import write_model
 from oracle.projection import pack_values
 from slang_amd import decoder as D
@@ -51,16 +51,6 @@ def test_qgemv_parity(bits, n_in, n_out, in_q, out_q):
         contract_close(got, ref, f"qgemv {bits}-bit {n_out}x{n_in}")
 
 
-def srq_chain_close(got, ref_unq, step, what, frac=0.97, max_steps=8):
-    """An SRQ'd value computed from other SRQ'd values: on the grid, most elements within one
-    step of srq(ref), the rest (an input code that rounded the other way) a few steps off."""
-    got = np.asarray(got, np.float64)
-    assert np.abs(got / step - np.round(got / step)).max() < 1e-3, f"{what}: off the SRQ grid"
-    d = np.abs(got - OD.srq(np.asarray(ref_unq, np.float32), step))
-    assert (d <= step * 1.001).mean() >= frac, f"{what}: {(d > step * 1.001).mean():.2%} beyond one step"
-    assert d.max() <= step * max_steps * 1.001, f"{what}: {d.max() / step:.1f} steps off"
-
-
 @pytest.mark.parametrize("bits,n_in,n_out", [(4, 1536, 6144), (2, 1536, 12288), (4, 256, 1024), (8, 512, 64)])
 def test_qgemv_geglu_and_gelu_mul(bits, n_in, n_out):
     rng = np.random.default_rng(bits + n_out)
@@ -70,15 +60,12 @@ def test_qgemv_geglu_and_gelu_mul(bits, n_in, n_out):
     wd = lambda a: dev(a).view(torch.int32).reshape(-1)  # noqa: E731
     got = host(D.qgemv_geglu(dev(x), (wd(gw), dev(gs), 0.05, 0.02), (wd(uw), dev(us), 0.04, 0.03), n_in, n_out,
                              out_q=0.01, bits=bits))
-    g = OD.qlin(x, gw, gs, n_in, bits, 0.05, 0.0)
-    u = OD.qlin(x, uw, us, n_in, bits, 0.04, 0.0)
-    srq_chain_close(got, OD.gelu_tanh(OD.srq(g, 0.02)) * OD.srq(u, 0.03), 0.01, f"gate/up {bits}-bit")
+    g = qlin_codes(x, gw, gs, n_in, bits, 0.05, 0.02)
+    u = qlin_codes(x, uw, us, n_in, bits, 0.04, 0.03)
+    chain_close(got, lambda a, b: OD.gelu_tanh(a) * b, [g, u], f"gate/up {bits}-bit", step=0.01)
     mul = rng.standard_normal(n_out).astype(np.float32)
     got = host(D.qgemv_gelu_mul(dev(x), wd(gw), dev(gs), dev(mul), n_in, n_out, in_q=0.05, out_q=0.02, bits=bits))
-    ref = OD.gelu_tanh(OD.srq(g, 0.02)) * mul
-    ok = np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref)
-    assert ok.mean() >= 0.97, f"gelu_mul: {1 - ok.mean():.2%} off"   # the rest: a gate code rounded the other way
-    assert (np.abs(got - ref) <= 0.02 * 1.2 * np.abs(mul) + 2e-3).all()
+    chain_close(got, lambda a: OD.gelu_tanh(a) * mul, [g], f"gelu_mul {bits}-bit")
 
 
 def test_gemv_f16_parity():
@@ -170,17 +157,14 @@ def _stage_checks(m, L, t, ple_in):
     y2 = OD.srq(OD.rms_norm(g["x1"], o_w12[H:]).astype(np.float16).astype(np.float32), sc["gate_in"])
     assert np.abs(g["y2"] - y2).max() <= sc["gate_in"] * 1.001 and (g["y2"] != y2.astype(np.float16)).mean() < 0.05
     gb = bits("gate_bits", inter, H)
-    gate = OD.srq(OD.qlin(g["y2"], w("gate_bits"), w("gate_scale"), H, gb, sc["gate_in"]), sc["gate_out"])
-    up = OD.srq(OD.qlin(g["y2"], w("up_bits"), w("up_scale"), H, gb, sc["up_in"]), sc["up_out"])
-    srq_chain_close(g["geglu"], OD.gelu_tanh(gate) * up, sc["down_in"], what + " gate/up/geglu")
+    gate = qlin_codes(g["y2"], w("gate_bits"), w("gate_scale"), H, gb, sc["gate_in"], sc["gate_out"])
+    up = qlin_codes(g["y2"], w("up_bits"), w("up_scale"), H, gb, sc["up_in"], sc["up_out"])
+    chain_close(g["geglu"], lambda a, b: OD.gelu_tanh(a) * b, [gate, up], what + " gate/up/geglu", step=sc["down_in"])
     srq_close(g["down"], OD.qlin(g["geglu"], w("down_bits"), w("down_scale"), inter, bits("down_bits", H, inter),
                                  sc["down_in"]), sc["down_out"], what + " down")
     contract_close(g["x2"], g["x1"] + OD.rms_norm(g["down"], w("down_nw")), what + " x2")
-    pgate = OD.srq(OD.qlin(g["x2"], w("plegate_codes"), w("plegate_rowscale"), H, 8, sc["plegate_in"]),
-                   sc["plegate_out"])
-    ref = OD.gelu_tanh(pgate) * ple_in[L]
-    ok = np.abs(g["pleg"] - ref) <= 2e-3 + 1e-2 * np.abs(ref)
-    assert ok.mean() >= 0.9 and (np.abs(g["pleg"] - ref) <= 1.2 * sc["plegate_out"] * np.abs(ple_in[L]) + 2e-3).all()
+    pgate = qlin_codes(g["x2"], w("plegate_codes"), w("plegate_rowscale"), H, 8, sc["plegate_in"], sc["plegate_out"])
+    chain_close(g["pleg"], lambda a: OD.gelu_tanh(a) * ple_in[L], [pgate], what + " plegate")
     srq_close(g["pleproj"], OD.qlin(g["pleg"], w("pleproj_codes"), w("pleproj_rowscale"), d, 8, sc["pleproj_in"]),
               sc["pleproj_out"], what + " pleproj")
     contract_close(g["x3"], (g["x2"] + OD.rms_norm(g["pleproj"], pl[:H])) * pl[2 * H], what + " x3")

@@ -6,7 +6,7 @@ import sys
 import numpy as np
 
 import oracle.decoder as OD
-from oracle.projection import pack_values
+from oracle.projection import pack_values, unpack_values
 
 sys.path.insert(0, __file__.rsplit("/", 1)[0])
 from manifest_fixture import write_model  # noqa: E402
@@ -176,3 +176,61 @@ def test_prefill_inputs_match_the_decode_step_inputs(tmp_path):
         ref = OD.ple_input(m, t, x)
         assert np.abs(ple[i] - ref).max() < 2e-2 * np.abs(ref).max()
         assert np.abs(ple[i] - ref).mean() < 2e-3 * np.abs(ref).mean()
+
+
+def _qgemv_f32(x, words, scale, n_in, bits, in_q, out_q, drop_last=False, unq=False):
+    """A quantised GEMV summed the way the decode kernels sum it, in f32: per-16-value chunk
+    partial sums, the chunks added in order, the zero point times the sum of x subtracted,
+    then the scale and srq -- a different order and precision than the oracle's."""
+    codes = unpack_values(words, n_in, bits).astype(np.float32)
+    xs = OD.srq(np.asarray(x, np.float32), in_q)
+    if drop_last:
+        xs = xs.copy()
+        xs[-1] = 0
+    prod = (codes * xs[None, :]).reshape(codes.shape[0], -1, 16)
+    acc = np.zeros(codes.shape[0], np.float32)
+    for c in range(prod.shape[1]):
+        part = np.zeros(codes.shape[0], np.float32)
+        for e in range(16):
+            part = (part + prod[:, c, e]).astype(np.float32)
+        acc = (acc + part).astype(np.float32)
+    zsx = np.float32(1 << (bits - 1)) * np.float32(xs.sum(dtype=np.float32))
+    v = (np.asarray(scale, np.float32) * (acc - zsx)).astype(np.float32)
+    return v if unq else OD.srq(v, out_q)
+
+
+def test_tie_aware_chain_check_accepts_f32_orders_and_rejects_mistakes():
+    """The GPU decoder checks compare srq(gelu(srq(gate)) * srq(up)) chains against every choice
+    of the operand codes whose sums sit on a rounding midpoint (helpers.qlin_codes/chain_close).
+    An f32 GEMV in another summation order passes it; a dropped term, a swapped operand pair
+    or a wrong sign fails it; and few codes have a second choice."""
+    import pytest
+    from helpers import chain_close, qlin_codes
+    rng = np.random.default_rng(11)
+    n_in, n_out, bits = 1536, 4096, 4
+    gw, uw = (pack_values(rng.integers(0, 1 << bits, size=(n_out, n_in)), bits) for _ in range(2))
+    gs, us = ((0.01 * (1 + rng.random(n_out))).astype(np.float32) for _ in range(2))
+    x = (2 * rng.standard_normal(n_in)).astype(np.float32)
+    g = qlin_codes(x, gw, gs, n_in, bits, 0.05, 0.02)
+    u = qlin_codes(x, uw, us, n_in, bits, 0.04, 0.03)
+    assert (g[0] != g[1]).mean() < 0.05 and (u[0] != u[1]).mean() < 0.05
+    # the f32 order's error against the float64 sum, in units of 2^-24 * sum |terms|: a tenth
+    # of the allowance qlin_codes makes (lam 4)
+    codes = unpack_values(gw, n_in, bits).astype(np.float64)
+    xs = OD.srq(x, 0.05).astype(np.float64)
+    v64 = gs * ((codes - 8) @ xs)
+    m = gs * (codes @ np.abs(xs) + 8 * np.abs(xs).sum())
+    err = np.abs(_qgemv_f32(x, gw, gs, n_in, bits, 0.05, 0.0, unq=True) - v64) / (2.0 ** -24 * m)
+    assert 0 < err.max() < 0.4
+    fn = lambda a, b: OD.gelu_tanh(a) * b  # noqa: E731
+    gk = _qgemv_f32(x, gw, gs, n_in, bits, 0.05, 0.02)
+    uk = _qgemv_f32(x, uw, us, n_in, bits, 0.04, 0.03)
+    chain_close(OD.srq(fn(gk, uk), 0.01), fn, [g, u], "f32 order", step=0.01)
+    mul = rng.standard_normal(n_out).astype(np.float32)
+    chain_close(OD.gelu_tanh(gk) * mul, lambda a: OD.gelu_tanh(a) * mul, [g], "gelu_mul f32 order")
+    for bad in (OD.srq(fn(_qgemv_f32(x, gw, gs, n_in, bits, 0.05, 0.02, drop_last=True), uk), 0.01),
+                OD.srq(fn(uk, gk), 0.01), OD.srq(fn(gk, -uk), 0.01)):
+        with pytest.raises(AssertionError):
+            chain_close(bad, fn, [g, u], "planted", step=0.01)
+    with pytest.raises(AssertionError):
+        chain_close(OD.gelu_tanh(gk) * mul[::-1], lambda a: OD.gelu_tanh(a) * mul, [g], "planted gelu_mul")
