@@ -266,13 +266,16 @@ int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* 
 int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
               const float* w_scale, float out_q, float* out, void* stream);
 /*
- * Optional norm prologue of the two fused GEMVs below: the residual add and norm(s) in front
- * of them, done by every workgroup while it stages x (the runner's kernels fuse them the
- * same way, oproj_73 ending with the pre-FFN norm), so no kernel of its own runs:
- *   x = res + a / sqrt(mean(a^2) + eps) * w1          (stored to x_out by one workgroup)
+ * Optional norm prologue of the fused GEMVs below: the residual add and norm(s) in front of
+ * them, done by every workgroup while it stages x (the runner's kernels fuse them the same
+ * way, oproj_73 ending with the pre-FFN norm, pleproj_77 with the next layer's input norm),
+ * so no kernel of its own runs:
+ *   x = (res + a / sqrt(mean(a^2) + eps) * w1) * mult  (stored to x_out by one workgroup)
  *   z = x / sqrt(mean(x^2) + eps) * w2, or z = x when w2 is NULL
  *   GEMV input = f16 ? f16(srq(f16(z), q2)) : srq(z, q2)   (stored to z_out if non-NULL)
  * n_in <= 2048; x_out must not alias a, res or w1 (other workgroups still read them).
+ * mult is the layer scalar of the per-layer-embedding add (reference.py:191); 0 is read as 1,
+ * so a zero-initialised struct leaves x unscaled.
  */
 typedef struct {
     const float* a;
@@ -284,6 +287,7 @@ typedef struct {
     float q2;
     int f16;
     float eps;
+    float mult;
 } g4a_norm_in;
 /*
  * The MLP's gate/up pair with its GeGLU in one pass over x (gateup_74/95; reference.py:176-181):
@@ -299,6 +303,19 @@ int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_
 int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
                        const float* w_scale, float out_q, const float* mul, float* out,
                        const g4a_norm_in* pro, void* stream);
+/*
+ * g4a_qkv_gemv with its input made in the kernel from the previous layer's tail, so the
+ * layer-end add and the next input norm (rmssrq_69 after pleproj_77, runner.py:373-407)
+ * need no launch of their own: every workgroup forms
+ *   x = (res + a_pre / sqrt(mean(a_pre^2) + eps) * w1) * mult,  a = srq(rms(x) * w2, q2)
+ * from pro (w2 required, f16 must be 0) and runs qkv_70 on a with
+ * sum_a = sum of a. One workgroup stores x to pro->x_out, a to pro->z_out and sum_a to
+ * sum_out (each may be NULL). hidden <= 2048.
+ */
+int g4a_qkv_gemv_norm(int hidden, int q_dim, int kv_dim, const g4a_norm_in* pro, float* sum_out,
+                      const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
+                      const float* scales, float q_out, float k_out, float v_out, float* out_q,
+                      float* out_k, float* out_v, void* stream);
 /* Dense f16 GEMV: out[o] = sum_i w[o][i] x[i] in f32 (the per-layer-input projection,
  * reference.py:136, exported f16 by export.py:95). n_in a multiple of 8. */
 int g4a_gemv_f16(int n_in, int n_out, const float* x, const void* w_f16, float* out, void* stream);

@@ -28,7 +28,7 @@ EXPORTS = (
     "g4a_decode_ws_bytes", "g4a_decode", "g4a_decode_kv", "g4a_decode_noalloc",
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
-    "g4a_dequant", "g4a_qkv_gemv", "g4a_srqh", "g4a_gemm16",
+    "g4a_dequant", "g4a_qkv_gemv", "g4a_qkv_gemv_norm", "g4a_srqh", "g4a_gemm16",
     "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
     "g4a_embed", "g4a_embed_rows", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
     "g4a_rows_tail", "g4a_geglu16", "g4a_plegate16",
@@ -75,6 +75,7 @@ class G4ANormIn(ctypes.Structure):
         ("q2", ctypes.c_float),
         ("f16", ctypes.c_int),
         ("eps", ctypes.c_float),
+        ("mult", ctypes.c_float),
     ]
 
 
@@ -132,6 +133,8 @@ def load() -> ctypes.CDLL:
     lib.g4a_dequant.argtypes = [i, i, i, P, P, P, P]
     lib.g4a_qkv_gemv.restype = ctypes.c_int
     lib.g4a_qkv_gemv.argtypes = [i, i, i, P, P, P, P, P, P, f, f, f, P, P, P, P]
+    lib.g4a_qkv_gemv_norm.restype = ctypes.c_int
+    lib.g4a_qkv_gemv_norm.argtypes = [i, i, i, ctypes.POINTER(G4ANormIn), P, P, P, P, P, f, f, f, P, P, P, P]
     lib.g4a_srqh.restype = ctypes.c_int
     lib.g4a_srqh.argtypes = [i, P, f, P, P]
     lib.g4a_gemm16.restype = ctypes.c_int

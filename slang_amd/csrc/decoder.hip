@@ -49,7 +49,7 @@ struct QgemvArgs {
     const float* pw2;
     float* pxout;
     float* pzout;
-    float pq2, peps;
+    float pq2, peps, pmult;
     int pf16;
 };
 
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int i = tid + 256 * k;
-            const float y = rv[k] + av[k] / d * w1v[k];
+            const float y = (rv[k] + av[k] / d * w1v[k]) * g.pmult;
             av[k] = y;
             if (i < n_in) {
                 if (blockIdx.x == 0) g.pxout[i] = y;
@@ -608,6 +608,7 @@ static int norm_in_set(const g4a_norm_in* pro, int n_in, QgemvArgs& g) {
     g.pq2 = pro->q2;
     g.peps = pro->eps;
     g.pf16 = pro->f16 != 0;
+    g.pmult = pro->mult != 0.0f ? pro->mult : 1.0f;
     return G4A_OK;
 }
 

@@ -75,10 +75,21 @@ struct GemvArgs {
     float* out[3];
     float out_scale[3];
     int hidden, q_dim, kv_dim;
+    // norm prologue (PRO): a = srq(rms((pres + rms(pa) * pw1) * pmult) * pw2, pq2) made by
+    // every wave from the previous layer's tail; workgroup 0 stores x, a and sum_a
+    const float* pa;
+    const float* pres;
+    const float* pw1;
+    const float* pw2;
+    float* pxout;
+    float* pzout;
+    float* psum;
+    float pq2, peps, pmult;
 };
 
 // NJ chunks of 32 values per lane (hidden <= 2048 * NJ); RPW rows per wave, 4 waves.
-template <int NJ, int RPW>
+// PRO: the input a and its sum come from the norm prologue instead of memory (NJ 1).
+template <int NJ, int RPW, bool PRO>
 __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -100,15 +111,71 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
             const int off = c < row_bytes / 16 ? (r0 + r) * row_bytes + 16 * c : 0x7fffffff;
             wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kCpolNT);  // read once: non-temporal
         }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    float sa;
+    if constexpr (PRO) {
+        // lane c holds elements 32c .. 32c+31 of each operand (zeros past hidden); every wave
+        // forms the whole row's sums itself, so no barrier is needed. The arithmetic is the
+        // rms_kernel's: y = (res + pa / d1 * w1) * mult, z = y / d2 * w2, a = srq(z, q2).
+        static_assert(NJ == 1, "the norm prologue covers hidden <= 2048");
+        const uint32_t nb = (uint32_t)g.hidden * 4u;
+        const rsrc_t rpa = make_rsrc(g.pa, nb), rres = make_rsrc(g.pres, nb);
+        const rsrc_t rw1 = make_rsrc(g.pw1, nb), rw2 = make_rsrc(g.pw2, nb);
+        float pv[32], rv[32], w1v[32], w2v[32];
 #pragma unroll
         for (int q4 = 0; q4 < 8; ++q4) {
-            const float4v v = bload_f32x4(ra, 128 * (lane + 64 * j) + 16 * q4);
+            const int off = 128 * lane + 16 * q4;
+            const float4v a4 = bload_f32x4(rpa, off), r4 = bload_f32x4(rres, off);
+            const float4v u4 = bload_f32x4(rw1, off), v4 = bload_f32x4(rw2, off);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) av[j][4 * q4 + i] = v[i];
+            for (int i = 0; i < 4; ++i) {
+                pv[4 * q4 + i] = a4[i];
+                rv[4 * q4 + i] = r4[i];
+                w1v[4 * q4 + i] = u4[i];
+                w2v[4 * q4 + i] = v4[i];
+            }
         }
-    const float sa = g.sum_a[0];
+        const float inv_n = 1.0f / (float)g.hidden;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(pv[i], pv[i], ss);
+        const float d1 = sqrtf(wave_sum(ss) * inv_n + g.peps);
+        float ss2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            rv[i] = (rv[i] + pv[i] / d1 * w1v[i]) * g.pmult;  // x, zeros past hidden
+            ss2 = __builtin_fmaf(rv[i], rv[i], ss2);
+        }
+        const float d2 = sqrtf(wave_sum(ss2) * inv_n + g.peps);
+        float s2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            av[0][i] = srq(rv[i] / d2 * w2v[i], g.pq2);
+            s2 += av[0][i];
+        }
+        sa = wave_sum(s2);
+        if (blockIdx.x == 0 && wave == 0 && 32 * lane < g.hidden) {
+#pragma unroll
+            for (int q4 = 0; q4 < 8; ++q4) {
+                if (g.pxout)
+                    *reinterpret_cast<float4v*>(g.pxout + 32 * lane + 4 * q4) =
+                        float4v{rv[4 * q4], rv[4 * q4 + 1], rv[4 * q4 + 2], rv[4 * q4 + 3]};
+                if (g.pzout)
+                    *reinterpret_cast<float4v*>(g.pzout + 32 * lane + 4 * q4) =
+                        float4v{av[0][4 * q4], av[0][4 * q4 + 1], av[0][4 * q4 + 2], av[0][4 * q4 + 3]};
+            }
+            if (g.psum && lane == 0) g.psum[0] = sa;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int q4 = 0; q4 < 8; ++q4) {
+                const float4v v = bload_f32x4(ra, 128 * (lane + 64 * j) + 16 * q4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av[j][4 * q4 + i] = v[i];
+            }
+        sa = g.sum_a[0];
+    }
     float sc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) sc[r] = g.scales[(row0 + r)];
@@ -372,13 +439,26 @@ extern "C" int g4a_dequant(int bits, int n_in, int n_out, const uint32_t* w_bits
     return G4A_OK;
 }
 
-extern "C" int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, const float* sum_a,
-                            const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
-                            const float* scales, float q_out, float k_out, float v_out, float* out_q,
-                            float* out_k, float* out_v, void* stream) {
-    if (hidden <= 0 || hidden % 32 || hidden > 4096) {
-        set_error("hidden (%d) must be a positive multiple of 32, at most 4096", hidden);
+static int qkv_run(int hidden, int q_dim, int kv_dim, const float* a, const float* sum_a,
+                   const g4a_norm_in* pro, float* sum_out, const uint32_t* q_bits, const uint32_t* k_bits,
+                   const uint32_t* v_bits, const float* scales, float q_out, float k_out, float v_out,
+                   float* out_q, float* out_k, float* out_v, void* stream) {
+    if (hidden <= 0 || hidden % 32 || hidden > (pro ? 2048 : 4096)) {
+        set_error("hidden (%d) must be a positive multiple of 32, at most %d", hidden, pro ? 2048 : 4096);
         return G4A_EINVAL;
+    }
+    if (pro) {
+        if (!pro->a || !pro->res || !pro->w1 || !pro->w2 || pro->f16 || !(pro->q2 >= 0.0f) || !(pro->eps >= 0.0f)) {
+            set_error("qkv norm prologue: a, res, w1 and w2 non-NULL, f16 0, q2 and eps >= 0");
+            return G4A_EINVAL;
+        }
+        if (((uintptr_t)pro->a | (uintptr_t)pro->res | (uintptr_t)pro->w1 | (uintptr_t)pro->w2 |
+             (uintptr_t)pro->x_out | (uintptr_t)pro->z_out) & 15) {
+            set_error("qkv norm prologue: vectors must be 16-byte aligned");
+            return G4A_EINVAL;
+        }
+        a = pro->a;  // checked as the input below; the prologue makes the real one
+        sum_a = pro->a;
     }
     if (q_dim <= 0 || q_dim % 8 || kv_dim < 0 || kv_dim % 8) {
         set_error("q_dim (%d) must be a positive and kv_dim (%d) a non-negative multiple of 8", q_dim, kv_dim);
@@ -417,13 +497,45 @@ extern "C" int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, c
     g.hidden = hidden;
     g.q_dim = q_dim;
     g.kv_dim = kv_dim;
+    g.pa = pro ? pro->a : nullptr;
+    g.pres = pro ? pro->res : nullptr;
+    g.pw1 = pro ? pro->w1 : nullptr;
+    g.pw2 = pro ? pro->w2 : nullptr;
+    g.pxout = pro ? pro->x_out : nullptr;
+    g.pzout = pro ? pro->z_out : nullptr;
+    g.psum = sum_out;
+    g.pq2 = pro ? pro->q2 : 0.0f;
+    g.peps = pro ? pro->eps : 0.0f;
+    g.pmult = pro && pro->mult != 0.0f ? pro->mult : 1.0f;
     const int total = q_dim + 2 * kv_dim;  // rows; 2 per wave, 8 per workgroup
     const dim3 grid(total / 8);
-    if (hidden <= 2048)
-        hipLaunchKernelGGL((qkv_gemv_kernel<1, 2>), grid, dim3(256), 0, (hipStream_t)stream, g);
+    if (pro)
+        hipLaunchKernelGGL((qkv_gemv_kernel<1, 2, true>), grid, dim3(256), 0, (hipStream_t)stream, g);
+    else if (hidden <= 2048)
+        hipLaunchKernelGGL((qkv_gemv_kernel<1, 2, false>), grid, dim3(256), 0, (hipStream_t)stream, g);
     else
-        hipLaunchKernelGGL((qkv_gemv_kernel<2, 2>), grid, dim3(256), 0, (hipStream_t)stream, g);
+        hipLaunchKernelGGL((qkv_gemv_kernel<2, 2, false>), grid, dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "qkv_gemv launch");
     return G4A_OK;
+}
+
+extern "C" int g4a_qkv_gemv(int hidden, int q_dim, int kv_dim, const float* a, const float* sum_a,
+                            const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
+                            const float* scales, float q_out, float k_out, float v_out, float* out_q,
+                            float* out_k, float* out_v, void* stream) {
+    return qkv_run(hidden, q_dim, kv_dim, a, sum_a, nullptr, nullptr, q_bits, k_bits, v_bits, scales, q_out, k_out,
+                   v_out, out_q, out_k, out_v, stream);
+}
+
+extern "C" int g4a_qkv_gemv_norm(int hidden, int q_dim, int kv_dim, const g4a_norm_in* pro, float* sum_out,
+                                 const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
+                                 const float* scales, float q_out, float k_out, float v_out, float* out_q,
+                                 float* out_k, float* out_v, void* stream) {
+    if (!pro) {
+        set_error("pro must be non-NULL (g4a_qkv_gemv takes a made input)");
+        return G4A_EINVAL;
+    }
+    return qkv_run(hidden, q_dim, kv_dim, nullptr, nullptr, pro, sum_out, q_bits, k_bits, v_bits, scales, q_out,
+                   k_out, v_out, out_q, out_k, out_v, stream);
 }

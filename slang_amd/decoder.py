@@ -49,14 +49,17 @@ def qgemv(x, words, scale, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: f
     return out
 
 
-def norm_in(a, res, w1, x_out, *, w2=None, z_out=None, q2: float = 0.0, f16: bool = False, eps: float = EPS):
+def norm_in(a, res, w1, x_out, *, w2=None, z_out=None, q2: float = 0.0, f16: bool = False, eps: float = EPS,
+            mult: float = 1.0):
     """The residual-add + norm prologue of the fused GEMVs (struct g4a_norm_in): their input
-    becomes srq(rms(res + rms(a) * w1) * w2, q2) (f16-rounded around the srq with f16), with
-    x = res + rms(a) * w1 stored to x_out (which must not alias a, res or w1)."""
+    becomes srq(rms(x) * w2, q2) (f16-rounded around the srq with f16), with
+    x = (res + rms(a) * w1) * mult stored to x_out (which must not alias a, res or w1).
+    The struct holds raw device pointers: the tensors must stay alive until the call that
+    takes it has been issued."""
     for t, n in ((a, "a"), (res, "res"), (w1, "w1"), (x_out, "x_out")):
         _need(t, n, torch.float32)
     return _lib.G4ANormIn(_ptr(a), _ptr(res), _ptr(w1), _ptr(w2) if w2 is not None else None, _ptr(x_out),
-                          _ptr(z_out) if z_out is not None else None, float(q2), int(f16), float(eps))
+                          _ptr(z_out) if z_out is not None else None, float(q2), int(f16), float(eps), float(mult))
 
 
 def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int | None = None, out=None,
@@ -304,17 +307,33 @@ class DecoderStack:
         rms_norm(self.x, self.w[0]["in_norm"], out=self.h, q2=self.man.layers[0].scales["qkv_in"], out2=self.a,
                  sum2=self.sum_a)
 
-    def layer(self, L: int, pos: int, trace: dict | None = None):
-        """Layer L on self.x in place (reference.py:141-191), from its srq'd input norm in
-        self.a / self.sum_a; it leaves the next layer's (or, last, the final norm in self.hf).
-        The norms ride on the kernels after the adds as the runner fuses them (oproj_73 ends
-        with the pre-FFN norm, pleproj_77 with the next layer's input norm)."""
+    def layer(self, L: int, pos: int, trace: dict | None = None, prev: dict | None = None):
+        """Layer L on the residual from its input norm (reference.py:141-191). Layer 0 starts
+        from x and its srq'd input norm in self.a / self.sum_a (embed_token); every later layer
+        first finishes the previous layer's tail inside its q/k/v GEMV: x3 = (x2 + rms(pleproj)
+        * post_ple) * layer_scalar and a = srq(rms(x3) * in_norm, qkv_in), as pleproj_77 ends
+        with rmssrq_69. The norms ride on the kernels after the adds as the runner fuses them
+        (oproj_73 ends with the pre-FFN norm). The residual alternates between self.x and
+        self.xb, since a workgroup that stores the new residual must not overwrite the one the
+        others still read: layer L's input is in self.x for even L, self.xb for odd L, and the
+        last layer's tail and the final norm run as one g4a_rms_norm in place (residual()).
+        trace gets this layer's stages, prev (the previous layer's trace) its x3 and a_next."""
         s, w, H = self.man.layers[L], self.w[L], self.H
         sc, inter = s.scales, s.intermediate
+        xin, xalt = (self.x, self.xb) if L % 2 == 0 else (self.xb, self.x)
         snap = (lambda k, t: trace.__setitem__(k, t.clone())) if trace is not None else (lambda k, t: None)
-        snap("x0", self.x)
+        if L == 0:
+            attn = self.attn.decode_layer(L, pos, self.a, self.sum_a).view(-1)
+        else:
+            pw = self.w[L - 1]
+            pro = norm_in(self.pleproj, xalt, pw["post_ple"], xin, w2=w["in_norm"], q2=sc["qkv_in"],
+                          mult=pw["layer_scalar"])
+            attn = self.attn.decode_layer(L, pos, self.a, self.sum_a, pro=pro).view(-1)
+            if prev is not None:
+                prev["x3"] = xin.clone()
+                prev["a_next"] = self.a.clone()
+        snap("x0", xin)
         snap("a", self.a)
-        attn = self.attn.decode_layer(L, pos, self.a, self.sum_a).view(-1)
         snap("attn", attn)
         # inputs already on their step's grid skip the GEMV's srq (srq(srq(v, s), s) = srq(v, s)
         # exactly): the attention output carries o_in, the GeGLU output down_in
@@ -322,39 +341,38 @@ class DecoderStack:
               out=self.o)
         snap("o", self.o)
         # x1 = x + rms(o) * w1 and the MLP input y2 = f16(srq(f16(rms(x1) * w2), gate_in)) are
-        # made by the gate/up kernel's prologue (x1 into the second residual buffer xb)
+        # made by the gate/up kernel's prologue (x1 into the other residual buffer)
         gg = self.gg[:inter]
         qgemv_geglu(None, (w["gate_bits"], w["gate_scale"], sc["gate_in"], sc["gate_out"]),
                     (w["up_bits"], w["up_scale"], sc["up_in"], sc["up_out"]), H, inter, out_q=sc["down_in"],
                     bits=w["gate_bits_n"], out=gg,
-                    pro=norm_in(self.o, self.x, w["o_w1"], self.xb, w2=w["o_w2"], z_out=self.y2, q2=sc["gate_in"],
+                    pro=norm_in(self.o, xin, w["o_w1"], xalt, w2=w["o_w2"], z_out=self.y2, q2=sc["gate_in"],
                                 f16=True))
-        snap("x1", self.xb)
+        snap("x1", xalt)
         snap("y2", self.y2)
         snap("geglu", gg)
         qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=0.0, out_q=sc["down_out"],
               bits=w["down_bits_n"], out=self.down)
         snap("down", self.down)
-        # x2 = x1 + rms(down) * w: the per-layer-embedding gate kernel's prologue, back into x
+        # x2 = x1 + rms(down) * w: the per-layer-embedding gate kernel's prologue, back into xin
         qgemv_gelu_mul(None, w["plegate_codes"], w["plegate_rowscale"], self.ple_in[L], H, self.d,
                        in_q=sc["plegate_in"], out_q=sc["plegate_out"], bits=8, out=self.pleg,
-                       pro=norm_in(self.down, self.xb, w["down_nw"], self.x))
-        snap("x2", self.x)
+                       pro=norm_in(self.down, xalt, w["down_nw"], xin))
+        snap("x2", xin)
         snap("pleg", self.pleg)
         qgemv(self.pleg, w["pleproj_codes"], w["pleproj_rowscale"], self.d, H, in_q=sc["pleproj_in"],
               out_q=sc["pleproj_out"], bits=8, out=self.pleproj)
         snap("pleproj", self.pleproj)
-        if L + 1 < self.nL:
-            rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x,
-                     w2=self.w[L + 1]["in_norm"], q2=self.man.layers[L + 1].scales["qkv_in"], out2=self.a,
-                     sum2=self.sum_a)
-            snap("x3", self.x)
-            snap("a_next", self.a)
-        else:
-            rms_norm(self.pleproj, w["post_ple"], res=self.x, mult=w["layer_scalar"], out=self.x,
+        if L + 1 == self.nL:
+            # the last layer's tail and the final norm (no q/k/v GEMV follows to carry them)
+            rms_norm(self.pleproj, w["post_ple"], res=xin, mult=w["layer_scalar"], out=xin,
                      w2=self.final_norm, out2=self.hf)
-            snap("x3", self.x)
+            snap("x3", xin)
             snap("hf", self.hf)
+
+    def residual(self) -> torch.Tensor:
+        """The residual stream after the last layer (x3 of layer nL - 1)."""
+        return self.x if (self.nL - 1) % 2 == 0 else self.xb
 
     # ---------------------------------------------------------------- batched prefill
     def _prefill_weights(self, L: int) -> dict:
@@ -495,10 +513,12 @@ class DecoderStack:
         self.embed_token()
         if trace is not None:
             trace.append({"x": self.x.clone(), "ple_in": self.ple_in.clone()})
+        prev = None
         for L in range(self.nL):
             t = {} if trace is not None else None
-            self.layer(L, pos, t)
+            self.layer(L, pos, t, prev)
             if trace is not None:
                 trace.append(t)
+            prev = t
         self.head()
         return self.tok

@@ -260,11 +260,13 @@ class AttentionStack:
         cos, sin = self.rope[self.man.rope_key(L)]
         return cos[lo:hi], sin[lo:hi]
 
-    def decode_layer(self, L: int, pos: int, a: torch.Tensor, sum_a: torch.Tensor, out=None):
+    def decode_layer(self, L: int, pos: int, a: torch.Tensor, sum_a: torch.Tensor, out=None, pro=None):
         """Layer L's attention for one token at position pos from its normed, srq'd input a
         f32 [H] (and sum_a f32 [1]): qkv_70 -> kvnorm (non-shared layers) -> attn_101.
         Returns the srq'd attention output f32 [nH][hd] (runner.py:408-441). The KV write of
-        a non-shared layer runs inside the decode call (g4a_decode_kv)."""
+        a non-shared layer runs inside the decode call (g4a_decode_kv). pro: a norm prologue
+        (decoder.norm_in) that makes a and sum_a inside the q/k/v GEMV from the previous
+        layer's tail instead (a, sum_a then receive them)."""
         s, man, w = self.man.layers[L], self.man, self.w[L]
         if not 0 <= pos < self.max_seq:
             raise ValueError(f"position {pos} outside the {self.max_seq}-row caches")
@@ -273,7 +275,8 @@ class AttentionStack:
         sc = s.scales
         q, k, v = P.qkv_gemv(a, sum_a, w["q_bits"], w["scales"], s.q_dim, kv_dim,
                              k_bits=w.get("k_bits"), v_bits=w.get("v_bits"), q_out=sc.get("q_out", 0.0),
-                             k_out=sc.get("k_out", 0.0), v_out=sc.get("v_out", 0.0))
+                             k_out=sc.get("k_out", 0.0), v_out=sc.get("v_out", 0.0), pro=pro,
+                             hidden=man.hidden)
         kc, vc = self.caches(L)
         cos, sin = self._rows(L, pos, pos + 1)
         kv = {} if s.shared else dict(k_new=k, v_new=v, k_gain=w["k_norm"])

@@ -62,12 +62,19 @@ def dq_f16(bits, scale, out, p, scale_offset: int = 0):
 
 def qkv_gemv(a, sum_a, q_bits, scales, q_dim: int, kv_dim: int = 0, k_bits=None, v_bits=None,
              q_out: float = 0.0, k_out: float = 0.0, v_out: float = 0.0,
-             out_q=None, out_k=None, out_v=None):
+             out_q=None, out_k=None, out_v=None, pro=None, hidden: int | None = None):
     """Decode q/k/v of one token from 4-bit rows (qkv_70). kv_dim 0: q only (KV-sharing
-    layers). Returns (q, k, v); k and v are None when kv_dim is 0."""
-    hidden = a.numel()
-    _need(a, "a", torch.float32)
-    _need(sum_a, "sum_a", torch.float32)
+    layers). Returns (q, k, v); k and v are None when kv_dim is 0.
+
+    pro: a decoder.norm_in(...) prologue (w2 given, f16 off) that makes the input in the kernel
+    from the previous layer's tail (g4a_qkv_gemv_norm); a and sum_a are then None or the
+    buffers that receive the made input and its sum, and hidden gives the width."""
+    if pro is None:
+        hidden = a.numel()
+        _need(a, "a", torch.float32)
+        _need(sum_a, "sum_a", torch.float32)
+    elif hidden is None:
+        raise ValueError("qkv_gemv with a prologue needs hidden")
     _need(scales, "scales", torch.float32)
     for t, nm, rows in ((q_bits, "q_bits", q_dim), (k_bits, "k_bits", kv_dim), (v_bits, "v_bits", kv_dim)):
         if rows:
@@ -76,7 +83,7 @@ def qkv_gemv(a, sum_a, q_bits, scales, q_dim: int, kv_dim: int = 0, k_bits=None,
                 raise ValueError(f"{nm} must hold {rows} 4-bit rows of {hidden} values")
     if scales.numel() < q_dim + 2 * kv_dim:
         raise ValueError("scales needs q_dim + 2*kv_dim entries")
-    dev = a.device
+    dev = scales.device
     out_q = torch.empty(q_dim, device=dev, dtype=torch.float32) if out_q is None else out_q
     if kv_dim:
         out_k = torch.empty(kv_dim, device=dev, dtype=torch.float32) if out_k is None else out_k
@@ -86,11 +93,20 @@ def qkv_gemv(a, sum_a, q_bits, scales, q_dim: int, kv_dim: int = 0, k_bits=None,
             _need(t, nm, torch.float32)
             if t.numel() < n:
                 raise ValueError(f"{nm} needs {n} entries")
-    check(_lib.load().g4a_qkv_gemv(hidden, q_dim, kv_dim, _ptr(a), _ptr(sum_a), _ptr(q_bits),
-                                   _ptr(k_bits if kv_dim else None), _ptr(v_bits if kv_dim else None),
-                                   _ptr(scales), q_out, k_out, v_out, _ptr(out_q),
-                                   _ptr(out_k if kv_dim else None), _ptr(out_v if kv_dim else None),
-                                   _stream()))
+    lib = _lib.load()
+    kb, vb = _ptr(k_bits if kv_dim else None), _ptr(v_bits if kv_dim else None)
+    ok, ov = _ptr(out_k if kv_dim else None), _ptr(out_v if kv_dim else None)
+    if pro is None:
+        check(lib.g4a_qkv_gemv(hidden, q_dim, kv_dim, _ptr(a), _ptr(sum_a), _ptr(q_bits), kb, vb,
+                               _ptr(scales), q_out, k_out, v_out, _ptr(out_q), ok, ov, _stream()))
+    else:
+        if a is not None:
+            _need(a, "a", torch.float32)
+            pro.z_out = _ptr(a)
+        if sum_a is not None:
+            _need(sum_a, "sum_a", torch.float32)
+        check(lib.g4a_qkv_gemv_norm(hidden, q_dim, kv_dim, ctypes.byref(pro), _ptr(sum_a), _ptr(q_bits), kb, vb,
+                                    _ptr(scales), q_out, k_out, v_out, _ptr(out_q), ok, ov, _stream()))
     return (out_q, out_k, out_v) if kv_dim else (out_q, None, None)
 
 

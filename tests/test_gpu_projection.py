@@ -98,6 +98,51 @@ def test_qkv_gemv_matches_oracle(hidden, qd, kvd, scales):
         assert np.count_nonzero(g), f"out_{nm} empty"
 
 
+@pytest.mark.parametrize("hidden,qd,kvd", [(1536, 2048, 256), (1536, 4096, 0), (2048, 512, 512), (256, 64, 8)])
+def test_qkv_gemv_norm_prologue(hidden, qd, kvd):
+    """g4a_qkv_gemv_norm: the previous layer's tail x = (x2 + rms(p) * w1) * mult and the input
+    norm a = srq(rms(x) * w2, q2) made in the kernel. x against the oracle at the contract, a
+    on its grid from the GPU's own x, sum_a against the sum of a, and q/k/v bit for bit equal
+    to g4a_qkv_gemv run on the stored a and sum_a (the same arithmetic from memory)."""
+    from oracle.decoder import rms_norm
+    from slang_amd.decoder import norm_in
+    rng = np.random.default_rng(hidden + qd)
+    _, _, qb, kb, vb, sc = gemv_case(7, hidden, qd, kvd)
+    p = (0.3 * rng.standard_normal(hidden)).astype(np.float32)
+    x2 = rng.standard_normal(hidden).astype(np.float32)
+    w1 = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    w2 = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    mult, q2 = 0.8125, 0.05
+    print(f"qkv_gemv_norm hidden {hidden} q {qd} kv {kvd}", flush=True)
+    x_out = torch.full((hidden,), 7.0, device=DEV)
+    a_out = torch.full((hidden,), 7.0, device=DEV)
+    s_out = torch.full((1,), 7.0, device=DEV)
+    kw = dict(k_bits=dev_words(kb), v_bits=dev_words(vb), q_out=0.03125, k_out=0.0234375, v_out=0.0156)
+    # the prologue struct holds raw pointers: its tensors must outlive the calls
+    dp, dx2, dw1, dw2, dqb, dsc = t(p), t(x2), t(w1), t(w2), dev_words(qb), t(sc)
+    pro = norm_in(dp, dx2, dw1, x_out, w2=dw2, q2=q2, mult=mult)
+    got = sa.qkv_gemv(a_out, s_out, dqb, dsc, qd, kvd, pro=pro, hidden=hidden, **kw)
+    torch.cuda.synchronize()
+    x = x_out.cpu().numpy()
+    contract_close(x, (x2 + rms_norm(p, w1)) * np.float32(mult), "x")
+    a = a_out.cpu().numpy()
+    srq_close(a, rms_norm(x, w2), q2, "a")
+    assert abs(float(s_out.cpu()[0]) - a.sum(dtype=np.float64)) <= 1e-5 * np.abs(a).sum() + 1e-6
+    ref = sa.qkv_gemv(a_out, s_out, dqb, dsc, qd, kvd, **kw)
+    torch.cuda.synchronize()
+    for nm, g, r in zip("qkv", got, ref):
+        if r is not None:
+            assert torch.equal(g, r), f"out_{nm} differs from g4a_qkv_gemv on the stored input"
+    # the stores are optional: without them the outputs are the same
+    pro = norm_in(dp, dx2, dw1, x_out, w2=dw2, q2=q2, mult=mult)
+    pro.x_out = None
+    again = sa.qkv_gemv(None, None, dqb, dsc, qd, kvd, pro=pro, hidden=hidden, **kw)
+    torch.cuda.synchronize()
+    for g, r in zip(again, ref):
+        if r is not None:
+            assert torch.equal(g, r)
+
+
 def test_qkv_70_dropin_and_shared_layer():
     a, suma, qb, kb, vb, sc = gemv_case(5, 1536, 2048, 256)
     oq = torch.full((2048,), 7.0, device=DEV)
