@@ -78,6 +78,8 @@ struct DecodeShape {
     static constexpr int VROWS = 64 / VLANES;      // V rows per load instruction
     static constexpr int VLOADS = 16 / VROWS;      // V load instructions per block
     static constexpr int VSTR = HD + 16;           // LDS V row stride (halves): tr reads conflict-free
+    static constexpr int KSTR = HD + 8;            // LDS K row stride (halves): A-operand reads conflict-free
+    static constexpr int K_HALVES = 4 * 16 * KSTR; // per-wave K blocks (whole-row K loads)
     static constexpr int QSTR = HD + 8;            // LDS q row stride (halves)
     static constexpr int V_HALVES = 4 * 16 * VSTR; // per-wave V blocks
     static constexpr int Q_HALVES = 2 * G * QSTR;  // high rows then low rows
@@ -261,9 +263,18 @@ void decode_kernel(DecodeArgs a) {
     using VO = VOp<KVT>;
     typedef typename KO::raw kraw_t;
     typedef typename VO::raw vraw_t;
+    // hd 256, f16 caches: K rows are loaded whole, as V rows are (two 512-byte rows per
+    // instruction), and staged in a per-wave LDS block from which the MFMA A operands are
+    // read. Loaded straight in the A layout, each instruction took 64 bytes from each of 16
+    // rows; a read-only kernel over config 4's geometry streamed 6.9 TB/s with whole rows
+    // against 6.4 TB/s with that pattern.
+    constexpr bool KROW = HD == 256 && sizeof(KVT) == 2;
+    constexpr int KSTR = Sh::KSTR;
+    constexpr int ARENA = KROW && (Sh::V_HALVES + Sh::K_HALVES) * 2 > Sh::LDS_BYTES
+                              ? (Sh::V_HALVES + Sh::K_HALVES) * 2 : Sh::LDS_BYTES;
 
-    // one LDS arena, reused: q rows (prologue) -> V blocks (main loop) -> partials (merges)
-    __shared__ __attribute__((aligned(16))) char arena[Sh::LDS_BYTES];
+    // one LDS arena, reused: q rows (prologue) -> V (and K) blocks (main loop) -> partials (merges)
+    __shared__ __attribute__((aligned(16))) char arena[ARENA];
     half_t* sQ = reinterpret_cast<half_t*>(arena);
     half_t* sV = reinterpret_cast<half_t*>(arena);
     float* lds = reinterpret_cast<float*>(arena);
@@ -358,12 +369,18 @@ void decode_kernel(DecodeArgs a) {
     const rsrc_t rv = make_rsrc(reinterpret_cast<const KVT*>(a.vc) + row0, range);
     const int vrow = lane / VLANES;
     const int koff = n * rsb + 8 * g * ESZ, voff = vrow * rsb + 8 * (lane % VLANES) * ESZ;
-    kraw_t kr[KSTEPS];
+    kraw_t kr[KROW ? 1 : KSTEPS];
+    half8 krow[KROW ? VLOADS : 1];
     vraw_t vr[VLOADS];
     auto load_block = [&](int blk) {
         const int r = (blk - k0) * rsb;
+        if constexpr (KROW) {
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::load(rk, r + koff + 32 * s * ESZ);
+            for (int i = 0; i < VLOADS; ++i) krow[i] = bload_h8_nt(rk, r + VROWS * i * rsb + voff);
+        } else {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::load(rk, r + koff + 32 * s * ESZ);
+        }
 #pragma unroll
         for (int i = 0; i < VLOADS; ++i) vr[i] = VO::load(rv, r + VROWS * i * rsb + voff);
     };
@@ -440,6 +457,7 @@ void decode_kernel(DecodeArgs a) {
 
     // ---- main loop: per wave, 16-key blocks with an online softmax per head column
     half_t* myV = sV + wave * 16 * VSTR;
+    half_t* myK = sV + Sh::V_HALVES + wave * 16 * KSTR;  // KROW only
     float m_run = kNegInf, l_run = 0.0f;  // column n (heads: n < G)
     float4v oacc[NDT];                    // O^T[16dt + 4g + i][column n]
 #pragma unroll
@@ -449,23 +467,48 @@ void decode_kernel(DecodeArgs a) {
         // the block holding the new key: its row comes from the prepared copy, whatever
         // the load (issued before the store) returned
         const bool patch = owns_new && p_new >= blk && p_new < blk + 16;  // wave-uniform
-        if (patch && n == p_new - blk) {
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::lds(&sKn[32 * s + 8 * g]);
-        }
         float4v c4 = float4v{0, 0, 0, 0};
+        if constexpr (KROW) {
+            // K and V rows into this wave's LDS blocks (the new key's row over whatever its
+            // load returned; LDS operations of one wave complete in order), the next block's
+            // loads, then the K operands back in the A layout
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
+            for (int i = 0; i < VLOADS; ++i) {
+                *reinterpret_cast<half8*>(&myK[(VROWS * i + vrow) * KSTR + 8 * (lane % VLANES)]) = krow[i];
+                *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
+            }
+            if (patch && lane < HD / 8) {
+                half8 hk, hv;
 #pragma unroll
-        for (int i = 0; i < VLOADS; ++i)
-            *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
-        if (patch && lane < HD / 8) {  // rounded to f16 as VO::h rounds a loaded row
-            half8 hv;
+                for (int i = 0; i < 8; ++i) {
+                    hk[i] = (half_t)(float)sKn[8 * lane + i];
+                    hv[i] = (half_t)(float)sVn[8 * lane + i];
+                }
+                *reinterpret_cast<half8*>(&myK[(p_new - blk) * KSTR + 8 * lane]) = hk;
+                *reinterpret_cast<half8*>(&myV[(p_new - blk) * VSTR + 8 * lane]) = hv;
+            }
+            if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during the products
 #pragma unroll
-            for (int i = 0; i < 8; ++i) hv[i] = (half_t)(float)sVn[8 * lane + i];
-            *reinterpret_cast<half8*>(&myV[(p_new - blk) * VSTR + 8 * lane]) = hv;
+            for (int s = 0; s < KSTEPS; ++s)
+                c4 = mfma16x32(*reinterpret_cast<const half8*>(&myK[n * KSTR + 32 * s + 8 * g]), qop[s], c4);
+        } else {
+            if (patch && n == p_new - blk) {
+#pragma unroll
+                for (int s = 0; s < KSTEPS; ++s) kr[s] = KO::lds(&sKn[32 * s + 8 * g]);
+            }
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) c4 = KO::dot(kr[s], qop[s], c4);
+#pragma unroll
+            for (int i = 0; i < VLOADS; ++i)
+                *reinterpret_cast<half8*>(&myV[(VROWS * i + vrow) * VSTR + 8 * (lane % VLANES)]) = VO::h(vr[i]);
+            if (patch && lane < HD / 8) {  // rounded to f16 as VO::h rounds a loaded row
+                half8 hv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) hv[i] = (half_t)(float)sVn[8 * lane + i];
+                *reinterpret_cast<half8*>(&myV[(p_new - blk) * VSTR + 8 * lane]) = hv;
+            }
+            if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during softmax and P.V
         }
-        if (blk + 64 < k1) load_block(blk + 64);  // next block in flight during softmax and P.V
         float sc[4], mloc = kNegInf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
