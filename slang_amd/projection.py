@@ -100,6 +100,7 @@ def qkv_gemv(a, sum_a, q_bits, scales, q_dim: int, kv_dim: int = 0, k_bits=None,
         check(lib.g4a_qkv_gemv(hidden, q_dim, kv_dim, _ptr(a), _ptr(sum_a), _ptr(q_bits), kb, vb,
                                _ptr(scales), q_out, k_out, v_out, _ptr(out_q), ok, ov, _stream()))
     else:
+        pro = _lib.G4ANormIn.from_buffer_copy(pro)  # the caller's struct stays as it was
         if a is not None:
             _need(a, "a", torch.float32)
             pro.z_out = _ptr(a)
