@@ -234,14 +234,21 @@ struct Gemm16Args {
     int tile_end[3];  // cumulative tiles (n_p / 128) * mtiles
 };
 
-template <int BK>
+// BN = 64 (outputs per tile) halves the tile for products too narrow to fill the GPU with
+// 128 x 128 tiles (N 1536 at M 1024 gives 96 of them for 256 CUs): each wave then covers 32
+// outputs x 64 tokens, reading one W block for two MFMAs, and three stages (72 KiB of LDS)
+// let two workgroups share a CU.
+template <int BK, int BN>
 __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
-    constexpr int BM = 128, BN = 128, ROWB = BK * 2, OPB = 128 * ROWB;  // operand tile bytes
-    constexpr int STAGES = 4, STAGEB = 2 * OPB;
+    constexpr int BM = 128, ROWB = BK * 2;
+    constexpr int OPBW = BN * ROWB, OPBA = BM * ROWB;  // operand tile bytes (W, A)
+    constexpr int STAGES = BN == 64 ? 3 : 4, STAGEB = OPBW + OPBA;  // 72 / 128 KiB: 2 / 1 per CU
     constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;           // rows per 1 KiB wave instruction
-    constexpr int IPO = 32 / RPI;           // instructions per operand and wave per stage
-    constexpr int IPS = 2 * IPO;            // ... per stage (W and A)
+    constexpr int WROWS = BN / 4;           // W rows each wave moves per stage
+    constexpr int IPOW = WROWS / RPI, IPOA = 32 / RPI;  // instructions per operand and wave per stage
+    constexpr int IPS = IPOW + IPOA;        // ... per stage (W and A)
+    constexpr int NB = BN / 64;             // 32-output blocks per wave
     // chunk c of row r sits at c ^ swz(r): the rows sharing a 256-byte bank window get
     // distinct chunks, so a quarter-wave operand read touches 16 distinct bank groups
     auto swz = [](int r) { return (r / (256 / ROWB)) % CPR; };
@@ -262,22 +269,29 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
 
     const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * K * 2);  // token rows >= M read as zeros
     const rsrc_t rw = make_rsrc(g.w[p], (uint32_t)g.n[p] * K * 2);
-    // wave w moves rows 32w .. 32w+31 of both operands, RPI rows (1 KiB) per instruction
+    // wave w moves W rows WROWS w .. and A rows 32w .. 32w+31, RPI rows (1 KiB) per instruction
     auto issue = [&](int kt) {
         char* st = lds + (kt % STAGES) * STAGEB;
         const int kb = kt * BK * 2;
 #pragma unroll
-        for (int i = 0; i < IPO; ++i) {
+        for (int i = 0; i < IPOW; ++i) {
+            const int r = WROWS * wave + RPI * i + lane / CPR;
+            const int c = (lane % CPR) ^ swz(r);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (WROWS * wave + RPI * i) * ROWB),
+                                                     16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < IPOA; ++i) {
             const int r = 32 * wave + RPI * i + lane / CPR;
             const int c = (lane % CPR) ^ swz(r);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (32 * wave + RPI * i) * ROWB),
-                                                     16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPB + (32 * wave + RPI * i) * ROWB),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPBW + (32 * wave + RPI * i) * ROWB),
                                                      16, (m0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
     };
 
-    float16v acc[2][2] = {{float16v{}, float16v{}}, {float16v{}, float16v{}}};
+    float16v acc[NB][2];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb][0] = acc[nb][1] = float16v{};
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < nk) issue(s);
@@ -290,15 +304,19 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
         __syncthreads();  // every wave's part of stage kt; stage kt - 1 fully consumed
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
         const char* wl = lds + (kt % STAGES) * STAGEB;
-        const char* al = wl + OPB;
+        const char* al = wl + OPBW;
         // lane (l32, h) holds k 16s + 8h .. +7 of k-step s; the operands of step s + 1 are
         // read while the MFMAs of step s run (one wave per SIMD hides no LDS latency itself)
-        half8 wo[2][2], ao[2][2];
-        auto rd = [&](int s, half8 (&w)[2], half8 (&x)[2]) {
+        half8 wo[2][NB], ao[2][2];
+        auto rd = [&](int s, half8 (&w)[NB], half8 (&x)[2]) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int rw_ = (BN / 2) * wn + 32 * b + l32;
+                w[b] = *reinterpret_cast<const half8*>(wl + rw_ * ROWB + 16 * ((2 * s + h) ^ swz(rw_)));
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int rw_ = 64 * wn + 32 * b + l32, ra_ = 64 * wm + 32 * b + l32;
-                w[b] = *reinterpret_cast<const half8*>(wl + rw_ * ROWB + 16 * ((2 * s + h) ^ swz(rw_)));
+                const int ra_ = 64 * wm + 32 * b + l32;
                 x[b] = *reinterpret_cast<const half8*>(al + ra_ * ROWB + 16 * ((2 * s + h) ^ swz(ra_)));
             }
         };
@@ -307,7 +325,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
         for (int s = 0; s < BK / 16; ++s) {
             if (s + 1 < BK / 16) rd(s + 1, wo[(s + 1) & 1], ao[(s + 1) & 1]);
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = proj_mfma32(wo[s & 1][nb], ao[s & 1][mb], acc[nb][mb]);
         }
@@ -324,10 +342,10 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
         const int m = m0 + 64 * wm + 32 * mb + l32;
         if (m >= g.M) continue;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int n = n0 + 64 * wn + 32 * nb + 8 * q + 4 * h;
+                const int n = n0 + (BN / 2) * wn + 32 * nb + 8 * q + 4 * h;
                 float4v v;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = (float)(half_t)pin(alpha * acc[nb][mb][4 * q + i]);
@@ -364,6 +382,11 @@ extern "C" int g4a_srqh(int n, const float* a, float a_in_q, void* out_f16, void
     return G4A_OK;
 }
 
+// launches whose 128 x 128 tiles number fewer than this run on 128 x 64 tiles (two per CU):
+// below two tiles per CU the narrower tiles finish sooner (decoder prefill at M 1024: the
+// N 1536 products 30.9 -> 26.7 us, the whole prompt 11.9 -> 10.9 ms)
+constexpr long kGemmNarrowBelow = 512;
+
 extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream) {
     if (M <= 0 || K <= 0 || K % 64) {
         set_error("M (%d) must be positive and K (%d) a positive multiple of 64", M, K);
@@ -383,6 +406,10 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
     g.K = K;
     g.mtiles = (M + 127) / 128;
     g.n_mats = n_mats;
+    // 64-wide output tiles when 128-wide ones would leave CUs without a tile
+    long tiles128 = 0;
+    for (int i = 0; i < n_mats; ++i) tiles128 += (long)(mats[i].n / 128) * g.mtiles;
+    const int BN = tiles128 < kGemmNarrowBelow ? 64 : 128;
     int tiles = 0;
     for (int i = 0; i < 3; ++i) {
         const g4a_gemm_mat* m = i < n_mats ? &mats[i] : nullptr;
@@ -393,17 +420,20 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
                           "within 32-bit offsets, out_q >= 0", i, m->n);
                 return G4A_EINVAL;
             }
-            tiles += (m->n / 128) * g.mtiles;
+            tiles += (m->n / BN) * g.mtiles;
         }
         g.w[i] = m ? reinterpret_cast<const half_t*>(m->w_f16) : nullptr;
         g.out[i] = m ? m->out : nullptr;
-        g.n[i] = m ? m->n : 128;
+        g.n[i] = m ? m->n : BN;
         g.out_f32[i] = m ? m->out_f32 : 0;
         g.out_q[i] = m ? m->out_q : 0.0f;
         g.alpha[i] = m && m->alpha != 0.0f ? m->alpha : 1.0f;
         g.tile_end[i] = tiles;
     }
-    hipLaunchKernelGGL(gemm16_kernel<64>, dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    if (BN == 64)
+        hipLaunchKernelGGL((gemm16_kernel<64, 64>), dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    else
+        hipLaunchKernelGGL((gemm16_kernel<64, 128>), dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "gemm16 launch");
     return G4A_OK;

@@ -208,10 +208,13 @@ def test_proj_gemm_matches_oracle(M, N, K):
 
 
 @pytest.mark.parametrize("M,K,ns", [(1024, 1536, (2048, 512, 512)), (200, 1536, (256,)),
-                                    (1, 64, (128, 128)), (129, 192, (384, 128, 256))])
+                                    (1, 64, (128, 128)), (129, 192, (384, 128, 256)),
+                                    (1024, 768, (4096, 4096))])
 def test_gemm16_grouped_matches_oracle(M, K, ns):
     """g4a_gemm16: up to three products over one f16 A in one launch, each f16 (gemm_tiled)
-    or f32 srq'd (srq_b); ragged M (rows past M read as zeros, nothing stored past M)."""
+    or f32 srq'd (srq_b); ragged M (rows past M read as zeros, nothing stored past M).
+    The last case has 512 tiles of 128 x 128 and runs on them; the others have fewer and run
+    on 128 x 64 tiles."""
     rng = np.random.default_rng(M + K + len(ns))
     print(f"gemm16 M {M} K {K} n {ns}", flush=True)
     a = rng.standard_normal((M, K)).astype(np.float32)
