@@ -241,6 +241,27 @@ typedef struct {
 int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream);
 
 /*
+ * g4a_gemm16 with a workspace, which lets a launch with too few output tiles to fill the
+ * GPU (the N 1536 products of the decoder prefill, the narrow per-layer-embedding gate)
+ * split K over several workgroups per tile. Replaces the same dispatches as g4a_gemm16
+ * (gemm_tiled, kernels_dsl.py:34-136, from PrefillGPU._gemm / _gemm_dsl, prefill_gpu.py:151-184);
+ * the workspace plays the part of the scratch PrefillGPU sizes per prompt (_alloc_acts,
+ * prefill_gpu.py:229-256).
+ * Each split's f32 partial tile goes to the workspace and the tile's last workgroup adds them
+ * in split order, so the result is deterministic and each output is still f16(alpha * sum)
+ * of one f32 sum (its terms grouped by K range). ws: device memory of at least
+ * g4a_gemm16_ws_bytes(...) bytes (0: the launch does not split, ws may be NULL), 256-byte
+ * aligned; its first G4A_GEMM_TICKET_BYTES bytes are per-tile tickets that must be zero before
+ * the first call on it (every call leaves them zero), the rest needs no initialisation. Calls
+ * that may run concurrently need separate workspaces. Returns G4A_EWORKSPACE if ws_bytes is
+ * short.
+ */
+#define G4A_GEMM_TICKET_BYTES 2048
+size_t g4a_gemm16_ws_bytes(int M, int K, int n_mats, const g4a_gemm_mat* mats);
+int g4a_gemm16_ws(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* ws,
+                  size_t ws_bytes, void* stream);
+
+/*
  * ---- The rest of a decode step: the decoder layer around the attention block ---------
  * One token's layer (gemma4_150/reference.py:141-191) is, with x f32 [H]:
  *   a = srq(rms(x, in_norm), qkv_in)        g4a_rms_norm (out2, sum2)     rmssrq_69

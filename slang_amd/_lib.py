@@ -29,10 +29,14 @@ EXPORTS = (
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
     "g4a_dequant", "g4a_qkv_gemv", "g4a_qkv_gemv_norm", "g4a_srqh", "g4a_gemm16",
+    "g4a_gemm16_ws_bytes", "g4a_gemm16_ws",
     "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
     "g4a_embed", "g4a_embed_rows", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
     "g4a_rows_tail", "g4a_geglu16", "g4a_plegate16",
 )
+
+# g4a_gemm16_ws: the workspace's leading ticket words (g4attn.h)
+GEMM_TICKET_BYTES = 2048
 
 # g4a_rows_tail modes (g4attn.h)
 TAIL_NONE, TAIL_SRQ, TAIL_NORM, TAIL_NORM16 = 0, 1, 2, 3
@@ -139,6 +143,10 @@ def load() -> ctypes.CDLL:
     lib.g4a_srqh.argtypes = [i, P, f, P, P]
     lib.g4a_gemm16.restype = ctypes.c_int
     lib.g4a_gemm16.argtypes = [i, i, P, i, ctypes.POINTER(G4AGemmMat), P]
+    lib.g4a_gemm16_ws_bytes.restype = ctypes.c_size_t
+    lib.g4a_gemm16_ws_bytes.argtypes = [i, i, i, ctypes.POINTER(G4AGemmMat)]
+    lib.g4a_gemm16_ws.restype = ctypes.c_int
+    lib.g4a_gemm16_ws.argtypes = [i, i, P, i, ctypes.POINTER(G4AGemmMat), P, ctypes.c_size_t, P]
     lib.g4a_qgemv.restype = ctypes.c_int
     lib.g4a_qgemv.argtypes = [i, i, i, P, f, P, P, f, P, P]
     lib.g4a_gemv_f16.restype = ctypes.c_int

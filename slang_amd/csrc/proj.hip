@@ -23,6 +23,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace g4a {
@@ -216,14 +218,20 @@ __global__ __launch_bounds__(256) void srqh_kernel(const float* __restrict__ a, 
 }
 
 // Grouped f16 GEMM: up to three products out_p = A . W_p^T sharing A (the q, k and v
-// projections of one layer in one launch). Tiles of 128 tokens x 128 outputs, 64-deep k
+// projections of one layer in one launch). Tiles of 128 tokens x BN outputs, 64-deep k
 // stages DMA'd straight from HBM into LDS (buffer_load ... lds, 1 KiB per wave
-// instruction), four stages in flight so the loads of three stages hide the memory
-// latency behind the MFMAs of the fourth. LDS rows are 128 B (64 halves, 8 chunks of
-// 16 B); chunk c of row r sits at c ^ ((r >> 1) & 7), so the 16 rows of a quarter-wave
-// operand read fall in 16 distinct bank groups. Each wave owns 64 x 64 of the tile as 2x2
-// v_mfma_f32_32x32x16_f16 blocks computed transposed (D^T = W . A^T) so a lane holds 4
-// consecutive outputs of one token and stores them in one instruction.
+// instruction), STAGES - 1 stages in flight while the MFMAs run on the oldest. LDS rows are
+// 128 B (64 halves, 8 chunks of 16 B); chunk c of row r sits at c ^ ((r >> 1) & 7), so the
+// 16 rows of a quarter-wave operand read fall in 16 distinct bank groups. Waves compute
+// v_mfma_f32_32x32x16_f16 blocks transposed (D^T = W . A^T) so a lane holds 4 consecutive
+// outputs of one token and stores them in one instruction.
+//
+// Split k: with a workspace, launches with too few tiles to fill the GPU cut k into
+// `splits` ranges, one workgroup each. Every workgroup stores its f32 partial tile
+// device-coherently, waits for the stores and takes the tile's ticket (a relaxed agent-scope
+// atomic); the last of the tile's workgroups to take it adds the partials in split order
+// (p0 + p1 + ..., whichever workgroup that is, so the result does not depend on arrival
+// order), resets the ticket to zero for the next call and runs the epilogue.
 struct Gemm16Args {
     const half_t* a;  // [M][K] f16
     int M, K, mtiles, n_mats;
@@ -231,18 +239,24 @@ struct Gemm16Args {
     void* out[3];        // [M][N_p] f16, or f32 (srq'd with out_q) when out_f32
     int n[3], out_f32[3];
     float out_q[3], alpha[3];
-    int tile_end[3];  // cumulative tiles (n_p / 128) * mtiles
+    int tile_end[3];  // cumulative tiles (n_p / BN) * mtiles
+    int tiles, splits;
+    unsigned* ticket;  // [tiles], zero between calls
+    float* part;       // [tiles][splits][NB * 8][256] float4: the f32 partial tiles
 };
+
+constexpr int kCpolSC1 = 16;  // device scope: the access bypasses the per-XCD caches
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 
 // BN = 64 (outputs per tile) halves the tile for products too narrow to fill the GPU with
 // 128 x 128 tiles (N 1536 at M 1024 gives 96 of them for 256 CUs): each wave then covers 32
-// outputs x 64 tokens, reading one W block for two MFMAs, and three stages (72 KiB of LDS)
-// let two workgroups share a CU.
-template <int BK, int BN>
+// outputs x 64 tokens, reading one W block for two MFMAs.
+template <int BK, int BN, int STAGES, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
+    static_assert(STAGES >= 2 && STAGES <= 6, "2 to 6 stages");
     constexpr int BM = 128, ROWB = BK * 2;
     constexpr int OPBW = BN * ROWB, OPBA = BM * ROWB;  // operand tile bytes (W, A)
-    constexpr int STAGES = BN == 64 ? 3 : 4, STAGEB = OPBW + OPBA;  // 72 / 128 KiB: 2 / 1 per CU
+    constexpr int STAGEB = OPBW + OPBA;
     constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;           // rows per 1 KiB wave instruction
     constexpr int WROWS = BN / 4;           // W rows each wave moves per stage
@@ -258,33 +272,35 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     const int wn = wave & 1, wm = wave >> 1;
     const int l32 = lane & 31, h = lane >> 5;
 
-    // ---- this workgroup's matrix and tile: tiles of one matrix run m-tile-major, so
-    // neighbouring workgroups share the rows of W they stream
-    int p = 0, t = blockIdx.x;
+    // ---- this workgroup's k range, matrix and tile: tiles of one matrix run m-tile-major,
+    // so neighbouring workgroups share the rows of A they stream
+    const int split = blockIdx.x / g.tiles, tile = blockIdx.x % g.tiles;
+    int p = 0, t = tile;
     if (t >= g.tile_end[0]) p = t >= g.tile_end[1] ? 2 : 1;
     if (p > 0) t -= g.tile_end[p - 1];
     const int ntiles = g.n[p] / BN;
     const int n0 = (t % ntiles) * BN, m0 = (t / ntiles) * BM;
-    const int K = g.K, nk = K / BK;
+    const int K = g.K, nkall = K / BK;
+    const int kt0 = split * nkall / g.splits, nk = (split + 1) * nkall / g.splits - kt0;
 
     const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * K * 2);  // token rows >= M read as zeros
     const rsrc_t rw = make_rsrc(g.w[p], (uint32_t)g.n[p] * K * 2);
     // wave w moves W rows WROWS w .. and A rows 32w .. 32w+31, RPI rows (1 KiB) per instruction
-    auto issue = [&](int kt) {
-        char* st = lds + (kt % STAGES) * STAGEB;
-        const int kb = kt * BK * 2;
+    auto issue = [&](int i) {  // stage i of this range = k-step kt0 + i
+        char* st = lds + (i % STAGES) * STAGEB;
+        const int kb = (kt0 + i) * BK * 2;
 #pragma unroll
-        for (int i = 0; i < IPOW; ++i) {
-            const int r = WROWS * wave + RPI * i + lane / CPR;
+        for (int j = 0; j < IPOW; ++j) {
+            const int r = WROWS * wave + RPI * j + lane / CPR;
             const int c = (lane % CPR) ^ swz(r);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (WROWS * wave + RPI * i) * ROWB),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (WROWS * wave + RPI * j) * ROWB),
                                                      16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < IPOA; ++i) {
-            const int r = 32 * wave + RPI * i + lane / CPR;
+        for (int j = 0; j < IPOA; ++j) {
+            const int r = 32 * wave + RPI * j + lane / CPR;
             const int c = (lane % CPR) ^ swz(r);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPBW + (32 * wave + RPI * i) * ROWB),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(st + OPBW + (32 * wave + RPI * j) * ROWB),
                                                      16, (m0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
     };
@@ -293,17 +309,22 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb][0] = acc[nb][1] = float16v{};
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nk) issue(s);
-    for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed once at most the IPS instructions of each later stage remain
-        const int later = min(STAGES - 2, nk - 1 - kt);
-        if (later >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPS) : "memory");
-        else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS) : "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // every wave's part of stage kt; stage kt - 1 fully consumed
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-        const char* wl = lds + (kt % STAGES) * STAGEB;
+    for (int i = 0; i < STAGES - 1; ++i)
+        if (i < nk) issue(i);
+    for (int i = 0; i < nk; ++i) {
+        // stage i has landed once at most the IPS instructions of each later stage remain
+        const int later = min(STAGES - 2, nk - 1 - i);
+        static_assert((STAGES - 2) * IPS < 64, "vmcnt holds 6 bits");
+        switch (later) {
+            case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * IPS) : "memory"); break;
+            case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * IPS) : "memory"); break;
+            case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPS) : "memory"); break;
+            case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS) : "memory"); break;
+            default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();  // every wave's part of stage i; stage i - 1 fully consumed
+        if (i + STAGES - 1 < nk) issue(i + STAGES - 1);
+        const char* wl = lds + (i % STAGES) * STAGEB;
         const char* al = wl + OPBW;
         // lane (l32, h) holds k 16s + 8h .. +7 of k-step s; the operands of step s + 1 are
         // read while the MFMAs of step s run (one wave per SIMD hides no LDS latency itself)
@@ -329,6 +350,59 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = proj_mfma32(wo[s & 1][nb], ao[s & 1][mb], acc[nb][mb]);
         }
+    }
+
+    if constexpr (SPLIT) {
+        // publish this split's partial: float4 v of thread tid at [tile][split][v][tid]
+        constexpr int NV = NB * 8;
+        const size_t tbytes = (size_t)g.splits * NV * 256 * 16;
+        const rsrc_t rp = make_rsrc(reinterpret_cast<char*>(g.part) + tile * tbytes, (uint32_t)tbytes);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int v = (nb * 2 + mb) * 4 + q;
+                    const float4v x{acc[nb][mb][4 * q], acc[nb][mb][4 * q + 1], acc[nb][mb][4 * q + 2], acc[nb][mb][4 * q + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, x), rp, ((split * NV + v) * 256 + tid) * 16, 0, kCpolSC1);
+                }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
+        __shared__ int s_last;
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned old = __hip_atomic_fetch_add(g.ticket + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = old == (unsigned)g.splits - 1;
+            if (last) __hip_atomic_store(g.ticket + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        // the sum in split order, this workgroup's own partial from its registers
+        float16v sum[NB][2];
+        for (int j = 0; j < g.splits; ++j) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    float16v x;
+                    if (j == split) {
+                        x = acc[nb][mb];
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int v = (nb * 2 + mb) * 4 + q;
+                            const float4v y = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                              rp, ((j * NV + v) * 256 + tid) * 16, 0, kCpolSC1));
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) x[4 * q + e] = y[e];
+                        }
+                    }
+                    sum[nb][mb] = j == 0 ? x : sum[nb][mb] + x;
+                }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb][0] = sum[nb][0], acc[nb][1] = sum[nb][1];
     }
 
     // D^T[n][m]: acc[r] is output n = 8(r/4) + 4h + r%4, token m = l32 of the 32x32 block;
@@ -386,8 +460,25 @@ extern "C" int g4a_srqh(int n, const float* a, float a_in_q, void* out_f16, void
 // below two tiles per CU the narrower tiles finish sooner (decoder prefill at M 1024: the
 // N 1536 products 30.9 -> 26.7 us, the whole prompt 11.9 -> 10.9 ms)
 constexpr long kGemmNarrowBelow = 512;
+// with a workspace, launches of fewer 128 x 64 tiles than CUs (kSplitBelow) split k so that
+// about kSplitTarget workgroups run, three a CU (two-stage tiles, 48 KiB of LDS), each over
+// at least kSplitMinSteps k-steps. Measured at M 1024 against the unsplit launch: down
+// (K 6144, N 1536) 74 -> 42 us, o_proj (K 2048 / 4096) 23.4 -> 19.9 / 50 -> 31 us, the
+// per-layer-embedding gate (N 256) 16.2 -> 12.4 us; splitting the 320-tile q/k/v launch
+// lost (22 -> 25 us), hence the bound.
+constexpr int kSplitBelow = 256, kSplitTarget = 768, kSplitMinSteps = 4, kSplitStages = 2;
+// the workspace starts with a ticket word for every tile a split launch can have, so ticket
+// words never hold partials of another call
+constexpr size_t kTicketBytes = G4A_GEMM_TICKET_BYTES;
+static_assert(kSplitBelow * 4 <= kTicketBytes, "a ticket word per split tile");
 
-extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream) {
+namespace {
+struct GemmPlan {
+    int BN, tiles, splits;
+    size_t ws_bytes;  // tickets + partials, 0 without a split
+};
+
+int gemm_check(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats) {
     if (M <= 0 || K <= 0 || K % 64) {
         set_error("M (%d) must be positive and K (%d) a positive multiple of 64", M, K);
         return G4A_EINVAL;
@@ -400,43 +491,98 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
         set_error("a must be non-NULL, 16-byte aligned and within 32-bit buffer offsets");
         return G4A_EINVAL;
     }
+    for (int i = 0; i < n_mats; ++i) {
+        const g4a_gemm_mat* m = &mats[i];
+        if (m->n <= 0 || m->n % 128 || !m->w_f16 || !m->out || (((uintptr_t)m->w_f16 | (uintptr_t)m->out) & 15) ||
+            (int64_t)m->n * K * 2 > 0x7fffffff || (int64_t)M * m->n > 0x7fffffff || !(m->out_q >= 0.0f)) {
+            set_error("matrix %d: n (%d) a positive multiple of 128, w/out non-NULL and 16-byte aligned, "
+                      "within 32-bit offsets, out_q >= 0", i, m->n);
+            return G4A_EINVAL;
+        }
+    }
+    return G4A_OK;
+}
+
+GemmPlan gemm_plan(int M, int K, int n_mats, const g4a_gemm_mat* mats, bool may_split) {
+    const int mtiles = (M + 127) / 128;
+    long tiles128 = 0;
+    for (int i = 0; i < n_mats; ++i) tiles128 += (long)(mats[i].n / 128) * mtiles;
+    GemmPlan pl;
+    pl.BN = tiles128 < kGemmNarrowBelow ? 64 : 128;  // 64-wide tiles when 128-wide ones leave CUs idle
+    pl.tiles = 0;
+    for (int i = 0; i < n_mats; ++i) pl.tiles += (mats[i].n / pl.BN) * mtiles;
+    pl.splits = 1;
+    if (may_split && pl.BN == 64 && pl.tiles < kSplitBelow)
+        pl.splits = std::max(1, std::min(K / 64 / kSplitMinSteps, kSplitTarget / pl.tiles));
+    pl.ws_bytes = pl.splits > 1 ? kTicketBytes + (size_t)pl.tiles * pl.splits * (pl.BN / 64) * 8 * 256 * 16 : 0;
+    return pl;
+}
+
+int gemm_run(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* ws, size_t ws_bytes,
+             void* stream) {
+    const int rc = gemm_check(M, K, a_f16, n_mats, mats);
+    if (rc != G4A_OK) return rc;
+    GemmPlan pl = gemm_plan(M, K, n_mats, mats, ws != nullptr);
+    if (pl.splits > 1 && ws_bytes < pl.ws_bytes) {
+        set_error("workspace of %zu bytes, this product needs %zu (g4a_gemm16_ws_bytes)", ws_bytes, pl.ws_bytes);
+        return G4A_EWORKSPACE;
+    }
+    if (pl.splits > 1 && ((uintptr_t)ws & 255)) {
+        set_error("the workspace must be 256-byte aligned");
+        return G4A_EINVAL;
+    }
     Gemm16Args g;
     g.a = reinterpret_cast<const half_t*>(a_f16);
     g.M = M;
     g.K = K;
     g.mtiles = (M + 127) / 128;
     g.n_mats = n_mats;
-    // 64-wide output tiles when 128-wide ones would leave CUs without a tile
-    long tiles128 = 0;
-    for (int i = 0; i < n_mats; ++i) tiles128 += (long)(mats[i].n / 128) * g.mtiles;
-    const int BN = tiles128 < kGemmNarrowBelow ? 64 : 128;
     int tiles = 0;
     for (int i = 0; i < 3; ++i) {
         const g4a_gemm_mat* m = i < n_mats ? &mats[i] : nullptr;
-        if (m) {
-            if (m->n <= 0 || m->n % 128 || !m->w_f16 || !m->out || (((uintptr_t)m->w_f16 | (uintptr_t)m->out) & 15) ||
-                (int64_t)m->n * K * 2 > 0x7fffffff || (int64_t)M * m->n > 0x7fffffff || !(m->out_q >= 0.0f)) {
-                set_error("matrix %d: n (%d) a positive multiple of 128, w/out non-NULL and 16-byte aligned, "
-                          "within 32-bit offsets, out_q >= 0", i, m->n);
-                return G4A_EINVAL;
-            }
-            tiles += (m->n / BN) * g.mtiles;
-        }
+        if (m) tiles += (m->n / pl.BN) * g.mtiles;
         g.w[i] = m ? reinterpret_cast<const half_t*>(m->w_f16) : nullptr;
         g.out[i] = m ? m->out : nullptr;
-        g.n[i] = m ? m->n : BN;
+        g.n[i] = m ? m->n : pl.BN;
         g.out_f32[i] = m ? m->out_f32 : 0;
         g.out_q[i] = m ? m->out_q : 0.0f;
         g.alpha[i] = m && m->alpha != 0.0f ? m->alpha : 1.0f;
         g.tile_end[i] = tiles;
     }
-    if (BN == 64)
-        hipLaunchKernelGGL((gemm16_kernel<64, 64>), dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+    g.tiles = tiles;
+    g.splits = pl.splits;
+    g.ticket = pl.splits > 1 ? reinterpret_cast<unsigned*>(ws) : nullptr;
+    g.part = pl.splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kTicketBytes) : nullptr;
+    const dim3 grid(tiles * pl.splits);
+    // LDS 48 / 72 / 64 KiB a workgroup: three / two / two a CU (the 128-wide tiles measured
+    // 76 -> 58 us for the decoder's gate/up product with two stages, two a CU, against four
+    // stages, one a CU)
+    if (pl.splits > 1)
+        hipLaunchKernelGGL((gemm16_kernel<64, 64, kSplitStages, true>), grid, dim3(256), 0, (hipStream_t)stream, g);
+    else if (pl.BN == 64)
+        hipLaunchKernelGGL((gemm16_kernel<64, 64, 3, false>), grid, dim3(256), 0, (hipStream_t)stream, g);
     else
-        hipLaunchKernelGGL((gemm16_kernel<64, 128>), dim3(tiles), dim3(256), 0, (hipStream_t)stream, g);
+        hipLaunchKernelGGL((gemm16_kernel<64, 128, 2, false>), grid, dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "gemm16 launch");
     return G4A_OK;
+}
+}  // namespace
+
+extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream) {
+    return gemm_run(M, K, a_f16, n_mats, mats, nullptr, 0, stream);
+}
+
+extern "C" size_t g4a_gemm16_ws_bytes(int M, int K, int n_mats, const g4a_gemm_mat* mats) {
+    if (M <= 0 || K <= 0 || K % 64 || n_mats < 1 || n_mats > 3 || !mats) return 0;
+    for (int i = 0; i < n_mats; ++i)
+        if (mats[i].n <= 0 || mats[i].n % 128) return 0;
+    return gemm_plan(M, K, n_mats, mats, true).ws_bytes;
+}
+
+extern "C" int g4a_gemm16_ws(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* ws,
+                             size_t ws_bytes, void* stream) {
+    return gemm_run(M, K, a_f16, n_mats, mats, ws, ws_bytes, stream);
 }
 
 extern "C" int g4a_dequant(int bits, int n_in, int n_out, const uint32_t* w_bits, const float* w_scale,

@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
-from .projection import dequant, gemm16, packed_bits, srqh
+from .projection import GemmWorkspace, dequant, gemm16, packed_bits, srqh
 
 __all__ = ["qgemv", "norm_in", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
            "embed_rows", "rows_tail", "geglu16", "plegate16", "DecoderStack", "EPS"]
@@ -432,7 +432,8 @@ class DecoderStack:
         embed_rows(self.embed_q, tid, self.embed_sc, H, 2, H, self.embed_scale, out=hid)
         a16 = take("a16", S, H)
         srqh(hid, 0.0, out=a16)
-        gemm16(a16, [(self.pl_proj, ctx, 0.0)])       # f32(f16(h . P^T)): srq_b with step 0
+        gws = self.attn.gemm_ws
+        gemm16(a16, [(self.pl_proj, ctx, 0.0)], gws)  # f32(f16(h . P^T)): srq_b with step 0
         embed_rows(self.ple_q, tid, self.ple_sc, nL * d, 4, d, self.ple_scale, out=plegath)
         rms_norm(ctx.view(S * nL, d), self.pl_norm, res=plegath.view(S * nL, d), pre=H ** -0.5,
                  mult=2.0 ** -0.5, out=ple.view(S * nL, d))    # combine_b
@@ -449,28 +450,28 @@ class DecoderStack:
                                            trace=t).view(S, s.q_dim)
             snap(t, "attn", attn)
             o16, y2 = take("o16", S, H), take("y2", S, H)
-            gemm16(attn, [(wd["o"], o16, None)])
+            gemm16(attn, [(wd["o"], o16, None)], gws)
             rows_tail(hid, o16, x_q=sc["o_out"], w1=w["o_w1"], mode=_lib.TAIL_NORM16, w2=w["o_w2"],
                       q2=sc["gate_in"], y16=y2)
             snap(t, "o16", o16)
             snap(t, "x1", hid)
             snap(t, "y2", y2)
             g16, u16, gg = take("g16", S, it), take("u16", S, it), take("gg16", S, it)
-            gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)])
+            gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)], gws)
             geglu16(g16, u16, sc["gate_out"], sc["up_out"], sc["down_in"], out=gg)
             snap(t, "g16", g16)
             snap(t, "u16", u16)
             snap(t, "gg16", gg)
             d16, hh = take("d16", S, H), take("hh", S, H)
-            gemm16(gg, [(wd["down"], d16, None, sc["down_in"])])
+            gemm16(gg, [(wd["down"], d16, None, sc["down_in"])], gws)
             rows_tail(hid, d16, x_q=sc["down_out"], w1=w["down_nw"], mode=_lib.TAIL_SRQ, q2=sc["plegate_in"], y16=hh)
             snap(t, "d16", d16)
             snap(t, "x2", hid)
             snap(t, "hh", hh)
             plin, gph, pp = take("plin", S, d), take("gph", S, d), take("pp16", S, H)
-            gemm16(hh, [(wd["plegate"], plin, None)])
+            gemm16(hh, [(wd["plegate"], plin, None)], gws)
             plegate16(plin, sc["plegate_out"], ple[:, L], nL * d, sc["pleproj_in"], out=gph)
-            gemm16(gph, [(wd["pleproj"], pp, None)])
+            gemm16(gph, [(wd["pleproj"], pp, None)], gws)
             snap(t, "plin", plin)
             snap(t, "gph", gph)
             snap(t, "pp16", pp)

@@ -251,6 +251,7 @@ class AttentionStack:
                 self.rope[key] = A.rope_tables(np.arange(self.max_seq), hd, theta, cutoff, device=device)
         self.dq = {}  # dequantised f16 weights for prefill, made on first use per layer
         self.ws = A.DecodeWorkspace(device)
+        self.gemm_ws = P.GemmWorkspace(device)  # the K split of the prefill GEMMs
 
     def caches(self, L: int):
         src = self.man.layers[L].kv_source
@@ -318,9 +319,10 @@ class AttentionStack:
                 kraw = torch.empty(S, wk.shape[0], device=a.device, dtype=torch.float16)
                 vraw = torch.empty(S, wv.shape[0], device=a.device, dtype=torch.float16)
                 mats += [(wk, kraw, None), (wv, vraw, None)]
-            P.gemm16(a, mats)
+            P.gemm16(a, mats, self.gemm_ws)
         else:
-            q, kraw, vraw = P.prefill_qkv(a, wq, wk, wv, a_in_q=sc.get("qkv_in", 0.0), q_out=sc.get("q_out", 0.0))
+            q, kraw, vraw = P.prefill_qkv(a, wq, wk, wv, a_in_q=sc.get("qkv_in", 0.0), q_out=sc.get("q_out", 0.0),
+                                          workspace=self.gemm_ws)
         if trace is not None:
             trace.update(q=q.clone(), kraw=None if kraw is None else kraw.clone(),
                          vraw=None if vraw is None else vraw.clone())

@@ -20,7 +20,8 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 
-__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "prefill_qkv", "packed_bits"]
+__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "GemmWorkspace", "prefill_qkv",
+           "packed_bits"]
 
 _WORDS = (torch.int32, torch.uint32)
 
@@ -153,11 +154,22 @@ def srqh(a, a_in_q: float = 0.0, out=None):
     return out
 
 
-def gemm16(a16, mats):
-    """Up to three products sharing the f16 activation a16 [M][K], one launch (g4a_gemm16).
+class GemmWorkspace:
+    """Scratch of ``gemm16(..., workspace=)``: per-tile tickets (zero between calls; a new
+    buffer is allocated zeroed, and every call leaves them zero) and the f32 partial tiles of
+    the K split. Grows on demand. Calls that may run concurrently need separate workspaces."""
 
-    mats: sequence of (w_f16 [N][K], out, out_q or None[, alpha]); out f16 [M][N] gets the f16
-    GEMM result f16(alpha * sum) (gemm_tiled), out f32 [M][N] gets srq(f32(that), out_q) (srq_b)."""
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, _lib.GEMM_TICKET_BYTES), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def _gemm_table(a16, mats):
     _need(a16, "a16", torch.float16)
     M, K = a16.shape
     if not 1 <= len(mats) <= 3:
@@ -174,22 +186,41 @@ def gemm16(a16, mats):
             raise ValueError("out must hold M*N values")
         tab[i] = _lib.G4AGemmMat(w.data_ptr(), out.data_ptr(), w.shape[0], int(out.dtype == torch.float32),
                                  float(oq or 0.0), alpha)
-    check(_lib.load().g4a_gemm16(M, K, _ptr(a16), len(mats), tab, _stream()))
+    return M, K, tab
 
 
-def prefill_qkv(a, wq_f16, wk_f16=None, wv_f16=None, a_in_q: float = 0.0, q_out: float = 0.0):
+def gemm16(a16, mats, workspace: GemmWorkspace | None = None):
+    """Up to three products sharing the f16 activation a16 [M][K], one launch (g4a_gemm16).
+
+    mats: sequence of (w_f16 [N][K], out, out_q or None[, alpha]); out f16 [M][N] gets the f16
+    GEMM result f16(alpha * sum) (gemm_tiled), out f32 [M][N] gets srq(f32(that), out_q) (srq_b).
+    With a workspace, launches with too few output tiles to fill the GPU split K
+    (g4a_gemm16_ws); the partial sums are added in a fixed order, so results are deterministic."""
+    M, K, tab = _gemm_table(a16, mats)
+    lib = _lib.load()
+    if workspace is None:
+        check(lib.g4a_gemm16(M, K, _ptr(a16), len(mats), tab, _stream()))
+        return
+    need = lib.g4a_gemm16_ws_bytes(M, K, len(mats), tab)
+    ws = workspace.get(need) if need else None
+    check(lib.g4a_gemm16_ws(M, K, _ptr(a16), len(mats), tab, _ptr(ws), ws.numel() if ws is not None else 0,
+                            _stream()))
+
+
+def prefill_qkv(a, wq_f16, wk_f16=None, wv_f16=None, a_in_q: float = 0.0, q_out: float = 0.0,
+                workspace: GemmWorkspace | None = None):
     """The q/k/v block of PrefillGPU._layer (prefill_gpu.py:327-342) over dequantised weights:
     q = srq_b(gemm(srqh_b(a), wq)) f32 [S][q_dim]; kraw, vraw = gemm(...) f16 [S][kv_dim]
     (None on KV-sharing layers), ready for kvnorm_b. srqh_b runs once for the three GEMMs,
-    which run as one launch."""
+    which run as one launch (split over K with a workspace, as gemm16)."""
     S = a.shape[0]
     a16 = srqh(a, a_in_q)
     q = torch.empty(S, wq_f16.shape[0], device=a.device, dtype=torch.float32)
     mats = [(wq_f16, q, q_out)]
     if wk_f16 is None:
-        gemm16(a16, mats)
+        gemm16(a16, mats, workspace)
         return q, None, None
     k = torch.empty(S, wk_f16.shape[0], device=a.device, dtype=torch.float16)
     v = torch.empty(S, wv_f16.shape[0], device=a.device, dtype=torch.float16)
-    gemm16(a16, mats + [(wk_f16, k, None), (wv_f16, v, None)])
+    gemm16(a16, mats + [(wk_f16, k, None), (wv_f16, v, None)], workspace)
     return q, k, v

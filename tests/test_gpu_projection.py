@@ -253,3 +253,59 @@ def test_prefill_qkv_block():
         gemm_f16_close(got.cpu().numpy(), ref, nm)
     refq = P.proj_gemm(a_q, P.dequant_f16(ws[0][0], ws[0][1], H, qd, 4))
     srq_close(q.cpu().numpy(), refq.astype(np.float32), 0.03125, "q")
+
+
+@pytest.mark.parametrize("M,K,ns", [(1024, 6144, (1536,)), (1024, 2048, (1536,)), (1024, 1536, (256,)),
+                                    (200, 1536, (256,)), (512, 1536, (2048, 256, 256)), (77, 4096, (128, 384))])
+def test_gemm16_split_k_matches_oracle(M, K, ns):
+    """g4a_gemm16_ws: launches with few output tiles split K over several workgroups per tile
+    and add the f32 partials in split order. The outputs meet the same bounds as the unsplit
+    GEMM, a repeat call is bit-identical (the sum order does not depend on which workgroup
+    finishes last), rows past M are not stored, and the tickets are left at zero."""
+    rng = np.random.default_rng(M + K + 7 * len(ns))
+    print(f"gemm16 split M {M} K {K} n {ns}", flush=True)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    a16 = sa.srqh(t(a), 0.0625)
+    ws = [(words(rng, n * K // 8), (rng.random(n).astype(np.float32) * 0.01 + 0.02)) for n in ns]
+    w16 = [sa.dequant(dev_words(w), t(s), K, n) for (w, s), n in zip(ws, ns)]
+    alpha = 0.5
+    outs = [torch.full((M + 3, n), 7.0, device=DEV, dtype=torch.float32 if i == 0 else torch.float16)
+            for i, n in enumerate(ns)]
+    mats = [(w, o[:M], 0.03125 if i == 0 else None, 1.0 if i == 0 else alpha)
+            for i, (w, o) in enumerate(zip(w16, outs))]
+    gws = sa.GemmWorkspace()
+    _, _, tab = sa.projection._gemm_table(a16, mats)
+    need = sa._lib.load().g4a_gemm16_ws_bytes(M, K, len(ns), tab)
+    assert need > 0, "this shape should split K"
+    sa.gemm16(a16, mats, gws)
+    first = [o.clone() for o in outs]
+    sa.gemm16(a16, mats, gws)
+    torch.cuda.synchronize()
+    for o, f in zip(outs, first):
+        assert torch.equal(o, f), "a repeat call differs"
+    assert not gws.buf[:sa._lib.GEMM_TICKET_BYTES].any(), "tickets left non-zero"
+    a_q = P.srq(a, 0.0625)
+    for i, ((w, s), n, o) in enumerate(zip(ws, ns, outs)):
+        ref = P.proj_gemm(a_q, P.dequant_f16(w, s, K, n, 4))
+        got = o[:M].float().cpu().numpy()
+        if i == 0:
+            srq_close(got, ref.astype(np.float32), 0.03125, f"matrix {i} (q path)")
+        else:
+            ref = (alpha * ref.astype(np.float64)).astype(np.float16)  # f16(alpha * sum)
+            gemm_f16_close(got, ref, f"matrix {i}")
+        assert (o[M:] == 7.0).all(), "stores past M"
+
+
+def test_gemm16_split_k_workspace_checks():
+    """A workspace shorter than g4a_gemm16_ws_bytes is refused before anything runs."""
+    M, K, n = 1024, 2048, 1536
+    a16 = torch.zeros(M, K, device=DEV, dtype=torch.float16)
+    w = torch.zeros(n, K, device=DEV, dtype=torch.float16)
+    o = torch.zeros(M, n, device=DEV, dtype=torch.float16)
+    _, _, tab = sa.projection._gemm_table(a16, [(w, o, None)])
+    lib = sa._lib.load()
+    need = lib.g4a_gemm16_ws_bytes(M, K, 1, tab)
+    assert need > sa._lib.GEMM_TICKET_BYTES
+    short = torch.zeros(need - 256, device=DEV, dtype=torch.uint8)
+    rc = lib.g4a_gemm16_ws(M, K, a16.data_ptr(), 1, tab, short.data_ptr(), short.numel(), None)
+    assert rc == -3, "G4A_EWORKSPACE expected"
