@@ -40,13 +40,17 @@ _FLUSH = None
 
 
 def flush_mall():
-    """Evict the 256 MB MALL (Infinity Cache) and the L2s: read and write 1 GiB that no timed
-    call touches, so the first calls of a timed region find nothing of theirs cached."""
+    """Evict the 256 MB MALL (Infinity Cache) and the L2s: read 1 GiB that no timed call
+    touches, so the first calls of a timed region find nothing of theirs cached. The pass
+    only reads: a flush that also wrote the 1 GiB left dirty MALL lines whose write-back
+    then ran inside the timed region (the headline measured 20.6 us a call over 20 calls,
+    12.7 over 64, against 8.8 over 256)."""
     global _FLUSH
     if _FLUSH is None:
         _FLUSH = torch.empty(256 << 20, dtype=torch.float32, device="cuda")
         _FLUSH.fill_(0.0)
-    _FLUSH.add_(1.0)
+        torch.cuda.synchronize()
+    torch.sum(_FLUSH)
 
 
 def graph_time_ms(fn_list, steps, warmup, flush=True):
@@ -65,12 +69,11 @@ def graph_time_ms(fn_list, steps, warmup, flush=True):
             fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
     if EAGER:
-        if flush:
-            flush_mall()
-            torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
+            if flush:
+                flush_mall()
             ev0.record(stream)
             for i in range(steps):
                 fn_list[i % len(fn_list)]()
@@ -84,12 +87,15 @@ def graph_time_ms(fn_list, steps, warmup, flush=True):
     torch.cuda.synchronize()
     g.replay()                      # warm replay (untimed)
     torch.cuda.synchronize()
-    if flush:
-        flush_mall()
-        torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        # a second warm replay, the flush and the timed replay are queued back to back: the
+        # GPU does not idle (and drop its clocks) before the timed region, and the host
+        # launches the timed graph while the flush still runs, so the first call starts at ev0
+        g.replay()
+        if flush:
+            flush_mall()
         ev0.record(stream)
         g.replay()
         ev1.record(stream)
