@@ -456,10 +456,11 @@ extern "C" int g4a_srqh(int n, const float* a, float a_in_q, void* out_f16, void
     return G4A_OK;
 }
 
-// launches whose 128 x 128 tiles number fewer than this run on 128 x 64 tiles (two per CU):
-// below two tiles per CU the narrower tiles finish sooner (decoder prefill at M 1024: the
-// N 1536 products 30.9 -> 26.7 us, the whole prompt 11.9 -> 10.9 ms)
-constexpr long kGemmNarrowBelow = 512;
+// launches whose 128 x 128 tiles number fewer than the CUs run on 128 x 64 tiles: at M 1024
+// the N 1536 products (96 wide tiles) went 30.9 -> 26.7 us on them; with 256 or more wide
+// tiles (two a CU) the wide ones win (the E2B global layer's q/k/v, 288 wide tiles: 42.3 us
+// on 576 narrow ones, 28.2 us on the wide)
+constexpr long kGemmNarrowBelow = 256;
 // with a workspace, launches of fewer 128 x 64 tiles than CUs (kSplitBelow) split k so that
 // about kSplitTarget workgroups run, three a CU (two-stage tiles, 48 KiB of LDS), each over
 // at least kSplitMinSteps k-steps. Measured at M 1024 against the unsplit launch: down
