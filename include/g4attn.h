@@ -256,6 +256,18 @@ int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* 
  * that may run concurrently need separate workspaces. Returns G4A_EWORKSPACE if ws_bytes is
  * short.
  */
+/*
+ * The MLP's gate and up GEMMs and geglu_b in one launch: the two _gemm dispatches on the
+ * pre-FFN operand and the geglu_b dispatch after them (prefill_gpu.py:365-371; geglu_b,
+ * kernels_dsl.py:259-290). out f16 [M][n] = geglu_b's code of g = f16(A . w_gate^T) and
+ * u = f16(A . w_up^T): f16(clamp(round(gelu(srq(g, gate_q)) * srq(u, up_q) / out_q), -128,
+ * 127)), or f16(gelu(..) * ..) when out_q is 0 -- the same values as g4a_gemm16 on the two
+ * matrices followed by g4a_geglu16, without writing or reading g and u. w_gate and w_up are
+ * f16 [n][K]; K and n multiples of 64.
+ */
+int g4a_gemm16_geglu(int M, int K, const void* a_f16, const void* w_gate_f16, const void* w_up_f16, int n,
+                     float gate_q, float up_q, float out_q, void* out_f16, void* stream);
+
 #define G4A_GEMM_TICKET_BYTES 2048
 size_t g4a_gemm16_ws_bytes(int M, int K, int n_mats, const g4a_gemm_mat* mats);
 int g4a_gemm16_ws(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* ws,

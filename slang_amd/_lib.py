@@ -29,7 +29,7 @@ EXPORTS = (
     "g4a_prefill_ws_bytes", "g4a_prefill", "g4a_qprep",
     "g4a_kv_write",
     "g4a_dequant", "g4a_qkv_gemv", "g4a_qkv_gemv_norm", "g4a_srqh", "g4a_gemm16",
-    "g4a_gemm16_ws_bytes", "g4a_gemm16_ws",
+    "g4a_gemm16_ws_bytes", "g4a_gemm16_ws", "g4a_gemm16_geglu",
     "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
     "g4a_embed", "g4a_embed_rows", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
     "g4a_rows_tail", "g4a_geglu16", "g4a_plegate16",
@@ -147,6 +147,8 @@ def load() -> ctypes.CDLL:
     lib.g4a_gemm16_ws_bytes.argtypes = [i, i, i, ctypes.POINTER(G4AGemmMat)]
     lib.g4a_gemm16_ws.restype = ctypes.c_int
     lib.g4a_gemm16_ws.argtypes = [i, i, P, i, ctypes.POINTER(G4AGemmMat), P, ctypes.c_size_t, P]
+    lib.g4a_gemm16_geglu.restype = ctypes.c_int
+    lib.g4a_gemm16_geglu.argtypes = [i, i, P, P, P, i, f, f, f, P, P]
     lib.g4a_qgemv.restype = ctypes.c_int
     lib.g4a_qgemv.argtypes = [i, i, i, P, f, P, P, f, P, P]
     lib.g4a_gemv_f16.restype = ctypes.c_int

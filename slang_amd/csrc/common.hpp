@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "../../include/g4attn.h"
@@ -138,6 +139,21 @@ __device__ __forceinline__ float pin(float x) {
 __device__ __forceinline__ float srq(float x, float s) {
     if (s == 0.0f) return x;
     return pin(fminf(fmaxf(rintf(x / s), -128.0f), 127.0f) * s);  // an f32 product, as the reference's
+}
+
+// gelu with the tanh approximation (reference.py:34-35), 0.5 v (1 + tanh(c (v + 0.044715 v^3)))
+// with c = sqrt(2 / pi), in the equal form v / (1 + exp(-2 c (v + 0.044715 v^3))) since
+// 0.5 (1 + tanh(z)) = 1 / (1 + exp(-2z)): one hardware exp2 and a division instead of tanhf,
+// and no cancellation in 1 + tanh(z) where v is far below zero.
+__device__ __forceinline__ float gelu_tanh16(float v) {
+    const float z2 = -1.5957691216057308f * (v + 0.044715f * v * v * v);  // -2 c (..)
+    return v / (1.0f + __builtin_amdgcn_exp2f(z2 * 1.4426950408889634f));
+}
+// geglu_b's element (kernels_dsl.py:259-290) from the f16 gate and up products g, u:
+// y = gelu(srq(g, gq)) * srq(u, uq), stored as its code on oq's grid (f16(y) when oq is 0)
+__device__ __forceinline__ half_t geglu_code(float g, float u, float gq, float uq, float oq) {
+    const float y = pin(gelu_tanh16(srq(g, gq)) * srq(u, uq));
+    return oq == 0.0f ? (half_t)y : (half_t)fminf(fmaxf(rintf(y / oq), -128.0f), 127.0f);
 }
 
 // 8 consecutive cache elements as f32, from f16 (one 16 B load) or f32 (two 16 B loads).

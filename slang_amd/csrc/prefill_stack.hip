@@ -17,10 +17,6 @@
 
 namespace g4a {
 
-__device__ __forceinline__ float gelu_tanh16(float v) {
-    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-}
-
 __device__ __forceinline__ float row_sum(float v, float* red) {
     v = wave_sum(v);
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -174,10 +170,7 @@ __global__ __launch_bounds__(256) void geglu16_kernel(int n8, const half8* gate,
     const half8 g = gate[i], u = up[i];
     half8 o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float y = pin(gelu_tanh16(srq((float)g[j], gq)) * srq((float)u[j], uq));
-        o[j] = oq == 0.0f ? (half_t)y : (half_t)fminf(fmaxf(rintf(y / oq), -128.0f), 127.0f);
-    }
+    for (int j = 0; j < 8; ++j) o[j] = geglu_code((float)g[j], (float)u[j], gq, uq, oq);
     out[i] = o;
 }
 

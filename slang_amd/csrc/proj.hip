@@ -243,6 +243,7 @@ struct Gemm16Args {
     int tiles, splits;
     unsigned* ticket;  // [tiles], zero between calls
     float* part;       // [tiles][splits][NB * 8][256] float4: the f32 partial tiles
+    float gq, uq, oq;  // the gate/up form: geglu_b's steps
 };
 
 constexpr int kCpolSC1 = 16;  // device scope: the access bypasses the per-XCD caches
@@ -251,8 +252,14 @@ typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 // BN = 64 (outputs per tile) halves the tile for products too narrow to fill the GPU with
 // 128 x 128 tiles (N 1536 at M 1024 gives 96 of them for 256 CUs): each wave then covers 32
 // outputs x 64 tokens, reading one W block for two MFMAs.
-template <int BK, int BN, int STAGES, bool SPLIT>
+//
+// The gate/up form (GEGLU, BN 128): w[0] is the gate matrix, w[1] the up matrix, and a tile
+// covers 64 outputs of both: W rows 64 wn + 0..31 are gate rows and 64 wn + 32..63 the up
+// rows of the same 32 outputs, so a wave's two 32-output blocks hold gate and up for the same
+// (output, token) positions and the epilogue stores geglu_b's code of the two f16 products.
+template <int BK, int BN, int STAGES, bool SPLIT, bool GEGLU = false>
 __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
+    static_assert(!GEGLU || (BN == 128 && !SPLIT), "the gate/up form runs on 128-row tiles");
     static_assert(STAGES >= 2 && STAGES <= 6, "2 to 6 stages");
     constexpr int BM = 128, ROWB = BK * 2;
     constexpr int OPBW = BN * ROWB, OPBA = BM * ROWB;  // operand tile bytes (W, A)
@@ -278,13 +285,17 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     int p = 0, t = tile;
     if (t >= g.tile_end[0]) p = t >= g.tile_end[1] ? 2 : 1;
     if (p > 0) t -= g.tile_end[p - 1];
-    const int ntiles = g.n[p] / BN;
-    const int n0 = (t % ntiles) * BN, m0 = (t / ntiles) * BM;
+    constexpr int TN = GEGLU ? BN / 2 : BN;  // outputs a tile covers
+    const int ntiles = g.n[p] / TN;
+    const int n0 = (t % ntiles) * TN, m0 = (t / ntiles) * BM;
     const int K = g.K, nkall = K / BK;
     const int kt0 = split * nkall / g.splits, nk = (split + 1) * nkall / g.splits - kt0;
 
     const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.M * K * 2);  // token rows >= M read as zeros
-    const rsrc_t rw = make_rsrc(g.w[p], (uint32_t)g.n[p] * K * 2);
+    // the gate/up form: wave w moves gate rows (w even) or up rows (w odd) n0 + 32 (w / 2) ..
+    const int wsrc = GEGLU ? (wave & 1) : p;
+    const rsrc_t rw = make_rsrc(g.w[wsrc], (uint32_t)g.n[p] * K * 2);
+    const int wrow0 = GEGLU ? n0 + 32 * (wave >> 1) - WROWS * wave : n0;  // global row of tile row 0
     // wave w moves W rows WROWS w .. and A rows 32w .. 32w+31, RPI rows (1 KiB) per instruction
     auto issue = [&](int i) {  // stage i of this range = k-step kt0 + i
         char* st = lds + (i % STAGES) * STAGEB;
@@ -294,7 +305,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
             const int r = WROWS * wave + RPI * j + lane / CPR;
             const int c = (lane % CPR) ^ swz(r);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(st + (WROWS * wave + RPI * j) * ROWB),
-                                                     16, (n0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
+                                                     16, (wrow0 + r) * K * 2 + kb + 16 * c, 0, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < IPOA; ++j) {
@@ -411,6 +422,26 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     const int N = g.n[p];
     const bool f32 = g.out_f32[p] != 0;
     const float oq = g.out_q[p], alpha = g.alpha[p];
+    if constexpr (GEGLU) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int m = m0 + 64 * wm + 32 * mb + l32;
+            if (m >= g.M) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 32 * wn + 8 * q + 4 * h;
+                half4 y;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float gv = (float)(half_t)pin(alpha * acc[0][mb][4 * q + i]);
+                    const float uv = (float)(half_t)pin(alpha * acc[1][mb][4 * q + i]);
+                    y[i] = geglu_code(gv, uv, g.gq, g.uq, g.oq);
+                }
+                *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(g.out[0]) + (size_t)m * N + n) = y;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
         const int m = m0 + 64 * wm + 32 * mb + l32;
@@ -572,6 +603,45 @@ int gemm_run(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* ma
 
 extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* mats, void* stream) {
     return gemm_run(M, K, a_f16, n_mats, mats, nullptr, 0, stream);
+}
+
+extern "C" int g4a_gemm16_geglu(int M, int K, const void* a_f16, const void* w_gate_f16, const void* w_up_f16, int n,
+                                float gate_q, float up_q, float out_q, void* out_f16, void* stream) {
+    if (M <= 0 || K <= 0 || K % 64 || n <= 0 || n % 64) {
+        set_error("M (%d) positive, K (%d) a positive multiple of 64, n (%d) a positive multiple of 64", M, K, n);
+        return G4A_EINVAL;
+    }
+    if (!a_f16 || !w_gate_f16 || !w_up_f16 || !out_f16 ||
+        (((uintptr_t)a_f16 | (uintptr_t)w_gate_f16 | (uintptr_t)w_up_f16 | (uintptr_t)out_f16) & 15) ||
+        (int64_t)(M + 127) * K * 2 > 0x7fffffff || (int64_t)n * K * 2 > 0x7fffffff || (int64_t)M * n > 0x7fffffff) {
+        set_error("a, w_gate, w_up, out non-NULL, 16-byte aligned and within 32-bit offsets");
+        return G4A_EINVAL;
+    }
+    if (!(gate_q >= 0.0f) || !(up_q >= 0.0f) || !(out_q >= 0.0f)) {
+        set_error("gate_q, up_q and out_q must be >= 0");
+        return G4A_EINVAL;
+    }
+    Gemm16Args g = {};
+    g.a = reinterpret_cast<const half_t*>(a_f16);
+    g.M = M;
+    g.K = K;
+    g.mtiles = (M + 127) / 128;
+    g.n_mats = 1;
+    g.w[0] = reinterpret_cast<const half_t*>(w_gate_f16);
+    g.w[1] = reinterpret_cast<const half_t*>(w_up_f16);
+    g.out[0] = out_f16;
+    g.n[0] = n;
+    g.alpha[0] = 1.0f;
+    g.tiles = (n / 64) * g.mtiles;
+    g.tile_end[0] = g.tile_end[1] = g.tile_end[2] = g.tiles;
+    g.splits = 1;
+    g.gq = gate_q;
+    g.uq = up_q;
+    g.oq = out_q;
+    hipLaunchKernelGGL((gemm16_kernel<64, 128, 2, false, true>), dim3(g.tiles), dim3(256), 0, (hipStream_t)stream, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_error(e, "gemm16_geglu launch");
+    return G4A_OK;
 }
 
 extern "C" size_t g4a_gemm16_ws_bytes(int M, int K, int n_mats, const g4a_gemm_mat* mats) {

@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
-from .projection import GemmWorkspace, dequant, gemm16, packed_bits, srqh
+from .projection import GemmWorkspace, dequant, gemm16, gemm16_geglu, packed_bits, srqh
 
 __all__ = ["qgemv", "norm_in", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
            "embed_rows", "rows_tail", "geglu16", "plegate16", "DecoderStack", "EPS"]
@@ -456,11 +456,13 @@ class DecoderStack:
             snap(t, "o16", o16)
             snap(t, "x1", hid)
             snap(t, "y2", y2)
-            g16, u16, gg = take("g16", S, it), take("u16", S, it), take("gg16", S, it)
-            gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)], gws)
-            geglu16(g16, u16, sc["gate_out"], sc["up_out"], sc["down_in"], out=gg)
-            snap(t, "g16", g16)
-            snap(t, "u16", u16)
+            gg = take("gg16", S, it)
+            gemm16_geglu(y2, wd["gate"], wd["up"], sc["gate_out"], sc["up_out"], sc["down_in"], out=gg)
+            if t is not None:  # the two products on their own, for the stage checks
+                g16, u16 = take("g16", S, it), take("u16", S, it)
+                gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)], gws)
+                snap(t, "g16", g16)
+                snap(t, "u16", u16)
             snap(t, "gg16", gg)
             d16, hh = take("d16", S, H), take("hh", S, H)
             gemm16(gg, [(wd["down"], d16, None, sc["down_in"])], gws)

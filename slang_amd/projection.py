@@ -20,8 +20,8 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 
-__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "GemmWorkspace", "prefill_qkv",
-           "packed_bits"]
+__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "GemmWorkspace", "gemm16_geglu",
+           "prefill_qkv", "packed_bits"]
 
 _WORDS = (torch.int32, torch.uint32)
 
@@ -205,6 +205,27 @@ def gemm16(a16, mats, workspace: GemmWorkspace | None = None):
     ws = workspace.get(need) if need else None
     check(lib.g4a_gemm16_ws(M, K, _ptr(a16), len(mats), tab, _ptr(ws), ws.numel() if ws is not None else 0,
                             _stream()))
+
+
+def gemm16_geglu(a16, w_gate, w_up, gate_q: float, up_q: float, out_q: float, out=None):
+    """The MLP's gate and up GEMMs with geglu_b in one launch (g4a_gemm16_geglu;
+    prefill_gpu.py:365-371): f16 code of gelu(srq(f16(a.Wg^T), gate_q)) * srq(f16(a.Wu^T), up_q)
+    on out_q's grid, [M][n], the values gemm16 + geglu16 give."""
+    _need(a16, "a16", torch.float16)
+    _need(w_gate, "w_gate", torch.float16)
+    _need(w_up, "w_up", torch.float16)
+    M, K = a16.shape
+    n = w_gate.shape[0]
+    if tuple(w_gate.shape) != (n, K) or tuple(w_up.shape) != (n, K):
+        raise ValueError(f"w_gate {tuple(w_gate.shape)} and w_up {tuple(w_up.shape)} must both be [n][{K}]")
+    if out is None:
+        out = torch.empty(M, n, device=a16.device, dtype=torch.float16)
+    _need(out, "out", torch.float16)
+    if out.numel() != M * n:
+        raise ValueError("out must hold M*n values")
+    check(_lib.load().g4a_gemm16_geglu(M, K, _ptr(a16), _ptr(w_gate), _ptr(w_up), n, float(gate_q), float(up_q),
+                                       float(out_q), _ptr(out), _stream()))
+    return out
 
 
 def prefill_qkv(a, wq_f16, wk_f16=None, wv_f16=None, a_in_q: float = 0.0, q_out: float = 0.0,

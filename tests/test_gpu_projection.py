@@ -309,3 +309,38 @@ def test_gemm16_split_k_workspace_checks():
     short = torch.zeros(need - 256, device=DEV, dtype=torch.uint8)
     rc = lib.g4a_gemm16_ws(M, K, a16.data_ptr(), 1, tab, short.data_ptr(), short.numel(), None)
     assert rc == -3, "G4A_EWORKSPACE expected"
+
+
+@pytest.mark.parametrize("M,K,n", [(1024, 1536, 6144), (77, 192, 128), (300, 512, 640)])
+@pytest.mark.parametrize("out_q", [0.0, 0.05])
+def test_gemm16_geglu_is_gemm16_then_geglu16(M, K, n, out_q):
+    """g4a_gemm16_geglu: the gate/up GEMMs with geglu_b in their epilogue give exactly the codes
+    of g4a_gemm16 on the two matrices followed by g4a_geglu16 (both against the oracle
+    elsewhere), and store nothing past M."""
+    from slang_amd.decoder import geglu16
+    import oracle.decoder as OD
+    rng = np.random.default_rng(M + K + n)
+    print(f"gemm16_geglu M {M} K {K} n {n} out_q {out_q}", flush=True)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    a16 = sa.srqh(t(a), 0.0625)
+    ws = [(words(rng, n * K // 8), (rng.random(n).astype(np.float32) * 0.01 + 0.02)) for _ in range(2)]
+    wg, wu = [sa.dequant(dev_words(w), t(s), K, n) for w, s in ws]
+    gq, uq = 0.05, 0.04
+    out = torch.full((M + 2, n), 7.0, device=DEV, dtype=torch.float16)
+    sa.gemm16_geglu(a16, wg, wu, gq, uq, out_q, out=out[:M])
+    g16 = torch.empty(M, n, device=DEV, dtype=torch.float16)
+    u16 = torch.empty_like(g16)
+    sa.gemm16(a16, [(wg, g16, None), (wu, u16, None)])
+    ref = geglu16(g16, u16, gq, uq, out_q)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:M], ref), f"{(out[:M] != ref).sum().item()} codes differ from gemm16 + geglu16"
+    assert (out[M:] == 7.0).all(), "stores past M"
+    # and the unfused pair is the oracle's geglu_b of the GPU's f16 products (gelu's tanh in
+    # another f32 implementation: codes at most one apart, values within the contract)
+    want = OD.geglu_codes(g16.cpu().numpy(), u16.cpu().numpy(), gq, uq, out_q).astype(np.float32)
+    got = ref.float().cpu().numpy()
+    if out_q:
+        d = np.abs(got - want)
+        assert d.max() <= 1.0 and (d > 0).mean() <= 0.05, f"codes {d.max()} apart, {(d > 0).mean():.2%} off"
+    else:
+        contract_close(got, want, "geglu values")
