@@ -91,6 +91,16 @@ struct GemvArgs {
 
 // NJ chunks of 32 values per lane (hidden <= 2048 * NJ); RPW rows per wave, 4 waves.
 // PRO: the input a and its sum come from the norm prologue instead of memory (NJ 1).
+// sum over the 256 threads of a workgroup (per wave, then the 4 wave sums in order); every
+// thread gets it. Two barriers: red may still be read by the previous call.
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 template <int NJ, int RPW, bool PRO>
 __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
     const int lane = threadIdx.x & 63;
@@ -115,57 +125,56 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
         }
     float sa;
     if constexpr (PRO) {
-        // lane c holds elements 32c .. 32c+31 of each operand (zeros past hidden); every wave
-        // forms the whole row's sums itself, so no barrier is needed. The arithmetic is the
-        // rms_kernel's: y = (res + pa / d1 * w1) * mult, z = y / d2 * w2, a = srq(z, q2).
+        // once per workgroup: thread t holds elements t + 256k of each operand; the sums run
+        // per thread, then over the workgroup (block_sum); a is staged in LDS, from which lane c
+        // of every wave takes elements 32c .. 32c+31. The arithmetic is the rms_kernel's:
+        // y = (res + pa / d1 * w1) * mult, z = y / d2 * w2, a = srq(z, q2).
         static_assert(NJ == 1, "the norm prologue covers hidden <= 2048");
-        const uint32_t nb = (uint32_t)g.hidden * 4u;
-        const rsrc_t rpa = make_rsrc(g.pa, nb), rres = make_rsrc(g.pres, nb);
-        const rsrc_t rw1 = make_rsrc(g.pw1, nb), rw2 = make_rsrc(g.pw2, nb);
-        float pv[32], rv[32], w1v[32], w2v[32];
+        constexpr int PER = 8;
+        __shared__ float s_a[2048];
+        __shared__ float pred[4];
+        const int tid = threadIdx.x, n = g.hidden;
+        float pv[PER], rv[PER], w1v[PER], w2v[PER];
 #pragma unroll
-        for (int q4 = 0; q4 < 8; ++q4) {
-            const int off = 128 * lane + 16 * q4;
-            const float4v a4 = bload_f32x4(rpa, off), r4 = bload_f32x4(rres, off);
-            const float4v u4 = bload_f32x4(rw1, off), v4 = bload_f32x4(rw2, off);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pv[4 * q4 + i] = a4[i];
-                rv[4 * q4 + i] = r4[i];
-                w1v[4 * q4 + i] = u4[i];
-                w2v[4 * q4 + i] = v4[i];
-            }
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + 256 * k;
+            const bool ok = i < n;
+            pv[k] = ok ? g.pa[i] : 0.0f;
+            rv[k] = ok ? g.pres[i] : 0.0f;
+            w1v[k] = ok ? g.pw1[i] : 0.0f;
+            w2v[k] = ok ? g.pw2[i] : 0.0f;
         }
-        const float inv_n = 1.0f / (float)g.hidden;
+        const float inv_n = 1.0f / (float)n;
         float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(pv[i], pv[i], ss);
-        const float d1 = sqrtf(wave_sum(ss) * inv_n + g.peps);
+        for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(pv[k], pv[k], ss);
+        const float d1 = sqrtf(wg_sum(ss, pred) * inv_n + g.peps);
         float ss2 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            rv[i] = (rv[i] + pv[i] / d1 * w1v[i]) * g.pmult;  // x, zeros past hidden
-            ss2 = __builtin_fmaf(rv[i], rv[i], ss2);
+        for (int k = 0; k < PER; ++k) {
+            rv[k] = (rv[k] + pv[k] / d1 * w1v[k]) * g.pmult;  // x, zeros past hidden
+            ss2 = __builtin_fmaf(rv[k], rv[k], ss2);
         }
-        const float d2 = sqrtf(wave_sum(ss2) * inv_n + g.peps);
+        const float d2 = sqrtf(wg_sum(ss2, pred) * inv_n + g.peps);
         float s2 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            av[0][i] = srq(rv[i] / d2 * w2v[i], g.pq2);
-            s2 += av[0][i];
-        }
-        sa = wave_sum(s2);
-        if (blockIdx.x == 0 && wave == 0 && 32 * lane < g.hidden) {
-#pragma unroll
-            for (int q4 = 0; q4 < 8; ++q4) {
-                if (g.pxout)
-                    *reinterpret_cast<float4v*>(g.pxout + 32 * lane + 4 * q4) =
-                        float4v{rv[4 * q4], rv[4 * q4 + 1], rv[4 * q4 + 2], rv[4 * q4 + 3]};
-                if (g.pzout)
-                    *reinterpret_cast<float4v*>(g.pzout + 32 * lane + 4 * q4) =
-                        float4v{av[0][4 * q4], av[0][4 * q4 + 1], av[0][4 * q4 + 2], av[0][4 * q4 + 3]};
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + 256 * k;
+            const float z = srq(rv[k] / d2 * w2v[k], g.pq2);
+            if (i < 2048) s_a[i] = i < n ? z : 0.0f;
+            s2 += i < n ? z : 0.0f;
+            if (blockIdx.x == 0 && i < n) {
+                if (g.pxout) g.pxout[i] = rv[k];
+                if (g.pzout) g.pzout[i] = z;
             }
-            if (g.psum && lane == 0) g.psum[0] = sa;
+        }
+        sa = wg_sum(s2, pred);  // its barriers also publish s_a
+        if (blockIdx.x == 0 && tid == 0 && g.psum) g.psum[0] = sa;
+#pragma unroll
+        for (int q4 = 0; q4 < 8; ++q4) {
+            const float4v v = *reinterpret_cast<const float4v*>(&s_a[32 * lane + 4 * q4]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[0][4 * q4 + i] = v[i];
         }
     } else {
 #pragma unroll
