@@ -114,8 +114,8 @@ __device__ __forceinline__ float chunk_dot(u32x4_t w, const float4v* xq, int str
     return acc;
 }
 
-template <int BITS, int T, int RPW, int EPI>
-__global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
+template <int BITS, int T, int RPW, int EPI, int NT = 256>
+__global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // T threads per row group (16..256, the chunks of a row spread over them), 256/T groups
     // per workgroup, RPW rows per group; groups wider than a wave reduce through LDS.
     // With several groups per workgroup (T <= 64), or a norm prologue (which needs all of x in
@@ -124,13 +124,14 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
     // one copy per matrix step; wider groups use each chunk of x in one thread only and load
     // it straight from memory.
     constexpr int VPC = 128 / BITS;  // values per 16-byte chunk
-    constexpr int NGRP = 256 / T;
+    static_assert(NT == 256 || (T <= 64 && NT <= 1024), "groups wider than a wave reduce within 256 threads");
+    constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
     constexpr float ZP = BITS == 16 ? 0.0f : (float)(1 << (BITS - 1));
     const bool stage = T <= 64 || g.pa != nullptr;  // workgroup-uniform
     extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
     __shared__ float red[T > 64 ? 4 : 1][NM][RPW];
-    __shared__ float xsum_part[8][NM];
+    __shared__ float xsum_part[16][NM];
     __shared__ float xsum_red[4][NM];
     const int tid = threadIdx.x;
     const int sub = tid % T, grp = tid / T;
@@ -167,12 +168,12 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
         }
     };
     if (g.pa) {  // workgroup-uniform; n_in <= 2048
-        constexpr int PER = 8;
+        constexpr int PER = 2048 / NT;
         __shared__ float pred[16];
         float av[PER], rv[PER], w1v[PER], w2v[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + 256 * k;
+            const int i = tid + NT * k;
             const bool ok = i < n_in;
             av[k] = ok ? g.pa[i] : 0.0f;
             rv[k] = ok ? g.pres[i] : 0.0f;
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
         float ss2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + 256 * k;
+            const int i = tid + NT * k;
             const float y = (rv[k] + av[k] / d * w1v[k]) * g.pmult;
             av[k] = y;
             if (i < n_in) {
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
         const float d2 = g.pw2 ? sqrtf(block_sum(ss2, pred) / (float)n_in + g.peps) : 1.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int i = tid + 256 * k;
+            const int i = tid + NT * k;
             const float z = g.pw2 ? av[k] / d2 * w2v[k] : av[k];
             const float zq = g.pf16 ? (float)(half_t)srq((float)(half_t)pin(z), g.pq2) : srq(z, g.pq2);
             if (i < n_in) {
@@ -208,16 +209,16 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
     } else if (stage) {
         // every load of x first, in batches of 4096 values (4 float4 a thread), then the
         // staging: one L2 round trip per batch instead of one per element
-        for (int b0 = 0; b0 < n_in; b0 += 4096) {
+        for (int b0 = 0; b0 < n_in; b0 += 16 * NT) {
             float4v xv[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int i = b0 + 4 * (tid + 256 * k);
+                const int i = b0 + 4 * (tid + NT * k);
                 xv[k] = i < n_in ? *reinterpret_cast<const float4v*>(g.x + i) : float4v{0, 0, 0, 0};
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int i = b0 + 4 * (tid + 256 * k);
+                const int i = b0 + 4 * (tid + NT * k);
                 if (i < n_in) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) stage_x(i + e, xv[k][e]);
@@ -236,6 +237,11 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             xtot[m] = (xsum_part[0][m] + xsum_part[1][m]) + (xsum_part[2][m] + xsum_part[3][m]);
+            if constexpr (NT >= 512)
+                xtot[m] += (xsum_part[4][m] + xsum_part[5][m]) + (xsum_part[6][m] + xsum_part[7][m]);
+            if constexpr (NT == 1024)
+                xtot[m] += ((xsum_part[8][m] + xsum_part[9][m]) + (xsum_part[10][m] + xsum_part[11][m])) +
+                           ((xsum_part[12][m] + xsum_part[13][m]) + (xsum_part[14][m] + xsum_part[15][m]));
             sx[m] = 0.0f;
         }
     }
@@ -512,12 +518,12 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(int n_part, const fl
     if (threadIdx.x == 0) tok[0] = bi == 0x7fffffff ? 0 : bi;  // no finite maximum: 0, as numpy
 }
 
-template <int BITS, int T, int RPW, int EPI>
+template <int BITS, int T, int RPW, int EPI, int NT = 256>
 static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
-    const int rows_per_wg = (256 / T) * RPW;
+    const int rows_per_wg = (NT / T) * RPW;
     const size_t lds = T <= 64 || g.pa ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
-    hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg),
-                       dim3(256), lds, s, g);
+    hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg),
+                       dim3(NT), lds, s, g);
     return hipGetLastError();
 }
 
@@ -531,7 +537,11 @@ static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
     if (c <= 16) return launch_qgemv<BITS, 16, 2, EPI>(g, s);
     if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
-    if (c <= 64) return launch_qgemv<BITS, 64, 2, EPI>(g, s);
+    if (c <= 64)  // the norm prologue once per 1024 threads: a quarter of the workgroups read its
+                  // operands (the gate/up GEMV at E2B shape: whole step 1.807 -> 1.769 ms/token
+                  // with 512 threads, 1.746 with 1024)
+        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 64, 2, EPI, BITS >= 4 ? 1024 : 256>(g, s)
+                                 : launch_qgemv<BITS, 64, 2, EPI>(g, s);
     if (c <= 128) return launch_qgemv<BITS, 128, 2, EPI>(g, s);
     return launch_qgemv<BITS, 256, 2, EPI>(g, s);
 }
