@@ -379,7 +379,27 @@ def decoder_case(steps=32, T=4096):
         rows = min(rows, st.man.window) if s.sliding else rows
         kv += 2 * rows * st.man.n_kv_heads(s.index) * s.head_dim * 2
     pre = decoder_prefill_case(st)
-    return ms, wbytes + kv, wbytes, kv, pre
+    gen = generate_case(st)
+    return ms, wbytes + kv, wbytes, kv, (pre, gen)
+
+
+def generate_case(st, S=1024, n_new=64):
+    """Prompt to tokens on the device (DecoderStack.generate, the reference's generate_resident,
+    runner.py:542-569): the layers-outer prefill of S - 1 prompt tokens, then n_new greedy
+    steps from the last one, every token kept on the GPU, the whole call one HIP graph.
+    Returns ms per call."""
+    ids = torch.randint(0, st.vocab, (S,), generator=torch.Generator().manual_seed(7)).to(torch.int32).cuda()
+    st.generate(ids, n_new)  # sizes the prefill buffers before the capture
+    torch.cuda.synchronize()
+    return graph_time_ms([lambda: st.generate(ids, n_new)], 1, 1), S, n_new
+
+
+def generate_row(gen):
+    ms, S, n_new = gen
+    return {"ms_per_call": round(ms, 3), "prompt_tokens": S, "new_tokens": n_new,
+            "tokens/s": round(n_new / ms * 1e3, 1), "note": "prefill of the prompt's first S-1 tokens "
+            "(layers outer), then greedy decode steps from its last token with every token kept on the "
+            "GPU (DecoderStack.generate), one HIP graph per call"}
 
 
 def decoder_prefill_case(st, S=1024, reps=4):
@@ -603,10 +623,11 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.decoder_only:
-        msd, nbd, wb, kvb, pre = decoder_case()
+        msd, nbd, wb, kvb, (pre, gen) = decoder_case()
         print(json.dumps({"decoder_e2b": {"ms_per_token": round(msd, 4), "GB/s": round(nbd / msd / 1e6, 2),
                                           "weight_bytes": wb, "kv_bytes": kvb},
-                          "decoder_e2b_prefill": prefill_row(pre)}), flush=True)
+                          "decoder_e2b_prefill": prefill_row(pre), "decoder_e2b_generate": generate_row(gen)}),
+              flush=True)
         return
     if args.batched_only:
         ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
@@ -686,8 +707,9 @@ def main():
         if not args.no_stack:
             sec["stack_5"] = stack_case(sa, gen)
         if not args.no_decoder:
-            msd, nbd, wb, kvb, pre = decoder_case()
+            msd, nbd, wb, kvb, (pre, gen) = decoder_case()
             sec["decoder_e2b_prefill"] = prefill_row(pre)
+            sec["decoder_e2b_generate"] = generate_row(gen)
             sec["decoder_e2b"] = {"ms_per_token": round(msd, 4), "tokens/s": round(1e3 / msd, 1),
                                   "GB/s": round(nbd / msd / 1e6, 2), "hbm_frac": round(nbd / msd / 1e6 / HBM_PEAK_GBS, 4),
                                   "bytes_per_token": nbd, "weight_bytes": wb, "kv_bytes": kvb,

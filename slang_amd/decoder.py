@@ -492,14 +492,21 @@ class DecoderStack:
         """Greedy generation kept on the GPU (G4Runner.generate_resident, runner.py:542-569):
         prefill every prompt token but the last, then n_new decode steps from the last one, each
         step's argmax feeding the next step's embedding on the device. Returns the n_new tokens
-        (device int32); the caller reads them back when it wants them."""
-        ids = list(ids)
-        if not ids or n_new <= 0:
+        (device int32); the caller reads them back when it wants them. ids: host ints, or a device
+        int32 tensor (then nothing goes through the host, so the call can be captured in a graph)."""
+        dev_ids = torch.is_tensor(ids) and ids.device.type != "cpu"
+        if not dev_ids:
+            ids = list(ids)
+        n = int(ids.numel()) if dev_ids else len(ids)
+        if n == 0 or n_new <= 0:
             return torch.empty(0, dtype=torch.int32, device=self.device)
-        pos = self.prefill(ids[:-1], start_pos) if len(ids) > 1 else start_pos
+        pos = self.prefill(ids[:-1], start_pos) if n > 1 else start_pos
         if pos + n_new > self.attn.max_seq:
             raise ValueError(f"{pos + n_new} positions exceed the {self.attn.max_seq}-row caches")
-        self.tok.fill_(int(ids[-1]))
+        if dev_ids:
+            self.tok.copy_(ids[-1:].to(torch.int32))
+        else:
+            self.tok.fill_(int(ids[-1]))
         out = torch.empty(n_new, dtype=torch.int32, device=self.device)
         for i in range(n_new):
             self.step(pos + i)

@@ -192,3 +192,7 @@ def test_generate_is_prefill_then_resident_steps(tmp_path):
         st2.step(pos + i)
         want.append(int(host(st2.tok)[0]))
     assert got.tolist() == want
+    # the token ids on the device (nothing through the host, as under graph capture)
+    st3 = D.DecoderStack(m, max_seq=64, device=DEV)
+    dev = torch.tensor(ids, dtype=torch.int32, device=DEV)
+    assert host(st3.generate(dev, 6)).tolist() == want
