@@ -344,3 +344,45 @@ def test_gemm16_geglu_is_gemm16_then_geglu16(M, K, n, out_q):
         assert d.max() <= 1.0 and (d > 0).mean() <= 0.05, f"codes {d.max()} apart, {(d > 0).mean():.2%} off"
     else:
         contract_close(got, want, "geglu values")
+
+
+def test_split_gemm_and_geglu_gemm_replay_in_a_graph():
+    """The K-split GEMM (its tickets return to zero on every call) and the gate/up GEMM with
+    geglu_b, captured in one HIP graph: every replay, with eager work and synchronisations
+    between them, gives the eager results bit for bit."""
+    rng = np.random.default_rng(5)
+    M, K, n, K2 = 512, 2048, 1536, 1536
+    a16 = sa.srqh(t(rng.standard_normal((M, K)).astype(np.float32)), 0.0625)
+    b16 = sa.srqh(t(rng.standard_normal((M, K2)).astype(np.float32)), 0.0625)
+    w = sa.dequant(dev_words(words(rng, n * K // 8)), t(rng.random(n).astype(np.float32) * 0.01 + 0.02), K, n)
+    wg, wu = [sa.dequant(dev_words(words(rng, 640 * K2 // 8)), t(rng.random(640).astype(np.float32) * 0.01 + 0.02),
+                         K2, 640) for _ in range(2)]
+    gws = sa.GemmWorkspace()
+    o1 = torch.empty(M, n, device=DEV, dtype=torch.float16)
+    o2 = torch.empty(M, 640, device=DEV, dtype=torch.float16)
+
+    def run():
+        sa.gemm16(a16, [(w, o1, None, 0.5)], gws)
+        sa.gemm16_geglu(b16, wg, wu, 0.05, 0.04, 0.05, out=o2)
+
+    run()
+    torch.cuda.synchronize()
+    ref1, ref2 = o1.clone(), o2.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    for rep in range(3):
+        o1.fill_(float("nan"))
+        o2.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1, ref1), f"replay {rep}: split GEMM differs"
+        assert torch.equal(o2, ref2), f"replay {rep}: gate/up GEMM differs"
+        assert not gws.buf[:sa._lib.GEMM_TICKET_BYTES].any(), "tickets left non-zero"
+        _ = (a16.float() * 2).sum().item()  # eager work between replays
