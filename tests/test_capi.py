@@ -160,6 +160,35 @@ def test_projection_argument_errors(lib):
     assert b"matrix 0" in lib.g4a_last_error()
 
 
+def test_gemm16_split_plan(lib):
+    """g4a_gemm16_ws_bytes, the host side of the K split: launches with fewer 128 x 64 tiles
+    than CUs split K so about 768 workgroups run (each range at least 4 k-steps), the rest do
+    not split (0 bytes); the size is the ticket words plus one f32 partial tile (128 x 64) per
+    (tile, split)."""
+    f = FAKE
+    mat = lambda n: _lib.G4AGemmMat(f.value, f.value, n, 0, 0.0, 1.0)  # noqa: E731
+    tab = lambda *ns: (_lib.G4AGemmMat * len(ns))(*[mat(n) for n in ns])  # noqa: E731
+    ws = lambda M, K, *ns: lib.g4a_gemm16_ws_bytes(M, K, len(ns), tab(*ns))  # noqa: E731
+    part = 128 * 64 * 4
+    assert ws(1024, 6144, 1536) == _lib.GEMM_TICKET_BYTES + 192 * 4 * part   # down: 192 tiles, 4 splits
+    assert ws(1024, 2048, 1536) == _lib.GEMM_TICKET_BYTES + 192 * 4 * part   # o_proj
+    assert ws(1024, 1536, 256) == _lib.GEMM_TICKET_BYTES + 32 * 6 * part     # PLE gate: 24 k-steps, 6 ranges
+    assert ws(77, 4096, 128, 384) == _lib.GEMM_TICKET_BYTES + 8 * 16 * part  # one m-tile: 16 ranges of 4
+    assert ws(1024, 256, 1536) == 0                                          # 4 k-steps: nothing to split
+    assert ws(1024, 1536, 2048, 256, 256) == 0                               # 320 tiles: enough
+    assert ws(1024, 1536, 6144, 6144) == 0                                   # 128-wide tiles
+    assert ws(1024, 100, 1536) == 0 and ws(0, 1536, 1536) == 0 and ws(64, 1536, 100) == 0  # invalid: 0
+    # a short workspace is refused before anything runs
+    need = ws(1024, 2048, 1536)
+    assert lib.g4a_gemm16_ws(1024, 2048, f, 1, tab(1536), f, need - 16, None) == -3
+    assert lib.g4a_gemm16_ws(1024, 2048, f, 1, tab(1536), ctypes.c_void_p(0x10010), need, None) == -1  # alignment
+    # g4a_gemm16_geglu(M, K, a, w_gate, w_up, n, gate_q, up_q, out_q, out, stream)
+    assert lib.g4a_gemm16_geglu(16, 96, f, f, f, 128, 0.1, 0.1, 0.1, f, None) == -1  # K % 64
+    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 96, 0.1, 0.1, 0.1, f, None) == -1  # n % 64
+    assert lib.g4a_gemm16_geglu(16, 128, f, None, f, 128, 0.1, 0.1, 0.1, f, None) == -1
+    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 128, 0.1, -0.1, 0.1, f, None) == -1
+
+
 def test_gemm_mat_struct_layout():
     """struct g4a_gemm_mat: two pointers, two ints, two floats (8-byte aligned, 32 bytes)."""
     assert [f[0] for f in _lib.G4AGemmMat._fields_] == ["w_f16", "out", "n", "out_f32", "out_q", "alpha"]
