@@ -647,7 +647,7 @@ def main():
                    "timing": {"graph_calls": args.steps, "distinct_caches_timed": min(args.steps, 64),
                               "rotation_bytes": 64 * nbytes, "mall_flushed_before_timing": True,
                               "note": "one HIP graph of exactly `steps` calls over 64 rotated caches (512 MiB); "
-                                      "1 GiB is read and written before the timed replay, so every timed call "
+                                      "1 GiB is read before the timed replay, so every timed call "
                                       "streams a cache that is not in the 256 MB MALL"}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
