@@ -530,12 +530,14 @@ static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
 // Threads per row group: the smallest of 16..256 covering a row's chunks, so one pass
 // reads every row of the workgroup and all of them are in flight together (decode GEMVs
 // are latency-bound: o_proj and down have only 1536 rows). Rows per group: 8 for the
-// short 2-bit rows of the lm_head (x loaded once per 8 rows), else 2 (measured: 8 rows
-// per group on the 1536-row down projection, 192 workgroups, was 20 % slower).
+// short 2-bit rows of the lm_head (x loaded once per 8 rows), 1 for rows of at most 16
+// chunks (the per-layer-embedding projection: twice the workgroups, 1.737 -> 1.727 ms a
+// decode step), else 2 (measured: 8 rows per group on the 1536-row down projection, 192
+// workgroups, was 20 % slower).
 template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
-    if (c <= 16) return launch_qgemv<BITS, 16, 2, EPI>(g, s);
+    if (c <= 16) return launch_qgemv<BITS, 16, 1, EPI>(g, s);
     if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
     if (c <= 64)  // the norm prologue once per 1024 threads: a quarter of the workgroups read its
                   // operands (the gate/up GEMV at E2B shape: whole step 1.807 -> 1.769 ms/token
