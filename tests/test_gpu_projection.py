@@ -386,3 +386,21 @@ def test_split_gemm_and_geglu_gemm_replay_in_a_graph():
         assert torch.equal(o2, ref2), f"replay {rep}: gate/up GEMM differs"
         assert not gws.buf[:sa._lib.GEMM_TICKET_BYTES].any(), "tickets left non-zero"
         _ = (a16.float() * 2).sum().item()  # eager work between replays
+
+
+def test_split_gemm_workspace_shared_across_shapes():
+    """One workspace for K-split launches of different tile counts and split counts in a row
+    (the decoder prefill shares one): every result matches a fresh workspace's bit for bit and
+    the tickets are zero after each call."""
+    rng = np.random.default_rng(9)
+    shared = sa.GemmWorkspace()
+    for M, K, n in [(1024, 2048, 1536), (1024, 1536, 256), (512, 6144, 1536), (1024, 2048, 1536), (200, 1536, 256)]:
+        a16 = sa.srqh(t(rng.standard_normal((M, K)).astype(np.float32)), 0.0625)
+        w = sa.dequant(dev_words(words(rng, n * K // 8)), t(rng.random(n).astype(np.float32) * 0.01 + 0.02), K, n)
+        o1 = torch.empty(M, n, device=DEV, dtype=torch.float16)
+        o2 = torch.empty_like(o1)
+        sa.gemm16(a16, [(w, o1, None)], shared)
+        sa.gemm16(a16, [(w, o2, None)], sa.GemmWorkspace())
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2), f"M {M} K {K} n {n}: shared workspace result differs"
+        assert not shared.buf[:sa._lib.GEMM_TICKET_BYTES].any(), "tickets left non-zero"
