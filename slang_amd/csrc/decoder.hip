@@ -64,9 +64,20 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
-__device__ __forceinline__ float gelu_tanh(float v) {
-    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+// a reduction buffer written once per kernel: no barrier before the write
+__device__ __forceinline__ float block_sum_once(float v, float* red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
 }
+
+// gelu with the tanh approximation in its exp2 form (gelu_tanh16, the batched prefill's): the
+// libm tanhf form cost the decode step 1.665 -> 1.642 ms/token in the GEMV epilogues
+__device__ __forceinline__ float gelu_tanh(float v) { return gelu_tanh16(v); }
 
 // sum over the LPR lanes of a lane group (16, 32 or 64), every lane of the group gets it
 template <int LPR>
@@ -180,7 +191,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     };
     if (g.pa) {  // workgroup-uniform; n_in <= 2048
         constexpr int PER = 2048 / NT;
-        __shared__ float pred[16];
+        __shared__ float pred[2][16];  // one buffer per reduction
         float av[PER], rv[PER], w1v[PER], w2v[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
@@ -194,7 +205,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(av[k], av[k], ss);
-        const float d = sqrtf(block_sum(ss, pred) / (float)n_in + g.peps);
+        const float d = sqrtf(block_sum_once(ss, pred[0]) / (float)n_in + g.peps);
         float ss2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
                 ss2 = __builtin_fmaf(y, y, ss2);
             }
         }
-        const float d2 = g.pw2 ? sqrtf(block_sum(ss2, pred) / (float)n_in + g.peps) : 1.0f;
+        const float d2 = g.pw2 ? sqrtf(block_sum_once(ss2, pred[1]) / (float)n_in + g.peps) : 1.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int i = tid + NT * k;
