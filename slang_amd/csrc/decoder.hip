@@ -125,7 +125,32 @@ __device__ __forceinline__ float chunk_dot(u32x4_t w, const float4v* xq, int str
     return acc;
 }
 
-template <int BITS, int T, int RPW, int EPI, int NT = 256>
+// The same sum in integers when x is on its quantisation grid (x = k * in_q, k in [-128, 127]):
+// the codes times the int8 k with v_dot4_i32_i8, exact. 4-bit: the even and odd nibbles of
+// word w come out as bytes (codes 0..15) and meet the k of the same values, staged per chunk
+// as 8 dwords (dword 2w: values 8w, 8w+2, 8w+4, 8w+6; dword 2w+1: the odd ones) in two
+// uint4 planes [2][nch]; the zero point is taken out afterwards as in chunk_dot. 8-bit: the
+// biased codes XOR 0x80 are the signed c - 128, against k in row order (one plane).
+template <int BITS>
+__device__ __forceinline__ int chunk_idot(u32x4_t w, const u32x4_t* xk, int stride, int acc) {
+    if constexpr (BITS == 4) {
+        const u32x4_t x0 = xk[0], x1 = xk[stride];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+            const uint32_t xe = k < 2 ? x0[2 * k] : x1[2 * k - 4], xo = k < 2 ? x0[2 * k + 1] : x1[2 * k - 3];
+            acc = __builtin_amdgcn_sdot4((int)lo, (int)xe, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)hi, (int)xo, acc, false);
+        }
+    } else {
+        const u32x4_t x0 = xk[0];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_sdot4((int)(w[k] ^ 0x80808080u), (int)x0[k], acc, false);
+    }
+    return acc;
+}
+
+template <int BITS, int T, int RPW, int EPI, int NT = 256, bool IDOT = false>
 __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // T threads per row group (16..256, the chunks of a row spread over them), 256/T groups
     // per workgroup, RPW rows per group; groups wider than a wave reduce through LDS.
@@ -138,8 +163,11 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     static_assert(NT == 256 || (T <= 64 && NT <= 1024), "groups wider than a wave reduce within 256 threads");
     constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
-    constexpr float ZP = BITS == 16 ? 0.0f : (float)(1 << (BITS - 1));
-    const bool stage = T <= 64 || g.pa != nullptr;  // workgroup-uniform
+    // IDOT (4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
+    // index k, the dot products in integers (chunk_idot), y = scale * (sum - zp * sum k) * in_q
+    static_assert(!IDOT || BITS == 4 || BITS == 8, "integer dot products for 4- and 8-bit rows");
+    constexpr float ZP = BITS == 16 || (IDOT && BITS == 8) ? 0.0f : (float)(1 << (BITS - 1));
+    const bool stage = IDOT || T <= 64 || g.pa != nullptr;  // workgroup-uniform
     extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
     __shared__ float red[T > 64 ? 4 : 1][NM][RPW];
     __shared__ float xsum_part[16][NM];
@@ -181,6 +209,24 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     float* xsf = reinterpret_cast<float*>(xs);
     auto stage_x = [&](int i, float v) {
         const int c = i / VPC, e = i % VPC;
+        if constexpr (IDOT) {
+            // byte of value e of chunk c: 4-bit dword 2(e/8) + (e&1), byte (e%8)/2, in plane dword/4
+            int at;
+            if constexpr (BITS == 4) {
+                const int dw = 2 * (e >> 3) + (e & 1);
+                at = ((dw >> 2) * nch + c) * 16 + (dw & 3) * 4 + ((e & 7) >> 1);
+            } else {
+                at = c * 16 + e;
+            }
+            signed char* xsb = reinterpret_cast<signed char*>(xs);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float k = fminf(fmaxf(rintf(v / (m == 0 ? g.in_q : g.in_q2)), -128.0f), 127.0f);  // srq's index
+                xsb[m * n_in + at] = (signed char)(int)k;
+                sx[m] += k;
+            }
+            return;
+        }
         const int at = ((e >> 2) * nch + c) * 4 + (e & 3);
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
@@ -275,7 +321,14 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         for (int r = 0; r < RPW; ++r) acc[m][r] = 0.0f;
     for (int c = sub; c < nch; c += T) {
         if (c != sub) load_w(c);
-        if (stage) {
+        if constexpr (IDOT) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const u32x4_t* xk = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const signed char*>(xs) + m * n_in) + c;
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) acc[m][r] += (float)chunk_idot<BITS>(wv[m][r], xk, nch, 0);
+            }
+        } else if (stage) {
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -342,9 +395,12 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
         if (sub == r && row < g.n_out) {
-            float y = srq(esc[0] * (acc[0][r] - zsx[0]), g.out_q);
+            // IDOT: the integer sum (exact in f32 while below 2^24) times the input step
+            const float d0 = IDOT ? (acc[0][r] - zsx[0]) * g.in_q : acc[0][r] - zsx[0];
+            float y = srq(esc[0] * d0, g.out_q);
             if constexpr (EPI == 1) {
-                const float yb = srq(esc[NM - 1] * (acc[NM - 1][r] - zsx[NM - 1]), g.out_q2);
+                const float d1 = IDOT ? (acc[NM - 1][r] - zsx[NM - 1]) * g.in_q2 : acc[NM - 1][r] - zsx[NM - 1];
+                const float yb = srq(esc[NM - 1] * d1, g.out_q2);
                 y = srq(gelu_tanh(y) * yb, g.epi_q);
             } else if constexpr (EPI == 2) {
                 y = gelu_tanh(y) * emul;
@@ -543,9 +599,17 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(int n_part, const fl
 template <int BITS, int T, int RPW, int EPI, int NT = 256>
 static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
     const int rows_per_wg = (NT / T) * RPW;
-    const size_t lds = T <= 64 || g.pa ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
-    hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT>), dim3((g.n_out + rows_per_wg - 1) / rows_per_wg),
-                       dim3(NT), lds, s, g);
+    const bool staged = T <= 64 || g.pa;
+    const size_t lds = staged ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
+    const dim3 grid((g.n_out + rows_per_wg - 1) / rows_per_wg);
+    if constexpr (BITS == 4 || BITS == 8) {
+        // integer dot products where x is staged on a grid (every in_q > 0; whole chunks)
+        if (staged && g.in_q > 0.0f && (EPI != 1 || g.in_q2 > 0.0f) && g.n_in % (128 / BITS) == 0) {
+            hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT, true>), grid, dim3(NT), lds, s, g);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT>), grid, dim3(NT), lds, s, g);
     return hipGetLastError();
 }
 

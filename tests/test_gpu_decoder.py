@@ -51,6 +51,28 @@ def test_qgemv_parity(bits, n_in, n_out, in_q, out_q):
         contract_close(got, ref, f"qgemv {bits}-bit {n_out}x{n_in}")
 
 
+@pytest.mark.parametrize("bits,n_in,n_out", [(4, 1536, 6144), (4, 2048, 1531), (8, 256, 1536), (8, 512, 77)])
+def test_qgemv_integer_dot_is_exact(bits, n_in, n_out):
+    """Staged 4/8-bit GEMVs with in_q > 0 sum codes times the int8 grid index k = srq's
+    clamp(rint(x / in_q)) in integers (v_dot4_i32_i8). With out_q 0 the output is then
+    exactly f32(f32(D * in_q) * scale), D = sum (c - zp) k over the row computed here in int64:
+    a wrong nibble/byte order, zero point or index would change D."""
+    rng = np.random.default_rng(bits * 31 + n_out)
+    codes = rng.integers(0, 1 << bits, size=(n_out, n_in))
+    words = pack_values(codes, bits)
+    scale = (0.01 * (1 + rng.random(n_out))).astype(np.float32)
+    x = (3 * rng.standard_normal(n_in)).astype(np.float32)  # some |x / in_q| past 127: clamped
+    in_q = np.float32(0.03)
+    got = host(D.qgemv(dev(x), dev(words).view(torch.int32).reshape(-1), dev(scale), n_in, n_out, in_q=float(in_q),
+                       out_q=0.0, bits=bits))
+    k = np.clip(np.rint(x / in_q), -128, 127).astype(np.int64)
+    assert (np.abs(x / in_q) > 127.5).any()
+    d = (codes.astype(np.int64) - (1 << (bits - 1))) @ k
+    assert np.abs(d).max() < 1 << 24
+    want = (d.astype(np.float32) * in_q).astype(np.float32) * scale
+    np.testing.assert_array_equal(got, want)
+
+
 @pytest.mark.parametrize("bits,n_in,n_out", [(4, 1536, 6144), (2, 1536, 12288), (4, 256, 1024), (8, 512, 64)])
 def test_qgemv_geglu_and_gelu_mul(bits, n_in, n_out):
     rng = np.random.default_rng(bits + n_out)
