@@ -294,7 +294,11 @@ int g4a_gemm16_ws(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_ma
  * (reference.py:96-101 _qlin; :103-111 _ilin_raw is the bits = 8 case over export.py's
  * biased codes, :150-156; :200-206 the lm_head with in_q = out_q = 0). Rows are packed as
  * for g4a_dequant; bits 2, 4 or 8; n_in a multiple of 128/bits. x f32 [n_in], 16-byte
- * aligned; out f32 [n_out].
+ * aligned; out f32 [n_out]. With in_q > 0 and 4/8-bit rows of at most 64 16-byte chunks
+ * (or a norm prologue, in the fused GEMVs below) the row sum is formed in integers over
+ * srq's grid index of x and is exact: out = srq(f32(f32(D * in_q) * w_scale), out_q), D =
+ * sum (q - zp) * clamp(rint(x / in_q)); the f32 accumulation of the reference rounds its
+ * partial sums, so the two can differ in the last bits before the output srq.
  */
 int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
               const float* w_scale, float out_q, float* out, void* stream);
