@@ -160,7 +160,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // one copy per matrix step; wider groups use each chunk of x in one thread only and load
     // it straight from memory.
     constexpr int VPC = 128 / BITS;  // values per 16-byte chunk
-    static_assert(NT == 256 || (T <= 64 && NT <= 1024), "groups wider than a wave reduce within 256 threads");
+    static_assert(NT == 256 || (T <= 64 && NT <= 1024 && NT % 256 == 0), "groups wider than a wave reduce within 256 threads");
     constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
     // IDOT (4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         }
     };
     if (g.pa) {  // workgroup-uniform; n_in <= 2048
-        constexpr int PER = 2048 / NT;
+        constexpr int PER = (2048 + NT - 1) / NT;
         __shared__ float pred[2][16];  // one buffer per reduction
         float av[PER], rv[PER], w1v[PER], w2v[PER];
 #pragma unroll
@@ -307,6 +307,8 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             xtot[m] = (xsum_part[0][m] + xsum_part[1][m]) + (xsum_part[2][m] + xsum_part[3][m]);
             if constexpr (NT >= 512)
                 xtot[m] += (xsum_part[4][m] + xsum_part[5][m]) + (xsum_part[6][m] + xsum_part[7][m]);
+            if constexpr (NT == 768)
+                xtot[m] += (xsum_part[8][m] + xsum_part[9][m]) + (xsum_part[10][m] + xsum_part[11][m]);
             if constexpr (NT == 1024)
                 xtot[m] += ((xsum_part[8][m] + xsum_part[9][m]) + (xsum_part[10][m] + xsum_part[11][m])) +
                            ((xsum_part[12][m] + xsum_part[13][m]) + (xsum_part[14][m] + xsum_part[15][m]));
@@ -625,10 +627,11 @@ static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
     if (c <= 16) return launch_qgemv<BITS, 16, 1, EPI>(g, s);
     if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
-    if (c <= 64)  // the norm prologue once per 1024 threads: a quarter of the workgroups read its
-                  // operands (the gate/up GEMV at E2B shape: whole step 1.807 -> 1.769 ms/token
-                  // with 512 threads, 1.746 with 1024)
-        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 64, 2, EPI, BITS >= 4 ? 1024 : 256>(g, s)
+    if (c <= 64)  // the norm prologue once per 768 threads: fewer workgroups read its operands
+                  // (the gate/up GEMV at E2B shape: whole step 1.807 -> 1.769 ms/token with 512
+                  // threads, 1.746 with 1024; 768 gives its 6144 rows one workgroup per CU:
+                  // 1.583 -> 1.571 against 1024)
+        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 64, 2, EPI, 768>(g, s)
                                  : launch_qgemv<BITS, 64, 2, EPI>(g, s);
     if (c <= 128) return launch_qgemv<BITS, 128, 2, EPI>(g, s);
     return launch_qgemv<BITS, 256, 2, EPI>(g, s);
