@@ -160,7 +160,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // one copy per matrix step; wider groups use each chunk of x in one thread only and load
     // it straight from memory.
     constexpr int VPC = 128 / BITS;  // values per 16-byte chunk
-    static_assert(NT == 256 || (T <= 64 && NT <= 1024 && NT % 256 == 0), "groups wider than a wave reduce within 256 threads");
+    static_assert(NT == 256 || (T <= 128 && NT <= 1024 && NT % 256 == 0), "workgroup shapes the launches use");
     constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
     // IDOT (4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
@@ -169,9 +169,9 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     constexpr float ZP = BITS == 16 || (IDOT && BITS == 8) ? 0.0f : (float)(1 << (BITS - 1));
     const bool stage = IDOT || T <= 64 || g.pa != nullptr;  // workgroup-uniform
     extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
-    __shared__ float red[T > 64 ? 4 : 1][NM][RPW];
+    __shared__ float red[T > 64 ? NT / 64 : 1][NM][RPW];
     __shared__ float xsum_part[16][NM];
-    __shared__ float xsum_red[4][NM];
+    __shared__ float xsum_red[T > 64 ? NT / 64 : 1][NM];
     const int tid = threadIdx.x;
     const int sub = tid % T, grp = tid / T;
     const int row0 = (blockIdx.x * NGRP + grp) * RPW;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     }
     if constexpr (T > 64) {  // the group's waves through LDS (one group per 128/256 threads)
         const int wig = sub >> 6;  // wave in group
-        const int slot = (grp * (T / 64) + wig) & 3;
+        const int slot = grp * (T / 64) + wig;  // the wave's index
         if ((tid & 63) == 0) {
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
@@ -378,12 +378,12 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             for (int r = 0; r < RPW; ++r) {
                 float t = 0.0f;
 #pragma unroll
-                for (int k = 0; k < T / 64; ++k) t += red[(grp * (T / 64) + k) & 3][m][r];
+                for (int k = 0; k < T / 64; ++k) t += red[grp * (T / 64) + k][m][r];
                 acc[m][r] = t;
             }
             float t = 0.0f;
 #pragma unroll
-            for (int k = 0; k < T / 64; ++k) t += xsum_red[(grp * (T / 64) + k) & 3][m];
+            for (int k = 0; k < T / 64; ++k) t += xsum_red[grp * (T / 64) + k][m];
             sx[m] = t;
         }
     }
@@ -633,7 +633,8 @@ static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
                   // 1.583 -> 1.571 against 1024)
         return BITS >= 4 && g.pa ? launch_qgemv<BITS, 64, 2, EPI, 768>(g, s)
                                  : launch_qgemv<BITS, 64, 2, EPI>(g, s);
-    if (c <= 128) return launch_qgemv<BITS, 128, 2, EPI>(g, s);
+    if (c <= 128)  // with a prologue (the PLE gate): 512 threads, 4 elements of it a thread
+        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 128, 2, EPI, 512>(g, s) : launch_qgemv<BITS, 128, 2, EPI>(g, s);
     return launch_qgemv<BITS, 256, 2, EPI>(g, s);
 }
 
