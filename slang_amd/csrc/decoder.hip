@@ -620,8 +620,9 @@ static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
 // are latency-bound: o_proj and down have only 1536 rows). Rows per group: 8 for the
 // short 2-bit rows of the lm_head (x loaded once per 8 rows), 1 for rows of at most 16
 // chunks (the per-layer-embedding projection: twice the workgroups, 1.737 -> 1.727 ms a
-// decode step), else 2 (measured: 8 rows per group on the 1536-row down projection, 192
-// workgroups, was 20 % slower).
+// decode step), 3 for rows of more than 128 chunks (the down projection: 512 workgroups
+// of 256 threads, two a CU, each x chunk serving 3 rows: 1.549 -> 1.537 ms a step; 4 rows
+// gained nothing, 8 were 20 % slower), else 2.
 template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
@@ -635,7 +636,7 @@ static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
                                  : launch_qgemv<BITS, 64, 2, EPI>(g, s);
     if (c <= 128)  // with a prologue (the PLE gate): 512 threads, 4 elements of it a thread
         return BITS >= 4 && g.pa ? launch_qgemv<BITS, 128, 2, EPI, 512>(g, s) : launch_qgemv<BITS, 128, 2, EPI>(g, s);
-    return launch_qgemv<BITS, 256, 2, EPI>(g, s);
+    return launch_qgemv<BITS, 256, 3, EPI>(g, s);
 }
 
 static int qgemv_check(int bits, int n_in, int n_out, const float* x, const uint32_t* w, const float* scale,
