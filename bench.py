@@ -182,8 +182,11 @@ def prefill_case(sa, S, window, theta, steps, warmup, gen, nH=NH, kvH=KVH, hd=HD
     return ms, flops, host
 
 
-# the prefill modes beside config 3's default (tag: prefill_case keywords)
-PREFILL_MODES = {"hilo": dict(hilo=True), "f32kv": dict(kv32=True), "hd512": dict(nH=8, kvH=1, hd=512)}
+# the prefill modes beside config 3's default (tag: prefill_case keywords): the fused form's
+# f32 q (hilo), the GEMM form on f32 caches (f32kv: both caches rounded to f16 as its srqh_b
+# does), the fused form on its own f32 caches (fused32: f32 q, K at f32 accuracy), hd 512
+PREFILL_MODES = {"hilo": dict(hilo=True), "f32kv": dict(kv32=True), "fused32": dict(kv32=True, hilo=True),
+                 "hd512": dict(nH=8, kvH=1, hd=512)}
 
 
 def batched_decode_case(sa, steps, warmup, gen):
@@ -689,7 +692,10 @@ def main():
                 sec[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(tf, 2),
                             "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl,
                             "note": {"hilo": "config 3 in the f32-q attn_prefill form (G4A_Q_HILO)",
-                                     "f32kv": "config 3 on f32 caches",
+                                     "f32kv": "config 3 on f32 caches, GEMM form (caches rounded to f16 as "
+                                              "srqh_b does)",
+                                     "fused32": "config 3 as attn_prefill on its own f32 caches: f32 q, K at "
+                                                "f32 accuracy (high and low f16 parts)",
                                      "hd512": "S 1024 at hd 512, nH 8 / kvH 1 (E2B global layer shape)"}[mode]}
         ms4, nb4, toks = batched_decode_case(sa, max(8, args.steps // 16), args.warmup, gen)
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),

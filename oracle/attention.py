@@ -214,7 +214,7 @@ def decode_attention_batched(q, k_caches, v_caches, key_lens, n_kv_heads, **kw):
 
 def prefill_attention(q, k_cache, v_cache, start_pos, n_kv_heads, *, q_gain=None, cos=None,
                       sin=None, window=0, scale=1.0, eps=EPS, out_q=0.0, q_round_f16=True,
-                      block=256):
+                      kv_round_f16=False, block=256):
     """Batched causal attention for S prompt tokens at positions start_pos..start_pos+S-1.
 
     q [S][nH][hd] f32 raw; cos/sin [S][half] rows for those absolute positions
@@ -222,6 +222,11 @@ def prefill_attention(q, k_cache, v_cache, start_pos, n_kv_heads, *, q_gain=None
     k_cache/v_cache [>= start_pos+S][kvH][hd] already hold every token's k/v.
     q_round_f16 mirrors qprep_b's f16 rounding of the normalised, rotated q
     (kernels_dsl.py:1872-1873), which is also what the MFMA kernel consumes.
+    kv_round_f16 mirrors the GEMM form's conversion of the caches to f16 before its
+    products (srqh_b with step 0 on kc and vc, prefill_gpu.py:286-288; kernels_dsl.py:
+    232-242): a no-op on f16 caches, round-to-nearest-even on f32 ones. The fused form
+    (attn_prefill, kernels_dsl.py:1950-2098) reads its f32 caches as they are: both
+    roundings off.
     Each query attends [max(0, p+1-W), p] (kernels_dsl.py:1986-1992).
     Query rows are processed in blocks to bound memory at long S. Returns [S][nH][hd] f32.
     """
@@ -237,6 +242,9 @@ def prefill_attention(q, k_cache, v_cache, start_pos, n_kv_heads, *, q_gain=None
     for kh in range(n_kv_heads):
         keys = np.asarray(k_cache[:T, kh], np.float32)
         vals = np.asarray(v_cache[:T, kh], np.float32)
+        if kv_round_f16:
+            keys = keys.astype(np.float16).astype(np.float32)
+            vals = vals.astype(np.float16).astype(np.float32)
         for s0 in range(0, S, block):
             s1 = min(S, s0 + block)
             pos = start_pos + np.arange(s0, s1)

@@ -25,8 +25,8 @@ from . import _lib
 from ._lib import G4ACfg, check
 
 __all__ = [
-    "AttnConfig", "DecodeWorkspace", "Workspace", "decode", "prefill", "qprep", "kv_write", "rope_tables",
-    "attn_101", "kvnorm", "kvnorm_b", "attn_prefill", "attn_gemm", "qprep_b",
+    "AttnConfig", "DecodeWorkspace", "Workspace", "decode", "prefill", "prefill_ws_bytes", "qprep", "kv_write",
+    "rope_tables", "attn_101", "kvnorm", "kvnorm_b", "attn_prefill", "attn_gemm", "qprep_b",
 ]
 
 
@@ -82,21 +82,48 @@ def rope_tables(positions, head_dim: int, theta: float, cutoff: int | None = Non
 
 
 class DecodeWorkspace:
-    """Split-KV partials for ``decode`` (the reference's `partials` buffer, runner.py:367-371)
-    and for the key split of ``prefill`` on short prompts (the role of PrefillGPU's scores
-    buffer, prefill_gpu.py:229-256).
+    """Device scratch of the attention calls, owned by the caller as the runners own theirs
+    (runner.py:102-109, prefill_gpu.py:229-256): the split-KV partials of ``decode`` (the
+    reference's `partials` buffer, runner.py:367-371) and, for ``prefill``, the f16 copies of
+    f32 caches, hd-512 q and the key split's partials (the role of PrefillGPU's qf16 / kf16 /
+    vf16 / scores buffers).
 
-    Grows on demand; needs no initialisation. Calls that may run concurrently
-    need separate workspaces.
+    Needs no initialisation. Calls that may run concurrently need separate workspaces.
+    Unreserved, it grows on demand (an allocation when a call needs more than it holds).
+    ``reserve(nbytes)`` allocates once, up front, and pins the buffer: from then on no call
+    allocates, a call that needs more raises instead of reallocating, and the buffer's
+    address never changes -- what a HIP graph captured over calls on it relies on.
     """
 
     def __init__(self, device="cuda"):
         self.device = device
         self.buf = None
+        self.reserved = False
+        self._retired = []  # superseded buffers, kept alive (see get)
+
+    def reserve(self, nbytes: int) -> "DecodeWorkspace":
+        if self.reserved:
+            raise RuntimeError("workspace already reserved")
+        if self.buf is None or self.buf.numel() < nbytes:
+            self._grow(int(nbytes))
+        self.reserved = True
+        return self
+
+    def _grow(self, nbytes: int):
+        # a superseded buffer is never freed: a HIP graph captured over earlier calls still
+        # points at it, and freed memory could be handed to other tensors by the caching
+        # allocator. Growth at least doubles, so few are ever retired.
+        if self.buf is not None:
+            self._retired.append(self.buf)
+        size = max(nbytes, 256, 2 * self.buf.numel() if self.buf is not None else 0)
+        self.buf = torch.empty(size, dtype=torch.uint8, device=self.device)
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            if self.reserved:
+                raise RuntimeError(f"workspace reserved for {self.buf.numel()} bytes; this call needs {nbytes} "
+                                   "(reserve the largest call's size up front)")
+            self._grow(nbytes)
         return self.buf
 
 
@@ -188,18 +215,32 @@ def decode(q, k_cache, v_cache, key_len, cfg: AttnConfig, *, q_gain=None, rope_c
     return out[0] if single and out.dim() == 3 else out
 
 
-def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None, rope_cos=None,
-            rope_sin=None, out=None, out_dtype=torch.float16, q_hilo: bool = False,
-            workspace: DecodeWorkspace | None = None, split: bool = True):
+def _prefill_flags(kv_f32: bool, out_f32: bool, q_hilo: bool) -> int:
+    return (_lib.KV_F32 if kv_f32 else 0) | (_lib.OUT_F32 if out_f32 else 0) | (_lib.Q_HILO if q_hilo else 0)
+
+
+def prefill_ws_bytes(S: int, start_pos: int, cfg: AttnConfig, *, kv_f32: bool = False,
+                     q_hilo: bool = False) -> int:
+    """Workspace bytes a ``prefill`` call of this shape and mode uses (g4a_prefill_ws_bytes):
+    0 for hd 256 on f16 caches at S long enough to run unsplit. Reserve the largest call's."""
+    c = cfg.c(_prefill_flags(kv_f32, False, q_hilo))
+    return int(_lib.load().g4a_prefill_ws_bytes(ctypes.byref(c), int(S), int(start_pos)))
+
+
+def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, workspace: DecodeWorkspace,
+            q_gain=None, rope_cos=None, rope_sin=None, out=None, out_dtype=torch.float16,
+            q_hilo: bool = False, split: bool = True):
     """Causal prefill attention for S tokens at positions start_pos..start_pos+S-1.
 
     q [S][nH][hd] f32 raw; caches [>= start_pos+S][kvH][hd] f16/f32; rope_cos/sin
     [S][hd/2] rows for those positions. Returns out [S][nH][hd] (f16 by default).
     q_hilo keeps the normalised, rotated q at f32 accuracy (two f16 MFMA operands)
-    instead of rounding it to f16 as qprep_b does. Short prompts split long causal rows
-    over workgroups through `workspace` (allocated here when not given); split=False
-    passes no workspace, which the C ABI defines as the unsplit call (one kernel, the
-    q prologue fused in).
+    instead of rounding it to f16 as qprep_b does; on f32 caches it keeps K at f32
+    accuracy too (attn_prefill's form), where q in f16 converts both caches to f16 as the
+    GEMM form's srqh_b does. `workspace` is the caller's scratch (prefill_ws_bytes bytes):
+    f32 caches and hd 512 need it, and short prompts split long causal rows over
+    workgroups through it. split=False runs hd 256 on f16 caches unsplit, without it (one
+    kernel, the q prologue fused in).
     """
     S = q.shape[0]
     if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
@@ -219,12 +260,15 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, q_gain=None
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     _need(out, "out", (torch.float16, torch.float32))
-    flags = (_lib.KV_F32 if k_cache.dtype == torch.float32 else 0) | \
-            (_lib.OUT_F32 if out.dtype == torch.float32 else 0) | (_lib.Q_HILO if q_hilo else 0)
-    c = cfg.c(flags)
+    kv32 = k_cache.dtype == torch.float32
+    c = cfg.c(_prefill_flags(kv32, out.dtype == torch.float32, q_hilo))
     lib = _lib.load()
-    ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos)) if split else 0
-    ws = (workspace or DecodeWorkspace(q.device)).get(ws_bytes) if ws_bytes else None
+    ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos))
+    if not split:
+        if kv32 or cfg.head_dim != 256:
+            raise ValueError("split=False is the hd-256 f16-cache call without a workspace")
+        ws_bytes = 0
+    ws = workspace.get(ws_bytes) if ws_bytes else None
     check(lib.g4a_prefill(ctypes.byref(c), S, int(start_pos), _ptr(q), _ptr(q_gain), _ptr(rope_cos),
                           _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(ws),
                           0 if ws is None else ws.numel(), ctypes.c_void_p(_stream())))
@@ -324,22 +368,25 @@ def kvnorm_b(kraw, vraw, k_norm, cosT, sinT, kc, vc, p, *, S, head_dim, n_kv_hea
              rope_sin=sinT.view(-1, half)[start:start + S], k_in_q=ks, v_in_q=vs)
 
 
-def attn_prefill(q, q_norm, cosT, sinT, kc, vc, out, params, *, head_dim, out_q=0.0, q_f16=False):
+def attn_prefill(q, q_norm, cosT, sinT, kc, vc, out, params, *, head_dim, workspace, out_q=0.0, q_f16=False):
     """attn_prefill (kernels_dsl.py:1950-2098; prefill_gpu.py:347-354): slots [q, q_norm, cosT,
     sinT, k, v, out, params] with params = (startPos, qH, kvH, W, S); cosT/sinT absolute tables
     [max_pos][hd/2]. `out` may be f32 (attn_prefill's own output) or f16 (attnh).
 
-    The fused kernel keeps the normalised, rotated q in f32 (kernels_dsl.py:2007-2014), so
-    this uses the f32-accurate q mode; q_f16=True rounds q to f16 first, as qprep_b does
-    for the GEMM form."""
+    The fused kernel keeps the normalised, rotated q in f32 (kernels_dsl.py:2007-2014) and
+    reads its caches as they are, so this uses the f32-accurate q mode, and on f32 caches
+    scores at f32 accuracy; q_f16=True rounds q (and f32 caches) to f16 first, as qprep_b and
+    srqh_b do for the GEMM form. `workspace` is the runner-owned scratch this drop-in needs
+    beyond the reference's slots (as PrefillGPU owns its qf16 / kf16 / vf16 buffers,
+    prefill_gpu.py:229-256): reserve prefill_ws_bytes of the largest call once and no call
+    allocates."""
     start, qh, kvh, win, S = (int(x) for x in list(params)[:5])
     cfg = AttnConfig(qh, kvh, head_dim, win, 1.0, 1e-6, out_q)
     half = head_dim // 2
     maxseq = kc.numel() // (kvh * head_dim)
     prefill(q.view(S, qh, head_dim), kc.view(maxseq, kvh, head_dim), vc.view(maxseq, kvh, head_dim),
-            start, cfg, q_gain=q_norm, rope_cos=cosT.view(-1, half)[start:start + S],
-            rope_sin=sinT.view(-1, half)[start:start + S], out=out.view(S, qh, head_dim),
-            q_hilo=not q_f16)
+            start, cfg, workspace=workspace, q_gain=q_norm, rope_cos=cosT.view(-1, half)[start:start + S],
+            rope_sin=sinT.view(-1, half)[start:start + S], out=out.view(S, qh, head_dim), q_hilo=not q_f16)
     return out
 
 
@@ -355,9 +402,10 @@ def qprep_b(q, q_norm, cosT, sinT, qf16, p, *, S, head_dim):
 
 
 def attn_gemm(q, q_norm, cosT, sinT, kc, vc, attnh, *, S, start_pos, n_q_heads, n_kv_heads,
-              head_dim, window, o_in):
+              head_dim, window, o_in, workspace):
     """PrefillGPU._attn_gemm (prefill_gpu.py:259-313): writes attnh f16 [S][nH*hd] =
-    f16(srq(softmax(qf16 . kf16^T) . vf16, o_in)) in one fused kernel."""
+    f16(srq(softmax(qf16 . kf16^T) . vf16, o_in)) in one fused kernel (f32 caches are
+    converted to f16 first, as its srqh_b does). `workspace` as for attn_prefill."""
     return attn_prefill(q, q_norm, cosT, sinT, kc, vc, attnh,
                         (start_pos, n_q_heads, n_kv_heads, window, S), head_dim=head_dim, out_q=o_in,
-                        q_f16=True)
+                        q_f16=True, workspace=workspace)

@@ -1,24 +1,28 @@
-// Batched causal prefill attention for gfx950 on f16 MFMA (v_mfma_f32_16x16x32_f16).
+// Batched causal prefill attention for gfx950 on f16 MFMA (v_mfma_f32_32x32x16_f16).
 //
 // Reference semantics: PrefillGPU._attn_gemm (gemma4_150/prefill_gpu.py:259-313) --
 // qprep_b rounds the RMSNorm'd, rotated q to f16 (kernels_dsl.py:1837-1873), scores
 // are q.k (scale 1.0 for Gemma 4), smax_b masks each row to [max(0, p+1-W), p]
 // (:1898-1908), P.V, attnout_b divides by the row sum and applies srq(o_in)
-// (:1752-1763). attn_prefill (:1950-2098) is the fused f32 form with the same mask.
+// (:1752-1763). attn_prefill (:1950-2098) is the fused f32 form with the same mask, on
+// f32 q and f32 caches.
 //
 // MI355X design: flash attention with an online softmax instead of the reference's
-// materialised [S*nH][T] score matrix. A workgroup owns one kv head and BQ = 64/G
-// query positions, i.e. 64 query columns = all G heads of the GQA group x BQ
-// positions, so each K/V tile staged in LDS serves every head that reads it. Each of
-// the 4 waves owns 16 columns. Scores are computed transposed, S^T = K . Q^T
-// (A = K tile from LDS, B = Q^T held in registers), which leaves every lane with 4
-// keys of ONE query column -- exactly the B-operand layout the P.V product needs
-// when it is also computed transposed, O^T = V^T . P^T. V stays row-major in LDS and
-// its transposed A operand comes from ds_read_tr16_b64. K/V tiles are double
-// buffered in LDS: the next tile's global loads are in flight while the current one
-// is computed. Scores stay f32 in the MFMA accumulators; P is rounded to f16 only as
-// the MFMA operand. Tiles wholly outside [max(0, p0+1-W), p_last] are skipped;
-// boundary tiles are masked per element. Work-groups are launched longest-causal-row first.
+// materialised [S*nH][T] score matrix. A workgroup owns one kv head and a block of query
+// columns (all G heads of the GQA group x the block's positions), so each K/V tile staged
+// in LDS serves every head that reads it. Scores are computed transposed, S^T = K . Q^T
+// (A = K tile from LDS, B = Q^T held in registers), which leaves every lane with keys of
+// ONE query column -- exactly the B-operand layout the P.V product needs when it is also
+// computed transposed, O^T = V^T . P^T. V stays row-major in LDS and its transposed A
+// operand comes from ds_read_tr16_b64. K/V tiles are DMA'd straight into LDS, double
+// buffered. Scores stay f32 in the MFMA accumulators; P is rounded to f16 only as the MFMA
+// operand. Tiles wholly outside [max(0, p0+1-W), p_last] are skipped; boundary tiles are
+// masked per element. Workgroups are launched longest-causal-row first.
+//
+// Precision modes: q in f16 (qprep_b's rounding point, the GEMM form), or f32-accurate as
+// the f16 pair (q_hi, q_lo) (G4A_Q_HILO, attn_prefill's f32 q). f32 caches (G4A_KV_F32) are
+// converted to f16 as the GEMM form's srqh_b does, and with G4A_Q_HILO (attn_prefill on its
+// own f32 caches) K is kept as the f16 pair (k_hi, k_lo), so the scores are f32-accurate.
 #include "common.hpp"
 
 namespace g4a {
@@ -41,6 +45,7 @@ struct PrefillArgs {
     const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
     const half_t* q16lo;  // ... and with G4A_Q_HILO its f16 low parts (q - f32(q16))
     int kv_row0;  // prefill_kernel_w32: first row held in kc/vc (rows below it are never read)
+    const void* kclo;  // f32 caches: the f16 low parts k - f32(f16(k)) of the f16 K copy in kc
     half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
                       // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
     float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
@@ -51,24 +56,6 @@ struct PrefillArgs {
 // measured within +-2 % at S 1024 and S 8192
 constexpr int kQkAhead = 4;
 constexpr int kPvAhead = 3;
-template <int HD>
-struct PrefillShape {
-    static constexpr int KT = HD == 512 ? 32 : 64;  // keys per LDS tile
-    static constexpr int KSTEPS = HD / 32;           // MFMA k-steps of the score product
-    static constexpr int NKT = KT / 16;              // 16-key sub-tiles of S^T
-    static constexpr int NU = KT / 32;               // 32-key k-steps of the P.V product
-    static constexpr int NDT = HD / 16;              // 16-dim tiles of O^T
-    static constexpr int KS = HD + 8;                // K row stride (halves): A reads conflict-free
-    static constexpr int VS = HD + 16;               // V row stride (halves): transpose reads conflict-free
-    static constexpr int CH = HD / 8;                // 16 B chunks per row
-    static constexpr int PER = KT * CH / 256;        // chunks of K (and of V) per thread per tile
-    static constexpr int STAGE = KT * KS + KT * VS;  // halves per pipeline stage
-};
-
-__device__ __forceinline__ float4v mfma16(half8 a, half8 b, float4v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
 // 4 halves of a row-major LDS tile transposed across each 16-lane group: lane n of the
 // group receives element n%4 of the 8-byte chunks supplied by lanes n/4 + 4j (j < 4).
 __device__ __forceinline__ half4 lds_tr16(const half_t* p) {
@@ -106,173 +93,10 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
     }
 }
 
-template <int HD, int G, typename KVT, typename OUTT, bool HILO>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-    using Sh = PrefillShape<HD>;
-    constexpr int KT = Sh::KT, KSTEPS = Sh::KSTEPS, NKT = Sh::NKT, NU = Sh::NU, NDT = Sh::NDT;
-    constexpr int KS = Sh::KS, VS = Sh::VS;
-    constexpr int BQ = 64 / G;
-
-    constexpr int CH = Sh::CH, PER = Sh::PER;
-    __shared__ __attribute__((aligned(16))) half_t stage[2 * Sh::STAGE];  // [buf]{K[KT][KS], V[KT][VS]}
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = lane & 15, g = lane >> 4;
-    const int qb = a.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
-    const int kh = blockIdx.y;
-    const int T_total = a.start_pos + a.S;
-
-    // ---- this lane's query column: head hh of the group, position offset po
-    const int qc = 16 * wave + n;
-    const int hh = qc / BQ, po = qc % BQ;
-    const int s_raw = qb * BQ + po;
-    const bool col_ok = s_raw < a.S;
-    const int s_idx = col_ok ? s_raw : a.S - 1;
-    const int pos = a.start_pos + s_idx;
-    const int h = kh * G + hh;
-
-    // ---- q prologue: RMSNorm*gain, RoPE, f16; lane holds dims 32s + 8g + i
-    half8 qf[KSTEPS], ql[HILO ? KSTEPS : 1];
-    {
-        float x[KSTEPS][8];
-        prep_q_column<HD>(a.q + ((size_t)s_idx * a.n_q_heads + h) * HD, a.q_gain ? a.q_gain : kOnes,
-                          a.rcos ? a.rcos + (size_t)s_idx * (HD / 2) : kOnes,
-                          a.rsin ? a.rsin + (size_t)s_idx * (HD / 2) : kZeros, a.q_gain != nullptr, a.eps, g, x);
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const half_t hv = col_ok ? (half_t)x[s][i] : (half_t)0.0f;
-                qf[s][i] = hv;
-                if constexpr (HILO) ql[s][i] = col_ok ? (half_t)(x[s][i] - (float)hv) : (half_t)0.0f;
-            }
-    }
-
-    // ---- key range of the workgroup and of this column
-    const int p0 = a.start_pos + qb * BQ;
-    const int kv_hi = min(p0 + BQ, T_total);
-    const int wg_lo = (a.window > 0) ? max(0, p0 + 1 - a.window) : 0;
-    const int col_lo = (a.window > 0) ? pos + 1 - a.window : 0;
-    const size_t rstride = (size_t)a.n_kv_heads * HD;
-    const KVT* kcb = reinterpret_cast<const KVT*>(a.kc) + (size_t)kh * HD;
-    const KVT* vcb = reinterpret_cast<const KVT*>(a.vc) + (size_t)kh * HD;
-
-    float4v oacc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = float4v{0, 0, 0, 0};
-    float m_run = kNegInf, l_run = 0.0f;
-
-    // ---- K/V tile staging: thread chunk r covers row (tid + 256r) / CH, chunk (tid + 256r) % CH
-    half8 kst[PER], vst[PER];
-    auto load_tile = [&](int t0) {
-#pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int idx = tid + 256 * r, row = idx / CH, ch = idx % CH;
-            const int key = min(t0 + row, T_total - 1);  // rows past the prompt are masked
-            kst[r] = load8h(kcb + (size_t)key * rstride + 8 * ch);
-            vst[r] = load8h(vcb + (size_t)key * rstride + 8 * ch);
-        }
-    };
-    auto store_tile = [&](int buf) {
-        half_t* Kb = stage + buf * Sh::STAGE;
-        half_t* Vb = Kb + KT * KS;
-#pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int idx = tid + 256 * r, row = idx / CH, ch = idx % CH;
-            *reinterpret_cast<half8*>(&Kb[row * KS + 8 * ch]) = kst[r];
-            *reinterpret_cast<half8*>(&Vb[row * VS + 8 * ch]) = vst[r];
-        }
-    };
-
-    const int t_first = (wg_lo / KT) * KT;
-    const int ntiles = (kv_hi - t_first + KT - 1) / KT;  // >= 1: kv_hi > wg_lo
-    load_tile(t_first);
-    store_tile(0);
-    __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
-        const int t0 = t_first + it * KT, buf = it & 1;
-        if (it + 1 < ntiles) load_tile(t0 + KT);  // in flight during this tile's math
-        const half_t* Kb = stage + buf * Sh::STAGE;
-        const half_t* Vb = Kb + KT * KS;
-
-        // S^T = K . Q^T : sacc[kt][i] = score(key t0+16kt+4g+i, column n)
-        float4v sacc[NKT];
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            float4v c4 = float4v{0, 0, 0, 0};
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s) {
-                const half8 av = *reinterpret_cast<const half8*>(&Kb[(16 * kt + n) * KS + 32 * s + 8 * g]);
-                c4 = mfma16(av, qf[s], c4);
-                if constexpr (HILO) c4 = mfma16(av, ql[s], c4);
-            }
-            sacc[kt] = c4;
-        }
-        // scale (log2 domain), mask, online softmax
-        float mt = kNegInf;
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = t0 + 16 * kt + 4 * g + i;
-                const bool ok = key <= pos && key >= col_lo;
-                const float sv = ok ? sacc[kt][i] * a.scale_log2 : kNegInf;
-                sacc[kt][i] = sv;
-                mt = fmaxf(mt, sv);
-            }
-        mt = max32(max16(mt));
-        const float m_new = fmaxf(m_run, mt);
-        const float base = (m_new == kNegInf) ? 0.0f : m_new;
-        const float corr = fexp2(m_run - base);
-        float ps = 0.0f;
-        half8 pf[NU];
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = fexp2(sacc[kt][i] - base);
-                ps += p;
-                pf[kt >> 1][(kt & 1) * 4 + i] = (half_t)p;
-            }
-        l_run = l_run * corr + ps;
-        m_run = m_new;
-        if (__any(corr != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= corr;
-        }
-
-        // O^T += V^T . P^T; lane n of group g supplies V[32u + 4g + n/4 (+16)][16dt + 4(n%4)..]
-#pragma unroll
-        for (int u = 0; u < NU; ++u) {
-            const half_t* v0 = Vb + (32 * u + 4 * g + (n >> 2)) * VS + 4 * (n & 3);
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const half4 lo4 = lds_tr16(v0 + 16 * dt);
-                const half4 hi4 = lds_tr16(v0 + 16 * VS + 16 * dt);
-                const half8 av = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                oacc[dt] = mfma16(av, pf[u], oacc[dt]);
-            }
-        }
-        if (it + 1 < ntiles) store_tile(buf ^ 1);
-        __syncthreads();
-    }
-
-    // ---- epilogue: row sum over the 4 lane groups, normalise, srq, store
-    float l_tot = l_run;
-    l_tot = add32(add16(l_tot));
-    const float inv_l = 1.0f / l_tot;
-    if (!col_ok) return;
-    OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + h) * HD;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_elem(orow + 16 * dt + 4 * g + i, srq(oacc[dt][i] * inv_l, a.out_q));
-}
-
-// ---------------------------------------------------------------- hd 256 / f16 cache path
-// prefill_kernel_w32: the same attention with 32 query columns per wave (128 per workgroup:
-// G heads x 128/G positions) on v_mfma_f32_32x32x16_f16, which halves the LDS bytes each
-// MFMA FLOP costs compared with 16 columns per wave. K/V tiles of 64 keys go straight from
+// ---------------------------------------------------------------- hd 256
+// prefill_kernel_w32: 32 query columns per wave (128 per workgroup: G heads x 128/G
+// positions) on v_mfma_f32_32x32x16_f16, so each K or V operand read from LDS feeds a
+// 32-column MFMA (16 columns would double the LDS bytes per FLOP). K/V tiles of 64 keys go straight from
 // HBM into LDS (buffer_load ... lds, 16 B per lane, no staging registers), double buffered,
 // one barrier per tile. LDS rows are 512 B with the 16-byte chunk c of row r stored at a
 // swizzled position: c ^ (r % 32) for K, whose reads take one chunk of 32 consecutive rows,
@@ -351,13 +175,19 @@ __device__ __forceinline__ PrefillUnit prefill_unit(const PrefillArgs& a, int la
     return PrefillUnit{kh, qb, piece, n_pieces};
 }
 
-template <int G, typename OUTT, bool HILO>
+template <int G, typename OUTT, bool HILO, bool KLO>
 __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
     constexpr int QMF = HILO ? 2 : 1;  // score MFMAs per K operand (q high, then low parts)
+    constexpr int RPU = KLO ? 2 : 1;   // LDS reads per K operand (K high, then low parts)
+    constexpr int MPU = QMF + (KLO ? 1 : 0);  // score MFMAs per K operand pair
+    constexpr int NB = KLO ? 2 : 4;    // K operands read per batch
+    constexpr int AHEAD = KLO ? 2 : kQkAhead;
     constexpr int ROWB = HD * 2;      // bytes per LDS tile row
     constexpr int TILEB = KT * ROWB;  // one K or V tile
-    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
+    // [buffer][K, V]; with KLO one more tile: the K low parts of the current tile, single
+    // buffered (refilled once every wave has formed its scores)
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB + (KLO ? TILEB : 0)];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -405,7 +235,18 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(d + TILEB), 16, vvo, 0, 0, 0);
         }
     };
-
+    // K low parts of tile t into their own stage, in K's layout (8 instructions a wave)
+    const rsrc_t rkl = make_rsrc(KLO ? reinterpret_cast<const half_t*>(a.kclo) + (size_t)kh * HD : nullptr,
+                                 KLO ? (uint32_t)(kv_hi - a.kv_row0) * rowg : 0u);
+    auto issue_klo = [&](int t) {
+        const int kb = wg_lo + t * KT - a.kv_row0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 16 * wave + 2 * j + h;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rkl, (__attribute__((address_space(3))) void*)(lds + 4 * TILEB + (16 * wave + 2 * j) * ROWB),
+                                                     16, (kb + r) * rowg + 16 * (n32 ^ (r & 31)), 0, 0, 0);
+        }
+    };
 
     // ---- q prologue: lane (column, h) holds dims 16s + 8h + i (s < 16, i < 8), the B
     // operand layout of the 32x32x16 MFMA. The arithmetic, including the order of the
@@ -427,9 +268,11 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
                                                      16, qo, 0, 0, 0);
         }
         if (t0 < t1) issue(t0, t0 & 1);
-        // the 16 q DMAs were issued before tile t0's 16: they are done at vmcnt <= 16
-        if (t0 < t1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (KLO && t0 < t1) issue_klo(t0);
+        // the 16 q DMAs were issued before tile t0's 16 (+ 8 K low): done at vmcnt <= 16 (24)
+        if (t0 >= t1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if constexpr (KLO) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         const char* qrow = qs + c * ROWB;
 #pragma unroll
         for (int s = 0; s < 16; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
@@ -501,8 +344,11 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         // the first K/V tile is issued behind the q operands (loads complete in order), so
         // it lands while q is prepared without delaying the q data
         if (t0 < t1) issue(t0, t0 & 1);
-        if (t0 < t1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // all but tile t0's 16
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (KLO && t0 < t1) issue_klo(t0);
+        // all but tile t0's 16 (+ 8 K low)
+        if (t0 >= t1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if constexpr (KLO) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __syncthreads();  // every wave's share of the LDS operands
         const float* gl = reinterpret_cast<const float*>(shr) + 8 * h;
         auto gain8 = [&](int s) {
@@ -598,40 +444,63 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         __syncthreads();                                    // all parts; tile t-1 fully consumed
         if (t + 1 < t1) issue(t + 1, (t + 1) & 1);
         const int kb = wg_lo + t * KT;
-        if (kb > wp1 || kb + KT - 1 < w_lo) continue;  // no key of this tile for this wave
+        const bool live = !(kb > wp1 || kb + KT - 1 < w_lo);  // a key of this tile for this wave
+        if constexpr (!KLO) {
+            if (!live) continue;
+        }
         const char* K = lds + (t & 1) * 2 * TILEB;
         const char* V = K + TILEB;
 
         // S^T = K . Q^T: two 32-key sub-tiles, 16 k-steps of 16 dims. The two accumulator
         // chains alternate (a chain of dependent MFMAs issues at half rate), and the A
-        // operands are read in batches ahead of their MFMAs.
+        // operands are read in batches ahead of their MFMAs. With KLO each K operand is the
+        // f16 pair (high, low) of an f32 cache row, and q . k = q . k_hi + q . k_lo to f32
+        // accuracy: one more MFMA per operand.
         float16v sacc[2] = {float16v{}, float16v{}};
-        const char* krow0 = K + n32 * ROWB;
-        const char* krow1 = K + (32 + n32) * ROWB;
+        if (live) {
+            const char* krow0 = K + n32 * ROWB;
+            const char* krow1 = K + (32 + n32) * ROWB;
+            const char* klrow0 = lds + 4 * TILEB + n32 * ROWB;
+            const char* klrow1 = klrow0 + 32 * ROWB;
 #pragma unroll
-        for (int s0 = 0; s0 < 16; s0 += 4) {
-            half8 kv0[4], kv1[4];
+            for (int s0 = 0; s0 < 16; s0 += NB) {
+                half8 kv0[NB], kv1[NB], kl0[KLO ? NB : 1], kl1[KLO ? NB : 1];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                kv0[s] = *reinterpret_cast<const half8*>(krow0 + 16 * ((2 * (s0 + s) + h) ^ n32));
-                kv1[s] = *reinterpret_cast<const half8*>(krow1 + 16 * ((2 * (s0 + s) + h) ^ n32));
+                for (int s = 0; s < NB; ++s) {
+                    const int cb = 16 * ((2 * (s0 + s) + h) ^ n32);
+                    kv0[s] = *reinterpret_cast<const half8*>(krow0 + cb);
+                    kv1[s] = *reinterpret_cast<const half8*>(krow1 + cb);
+                    if constexpr (KLO) {
+                        kl0[s] = *reinterpret_cast<const half8*>(klrow0 + cb);
+                        kl1[s] = *reinterpret_cast<const half8*>(klrow1 + cb);
+                    }
+                }
+#pragma unroll
+                for (int s = 0; s < NB; ++s) {
+                    sacc[0] = mfma32(kv0[s], qf[s0 + s], sacc[0]);
+                    if constexpr (HILO) sacc[0] = mfma32(kv0[s], ql[s0 + s], sacc[0]);
+                    sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
+                    if constexpr (HILO) sacc[1] = mfma32(kv1[s], ql[s0 + s], sacc[1]);
+                    if constexpr (KLO) {
+                        sacc[0] = mfma32(kl0[s], qf[s0 + s], sacc[0]);
+                        sacc[1] = mfma32(kl1[s], qf[s0 + s], sacc[1]);
+                    }
+                }
             }
+            // keep AHEAD LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
+            __builtin_amdgcn_sched_group_barrier(0x100, RPU * AHEAD, 0);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                sacc[0] = mfma32(kv0[s], qf[s0 + s], sacc[0]);
-                if constexpr (HILO) sacc[0] = mfma32(kv0[s], ql[s0 + s], sacc[0]);
-                sacc[1] = mfma32(kv1[s], qf[s0 + s], sacc[1]);
-                if constexpr (HILO) sacc[1] = mfma32(kv1[s], ql[s0 + s], sacc[1]);
+            for (int i = 0; i < 32 - AHEAD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, MPU, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, RPU, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x008, MPU * AHEAD, 0);
         }
-        // keep kQkAhead LDS reads ahead of the score MFMAs (masks: 0x100 DS read, 0x008 MFMA)
-        __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);
-#pragma unroll
-        for (int i = 0; i < 32 - kQkAhead; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, QMF, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if constexpr (KLO) {
+            __syncthreads();  // every wave has its scores: the K low stage takes tile t + 1
+            if (t + 1 < t1) issue_klo(t + 1);
+            if (!live) continue;
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, QMF * kQkAhead, 0);
 
         // scores of this lane: key kb + 4h + 32kt + 8(r/4) + r%4 of its column, log2 domain;
         // tiles inside every column's range skip the per-element mask
@@ -746,13 +615,17 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 // the hd-256 kernel. Tiles of 32 keys (1 KiB rows: K and V 32 KiB each, double buffered:
 // 128 KiB of LDS, plus 16 KiB for the score exchange) are DMA'd as in prefill_kernel_w32.
 // q comes prepared in f16 (qprep_kernel; the RoPE pairs (i, i + 256) would span both waves).
-template <int G, typename OUTT, bool HILO>
+template <int G, typename OUTT, bool HILO, bool KLO>
 __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
     constexpr int HD = 512, KT = 32, NCOL = 64, BQ = NCOL / G;
     constexpr int QMF = HILO ? 2 : 1;
+    constexpr int MPU = QMF + (KLO ? 1 : 0);  // score MFMAs per K operand (pair)
     constexpr int ROWB = HD * 2;      // 1 KiB rows
     constexpr int TILEB = KT * ROWB;  // one K or V tile: 32 KiB
-    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB + 4 * 4096];  // [buffer][K, V], exchange
+    // [buffer][K, V], then the score exchange (16 KiB); with KLO that last region is a whole
+    // tile and holds the K low parts of the current tile until every wave has formed its
+    // scores, then the exchange, then the next tile's K low parts (160 KiB in all)
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB + (KLO ? TILEB : 4 * 4096)];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -797,6 +670,17 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
                                                      16, (kb + r) * rowg + 16 * (lane ^ vswz(r)), 0, 0, 0);
         }
     };
+    const rsrc_t rkl = make_rsrc(KLO ? reinterpret_cast<const half_t*>(a.kclo) + (size_t)kh * HD : nullptr,
+                                 KLO ? (uint32_t)(kv_hi - a.kv_row0) * rowg : 0u);
+    auto issue_klo = [&](int t) {
+        const int kb = wg_lo + t * KT - a.kv_row0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * wave + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rkl, (__attribute__((address_space(3))) void*)(lds + 4 * TILEB + r * ROWB), 16,
+                                                     (kb + r) * rowg + 16 * (lane ^ (r & 31)), 0, 0, 0);
+        }
+    };
 
     // ---- q: lane (column c, half h) holds dims 256 dh + 16s + 8h .. +7 (s < 16), the B
     // operand layout; the loads go out before the first tile's
@@ -812,6 +696,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
             for (int s = 0; s < 16; ++s) ql[s] = bload_h8(rql, qo + 32 * s);
         }
         if (t0 < t1) issue(t0, t0 & 1);
+        if (KLO && t0 < t1) issue_klo(t0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (!col_ok) {
 #pragma unroll
@@ -855,41 +740,58 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
         const char* V = K + TILEB;
         float16v sacc = float16v{};
         if (live) {
-            // S_dh^T = K_dh . Q_dh^T over 16 k-steps of 16 dims
+            // S_dh^T = K_dh . Q_dh^T over 16 k-steps of 16 dims (with KLO, K high then low parts)
             const char* krow = K + n32 * ROWB;
+            const char* klrow = lds + 4 * TILEB + n32 * ROWB;
 #pragma unroll
             for (int s0 = 0; s0 < 16; s0 += 4) {
-                half8 kv[4];
+                half8 kv[4], kl[KLO ? 4 : 1];
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    kv[s] = *reinterpret_cast<const half8*>(krow + 16 * ((32 * dh + 2 * (s0 + s) + h) ^ n32));
+                for (int s = 0; s < 4; ++s) {
+                    const int cb = 16 * ((32 * dh + 2 * (s0 + s) + h) ^ n32);
+                    kv[s] = *reinterpret_cast<const half8*>(krow + cb);
+                    if constexpr (KLO) kl[s] = *reinterpret_cast<const half8*>(klrow + cb);
+                }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     sacc = mfma32(kv[s], qf[s0 + s], sacc);
                     if constexpr (HILO) sacc = mfma32(kv[s], ql[s0 + s], sacc);
+                    if constexpr (KLO) sacc = mfma32(kl[s], qf[s0 + s], sacc);
                 }
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            if constexpr (!KLO) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-            for (int i = 0; i < 14; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, QMF, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int i = 0; i < 14; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, MPU, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * MPU, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * QMF, 0);
+        }
+        if constexpr (KLO) __syncthreads();  // K low parts consumed: the exchange may overwrite them
+        if (live) {
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4)
                 *reinterpret_cast<float4v*>(xme + (r4 * 64 + lane) * 4) =
                     float4v{sacc[4 * r4], sacc[4 * r4 + 1], sacc[4 * r4 + 2], sacc[4 * r4 + 3]};
         }
         __syncthreads();  // the partner's partial scores
-        if (!live) continue;
-        // S = S_0 + S_1 in both waves of the pair (the same sums in the same order)
+        if (live) {
+            // S = S_0 + S_1 in both waves of the pair (the same sums in the same order)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const float4v o = *reinterpret_cast<const float4v*>(xother + (r4 * 64 + lane) * 4);
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const float4v o = *reinterpret_cast<const float4v*>(xother + (r4 * 64 + lane) * 4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sacc[4 * r4 + i] = dh == 0 ? sacc[4 * r4 + i] + o[i] : o[i] + sacc[4 * r4 + i];
+                for (int i = 0; i < 4; ++i) sacc[4 * r4 + i] = dh == 0 ? sacc[4 * r4 + i] + o[i] : o[i] + sacc[4 * r4 + i];
+            }
         }
+        if constexpr (KLO) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __syncthreads();  // every exchange read done: the region takes tile t + 1's K low parts
+            if (t + 1 < t1) issue_klo(t + 1);
+        }
+        if (!live) continue;
         // scores of this lane: key kb + 4h + 8(r/4) + r%4 of its column, log2 domain
         const bool masked = (kb + KT - 1 > wp0) || (a.window > 0 && kb < wp1 + 1 - a.window);
         if (masked) {
@@ -1052,38 +954,25 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     }
 }
 
-template <int HD, int G>
-static void (*pick_w32(bool out32, bool hilo))(PrefillArgs) {
-    if constexpr (HD == 256) {
-        if (hilo) return out32 ? prefill_kernel_w32<G, float, true> : prefill_kernel_w32<G, half_t, true>;
-        return out32 ? prefill_kernel_w32<G, float, false> : prefill_kernel_w32<G, half_t, false>;
-    } else {
-        if (hilo) return out32 ? prefill_kernel_w32d<G, float, true> : prefill_kernel_w32d<G, half_t, true>;
-        return out32 ? prefill_kernel_w32d<G, float, false> : prefill_kernel_w32d<G, half_t, false>;
-    }
-}
-
 typedef void (*prefill_fn)(PrefillArgs);
 
-template <int HD, int G, typename KVT, typename OUTT>
-static prefill_fn pick_hilo(bool hilo) {
-    return hilo ? prefill_kernel<HD, G, KVT, OUTT, true> : prefill_kernel<HD, G, KVT, OUTT, false>;
-}
-template <int HD, int G, typename KVT>
-static prefill_fn pick_out(bool out32, bool hilo) {
-    return out32 ? pick_hilo<HD, G, KVT, float>(hilo) : pick_hilo<HD, G, KVT, half_t>(hilo);
+template <int HD, int G, bool HILO, bool KLO>
+static prefill_fn pick_w32_out(bool out32) {
+    if constexpr (HD == 256) return out32 ? prefill_kernel_w32<G, float, HILO, KLO> : prefill_kernel_w32<G, half_t, HILO, KLO>;
+    else return out32 ? prefill_kernel_w32d<G, float, HILO, KLO> : prefill_kernel_w32d<G, half_t, HILO, KLO>;
 }
 template <int HD, int G>
-static prefill_fn pick_kv(bool kv32, bool out32, bool hilo) {
-    return kv32 ? pick_out<HD, G, float>(out32, hilo) : pick_out<HD, G, half_t>(out32, hilo);
+static prefill_fn pick_w32(bool out32, bool hilo, bool klo) {
+    if (hilo) return klo ? pick_w32_out<HD, G, true, true>(out32) : pick_w32_out<HD, G, true, false>(out32);
+    return klo ? pick_w32_out<HD, G, false, true>(out32) : pick_w32_out<HD, G, false, false>(out32);
 }
 template <int HD>
-static prefill_fn pick_g(int G, bool kv32, bool out32, bool hilo) {
+static prefill_fn pick_g(int G, bool out32, bool hilo, bool klo) {
     switch (G) {
-        case 1: return pick_kv<HD, 1>(kv32, out32, hilo);
-        case 2: return pick_kv<HD, 2>(kv32, out32, hilo);
-        case 4: return pick_kv<HD, 4>(kv32, out32, hilo);
-        case 8: return pick_kv<HD, 8>(kv32, out32, hilo);
+        case 1: return pick_w32<HD, 1>(out32, hilo, klo);
+        case 2: return pick_w32<HD, 2>(out32, hilo, klo);
+        case 4: return pick_w32<HD, 4>(out32, hilo, klo);
+        case 8: return pick_w32<HD, 8>(out32, hilo, klo);
     }
     return nullptr;
 }
@@ -1100,16 +989,15 @@ using namespace g4a;
 struct PrefillSplit {
     int split_tiles, max_pieces, n_qblocks, total_pieces;
     int kv_row0, kv_rows;  // f32 caches: the attended rows copied to f16
-    // workspace layout [K16][V16][q16][q16 low][partials][(m, l)]; base: the bytes the
-    // unsplit call needs, total: with the split
+    // workspace layout [K16][V16][K16 low][q16][q16 low][partials][(m, l)]; base: the bytes
+    // the unsplit call needs, total: with the split
     size_t kv16_bytes, q16_bytes, q16lo_bytes, o_bytes, ml_bytes, base, total;
 };
 // Every mode runs the 32-column kernels (hd 256: prefill_kernel_w32, hd 512:
-// prefill_kernel_w32d) when the workspace holds what they need: f32 caches an f16 copy of
-// the attended rows (the 16-column kernel rounds them to f16 as it stages them, so the
-// operands are the same values); hd 512 its q in f16 (qprep_kernel; with G4A_Q_HILO the low
-// parts too). hd 256 runs unsplit without a workspace (its q prologue fused in); the rest
-// falls back to the 16-column kernel.
+// prefill_kernel_w32d). Some need workspace (base > 0): f32 caches the f16 (K high, V, K
+// low) copy of the attended rows (kv16_kernel); hd 512 its q in f16 (qprep_kernel; with
+// G4A_Q_HILO the low parts too). hd 256 on f16 caches runs unsplit without a workspace
+// (its q prologue fused in).
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -1123,7 +1011,8 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     if (cfg->flags & G4A_KV_F32) {
         p.kv_row0 = W > 0 && start_pos + 1 - W > 0 ? start_pos + 1 - W : 0;
         p.kv_rows = start_pos + S - p.kv_row0;
-        p.kv16_bytes = 2 * align256((size_t)p.kv_rows * kvH * HD * sizeof(half_t));
+        // K high and V; K low with G4A_Q_HILO (the fused form's f32 scores)
+        p.kv16_bytes = (hilo ? 3 : 2) * align256((size_t)p.kv_rows * kvH * HD * sizeof(half_t));
     }
     const size_t q16 = align256((size_t)S * cfg->n_q_heads * HD * sizeof(half_t));
     p.base = p.kv16_bytes + (HD == 512 ? q16 * (hilo ? 2 : 1) : 0);
@@ -1168,16 +1057,30 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
 }
 
 namespace g4a {
-// f32 -> f16 copy (round to nearest even) of n8 groups of 8 cache values, K and V
+// f32 caches as MFMA operands, n8 groups of 8 values: V and K as f16 (round to nearest
+// even), which is the GEMM form's own conversion (srqh_b with step 0 on both caches before
+// the score and P.V GEMMs, prefill_gpu.py:286-288); with klo also the low parts of K,
+// k_lo = f16(k - f16(k)) -- the difference is exact in f32 and f16(k) + k_lo is k to within
+// 2^-22 |k| -- so the fused form (f32 q and f32 caches, attn_prefill) forms q . k_hi + q . k_lo
+// at f32 accuracy: with scale 1.0 and |q.k| in the tens, K rounded to f16 alone moves its
+// scores by ~0.1. V stays f16 in both forms: its rounding (2^-11 relative) is that of P's
+// f16 operand.
 __global__ __launch_bounds__(256) void kv16_kernel(const float* kc, const float* vc, half_t* ko, half_t* vo,
-                                                   size_t n8) {
+                                                   half_t* klo, size_t n8) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n8) return;
     const float4v* k4 = reinterpret_cast<const float4v*>(kc) + 2 * i;
     const float4v* v4 = reinterpret_cast<const float4v*>(vc) + 2 * i;
     const float4v k0 = k4[0], k1 = k4[1], v0 = v4[0], v1 = v4[1];
-    reinterpret_cast<half8*>(ko)[i] = half8{(half_t)k0[0], (half_t)k0[1], (half_t)k0[2], (half_t)k0[3],
-                                            (half_t)k1[0], (half_t)k1[1], (half_t)k1[2], (half_t)k1[3]};
+    const float8v k = float8v{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+    half8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        hi[j] = (half_t)k[j];
+        lo[j] = (half_t)(k[j] - (float)hi[j]);
+    }
+    reinterpret_cast<half8*>(ko)[i] = hi;
+    if (klo) reinterpret_cast<half8*>(klo)[i] = lo;
     reinterpret_cast<half8*>(vo)[i] = half8{(half_t)v0[0], (half_t)v0[1], (half_t)v0[2], (half_t)v0[3],
                                             (half_t)v1[0], (half_t)v1[1], (half_t)v1[2], (half_t)v1[3]};
 }
@@ -1217,24 +1120,18 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     }
     const bool kv32 = (cfg->flags & G4A_KV_F32) != 0, out32 = (cfg->flags & G4A_OUT_F32) != 0;
     const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
-    // the 32-column kernels when the workspace holds what they need (prefill_split), else
-    // the 16-column one
+    // f32 caches need their f16 (K high, V, K low) copy and hd 512 its f16 q in the
+    // workspace (prefill_split's base); hd 256 on f16 caches runs without one
     const PrefillSplit sp = prefill_split(cfg, S, start_pos);
     const bool ws_ok = ws && (uintptr_t)ws % 256 == 0;
-    const bool need_ws = kv32 || HD == 512;
-    const bool w32 = !need_ws || (ws_ok && ws_bytes >= sp.base);
-    const bool split = w32 && sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total;
-    prefill_fn fn = nullptr;
-    if (w32) {
-        switch (G) {
-            case 1: fn = HD == 256 ? pick_w32<256, 1>(out32, hilo) : pick_w32<512, 1>(out32, hilo); break;
-            case 2: fn = HD == 256 ? pick_w32<256, 2>(out32, hilo) : pick_w32<512, 2>(out32, hilo); break;
-            case 4: fn = HD == 256 ? pick_w32<256, 4>(out32, hilo) : pick_w32<512, 4>(out32, hilo); break;
-            case 8: fn = HD == 256 ? pick_w32<256, 8>(out32, hilo) : pick_w32<512, 8>(out32, hilo); break;
-        }
-    } else {
-        fn = HD == 256 ? pick_g<256>(G, kv32, out32, hilo) : pick_g<512>(G, kv32, out32, hilo);
+    if (sp.base > 0 && !(ws_ok && ws_bytes >= sp.base)) {
+        set_error("%s needs a 256-byte aligned workspace of at least %zu bytes (g4a_prefill_ws_bytes), got %zu",
+                  kv32 ? "a prefill on f32 caches" : "an hd-512 prefill", sp.base, ws ? ws_bytes : (size_t)0);
+        return G4A_EWORKSPACE;
     }
+    const bool split = sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total;
+    const bool klo = kv32 && hilo;  // f32 q on f32 caches: K at f32 accuracy as well
+    const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo) : pick_g<512>(G, out32, hilo, klo);
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
@@ -1252,10 +1149,10 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
-    const int BQ = (w32 ? (HD == 256 ? 128 : 64) : 64) / G;
+    const int BQ = (HD == 256 ? 128 : 64) / G;
     a.n_qblocks = (S + BQ - 1) / BQ;
-    if (w32 && ((int64_t)(start_pos + S) * cfg->n_kv_heads * HD * 2 > 0x7fffffff ||
-                (int64_t)S * cfg->n_q_heads * HD * 4 > 0x7fffffff)) {
+    if ((int64_t)(start_pos + S) * cfg->n_kv_heads * HD * 2 > 0x7fffffff ||
+        (int64_t)S * cfg->n_q_heads * HD * 4 > 0x7fffffff) {
         set_error("q or cache rows beyond 32-bit buffer offsets");
         return G4A_EINVAL;
     }
@@ -1270,23 +1167,26 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.q16 = nullptr;
     a.q16lo = nullptr;
     a.kv_row0 = 0;
-    char* wsp = (char*)ws;  // workspace layout: [K16][V16][q16][q16 low][partials][(m, l)]
-    if (w32 && kv32) {
-        const size_t half_bytes = sp.kv16_bytes / 2, skip = (size_t)sp.kv_row0 * cfg->n_kv_heads * HD;
+    a.kclo = nullptr;
+    char* wsp = (char*)ws;  // workspace layout: [K16][V16][K16 low][q16][q16 low][partials][(m, l)]
+    if (kv32) {
+        const size_t part = sp.kv16_bytes / (klo ? 3 : 2), skip = (size_t)sp.kv_row0 * cfg->n_kv_heads * HD;
         const size_t n8 = (size_t)sp.kv_rows * cfg->n_kv_heads * HD / 8;
+        half_t* klo16 = klo ? (half_t*)(wsp + 2 * part) : nullptr;
         hipLaunchKernelGGL(kv16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                            reinterpret_cast<const float*>(k_cache) + skip, reinterpret_cast<const float*>(v_cache) + skip,
-                           (half_t*)wsp, (half_t*)(wsp + half_bytes), n8);
+                           (half_t*)wsp, (half_t*)(wsp + part), klo16, n8);
         hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return hip_error(e0, "prefill cache conversion launch");
         a.kc = wsp;
-        a.vc = wsp + half_bytes;
+        a.vc = wsp + part;
+        a.kclo = klo16;
         a.kv_row0 = sp.kv_row0;
     }
     wsp += sp.kv16_bytes;
     // q in f16 for hd 512 always, for hd 256 when the pieces of a split query block share it
     // (qprep_b's kernel, whose f16 values are those of the hd-256 fused prologue)
-    if (w32 && (HD == 512 || split)) {
+    if (HD == 512 || split) {
         const size_t q16b = align256((size_t)S * cfg->n_q_heads * HD * sizeof(half_t));
         half_t* q16 = (half_t*)wsp;
         half_t* q16lo = hilo ? (half_t*)(wsp + q16b) : nullptr;
@@ -1308,7 +1208,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         a.part_o = (half_t*)wsp;
         a.part_ml = (float2*)(wsp + sp.o_bytes);
     }
-    a.xcd_runs = w32 && a.split_tiles == 0 && cfg->window > 0;
+    a.xcd_runs = a.split_tiles == 0 && cfg->window > 0;
     const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
                       : a.xcd_runs      ? dim3(a.n_qblocks * cfg->n_kv_heads)
                                         : dim3(a.n_qblocks, cfg->n_kv_heads);

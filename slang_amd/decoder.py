@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 from .manifest import AttentionStack, Manifest, ManifestError
-from .projection import GemmWorkspace, dequant, gemm16, gemm16_geglu, packed_bits, srqh
+from .projection import GemmWorkspace, dequant, gemm16, gemm16_geglu, gemm16_ws_bytes, packed_bits, srqh
 
 __all__ = ["qgemv", "norm_in", "qgemv_geglu", "qgemv_gelu_mul", "gemv_f16", "rms_norm", "geglu", "embed", "softcap_argmax",
            "embed_rows", "rows_tail", "geglu16", "plegate16", "DecoderStack", "EPS"]
@@ -294,6 +294,7 @@ class DecoderStack:
                                   device=device)
         self.tok = torch.zeros(1, dtype=torch.int32, device=device)
         self.dq16, self._pb = {}, None  # batched prefill: f16 weights and activation buffers
+        self._pb_retired, self._pb_pinned = [], False
 
     def embed_token(self):
         """x = embed(tok), ple_in = ple_input(tok, x), and layer 0's srq'd input norm
@@ -391,10 +392,45 @@ class DecoderStack:
                 "pleproj": dequant(w["pleproj_codes"], w["pleproj_rowscale"], d, H, bits=8)}
         return self.dq16[L]
 
+    def reserve(self, max_S: int, start_pos: int = 0) -> "DecoderStack":
+        """Size every buffer that prefill() of up to max_S tokens at start_pos, step() and
+        generate() use -- the prefill activations, the attention workspace (decode up to the
+        caches' length, prefill at every S <= max_S) and the GEMM workspace -- and pin them.
+        After it no such call allocates a workspace or activation buffer, and one that would
+        need more raises instead of reallocating, so the buffers a HIP graph captured over
+        these calls points at stay its own. Call it before the first capture."""
+        if not 0 < max_S <= self.attn.max_seq - start_pos:
+            raise ValueError(f"max_S {max_S} at start_pos {start_pos} exceeds the {self.attn.max_seq}-row caches")
+        man, lib, H, d = self.man, _lib.load(), self.H, self.d
+        self._prefill_buffers(max_S)
+        self._pb_pinned = True
+        need = 0
+        for cfg in {man.attn_config(L) for L in range(self.nL)}:
+            c = cfg.c(0)
+            need = max(need, lib.g4a_decode_ws_bytes(ctypes.byref(c), 1, self.attn.max_seq))
+            for S in range(1, max_S + 1):
+                need = max(need, lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, start_pos))
+        self.attn.ws.reserve(need)
+        # the K split's scratch of every gemm16 a prefill issues: per-layer embedding
+        # projection, q/k/v, o_proj, down (and gate/up on their own when traced)
+        shapes = {(H, (self.nL * d,))}
+        for s in man.layers:
+            shapes |= {(H, (s.q_dim,) if s.shared else (s.q_dim, man.kv_dim(s.index), man.kv_dim(s.index))),
+                       (s.q_dim, (H,)), (s.intermediate, (H,)), (H, (s.intermediate, s.intermediate))}
+        gneed = max(gemm16_ws_bytes(M, K, ns) for M in range(1, max_S + 1) for K, ns in shapes)
+        self.attn.gemm_ws.reserve(gneed)
+        return self
+
     def _prefill_buffers(self, S: int):
         """Activations of an S-token prefill (flat, kept for later prompts of at most S tokens);
-        returns take(name, *shape), a contiguous view of the first prod(shape) values."""
+        returns take(name, *shape), a contiguous view of the first prod(shape) values. Buffers
+        outgrown by a longer prompt are retired, not freed: a HIP graph captured over an
+        earlier prefill still owns what it points at."""
         if self._pb is None or self._pb["S"] < S:
+            if self._pb_pinned:
+                raise RuntimeError(f"prefill buffers reserved for {self._pb['S']} tokens; this prompt has {S}")
+            if self._pb is not None:
+                self._pb_retired.append(self._pb)
             H, nL, d = self.H, self.nL, self.d
             it = max(s.intermediate for s in self.man.layers)
             qd = max(s.q_dim for s in self.man.layers)

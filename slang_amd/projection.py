@@ -20,7 +20,8 @@ from . import _lib
 from ._lib import check
 from .attention import _need, _ptr, _stream
 
-__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "GemmWorkspace", "gemm16_geglu",
+__all__ = ["dequant", "dq_f16", "qkv_gemv", "qkv_70", "proj", "srqh", "gemm16", "GemmWorkspace", "gemm16_ws_bytes",
+           "gemm16_geglu",
            "prefill_qkv", "packed_bits"]
 
 _WORDS = (torch.int32, torch.uint32)
@@ -157,16 +158,47 @@ def srqh(a, a_in_q: float = 0.0, out=None):
 class GemmWorkspace:
     """Scratch of ``gemm16(..., workspace=)``: per-tile tickets (zero between calls; a new
     buffer is allocated zeroed, and every call leaves them zero) and the f32 partial tiles of
-    the K split. Grows on demand. Calls that may run concurrently need separate workspaces."""
+    the K split. Calls that may run concurrently need separate workspaces.
+
+    Unreserved, it grows on demand; a superseded buffer is kept alive, never freed, so a HIP
+    graph captured over earlier calls still owns what it points at. ``reserve(nbytes)``
+    allocates once and pins the buffer: a later call that needs more raises instead of
+    reallocating."""
 
     def __init__(self, device="cuda"):
         self.device = device
         self.buf = None
+        self.reserved = False
+        self._retired = []
+
+    def reserve(self, nbytes: int) -> "GemmWorkspace":
+        if self.reserved:
+            raise RuntimeError("workspace already reserved")
+        if self.buf is None or self.buf.numel() < nbytes:
+            self._grow(int(nbytes))
+        self.reserved = True
+        return self
+
+    def _grow(self, nbytes: int):
+        if self.buf is not None:
+            self._retired.append(self.buf)
+        size = max(nbytes, _lib.GEMM_TICKET_BYTES, 2 * self.buf.numel() if self.buf is not None else 0)
+        self.buf = torch.zeros(size, dtype=torch.uint8, device=self.device)
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.zeros(max(nbytes, _lib.GEMM_TICKET_BYTES), dtype=torch.uint8, device=self.device)
+            if self.reserved:
+                raise RuntimeError(f"gemm workspace reserved for {self.buf.numel()} bytes; this call needs {nbytes}")
+            self._grow(nbytes)
         return self.buf
+
+
+def gemm16_ws_bytes(M: int, K: int, ns) -> int:
+    """g4a_gemm16_ws_bytes of a gemm16 call with A [M][K] and matrices of ns rows each."""
+    tab = (_lib.G4AGemmMat * len(ns))()
+    for i, n in enumerate(ns):
+        tab[i] = _lib.G4AGemmMat(0, 0, int(n), 0, 0.0, 1.0)
+    return int(_lib.load().g4a_gemm16_ws_bytes(int(M), int(K), len(ns), tab))
 
 
 def _gemm_table(a16, mats):

@@ -88,7 +88,8 @@ def test_config5_layer(window, theta):
 
     # ---- prefill: the cache write of the prompt, then attention
     sa.kv_write(k16, v16, kc, vc, 0, kvcfg, k_gain=kg, rope_cos=cos[:S], rope_sin=sin[:S])
-    outp = sa.prefill(q[:S], kc, vc, 0, cfg, q_gain=qg, rope_cos=cos[:S], rope_sin=sin[:S])
+    outp = sa.prefill(q[:S], kc, vc, 0, cfg, q_gain=qg, rope_cos=cos[:S], rope_sin=sin[:S],
+                      workspace=sa.Workspace(DEV))
     q16 = sa.qprep(q[:S], cfg, q_gain=qg, rope_cos=cos[:S], rope_sin=sin[:S])
     # ---- 256 decode steps with the KV write fused in
     outd = torch.empty(STEPS, NH, HD, device=DEV)

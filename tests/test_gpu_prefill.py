@@ -31,6 +31,7 @@ from helpers import contract_close, f16_ulp_close, gold, srq_close, tie_aware_e2
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+WS = sa.Workspace(DEV)  # grows to the largest call; the cases run one at a time on one stream
 
 
 def t(x):
@@ -38,7 +39,7 @@ def t(x):
 
 
 def run(q, k, v, start, cfg, out_dtype=torch.float16, q_hilo=False, **kw):
-    out = sa.prefill(t(q), t(k), t(v), start, cfg, out_dtype=out_dtype, q_hilo=q_hilo,
+    out = sa.prefill(t(q), t(k), t(v), start, cfg, out_dtype=out_dtype, q_hilo=q_hilo, workspace=WS,
                      **{n: (t(a) if isinstance(a, np.ndarray) else a) for n, a in kw.items()})
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
@@ -222,53 +223,143 @@ def test_mask_sets_exact(S, start, window):
         assert set(np.nonzero(got[s, 1] > 1e-6)[0]) == set(range(lo, p + 1)), f"row {s}"
 
 
+def f32_caches(T, kvH, hd, seed):
+    """f32 caches as the reference runners hold them (kvnorm's f32 rows): N(0,1) rows through
+    the oracle's cache write, stored f32, so almost no value is an f16 grid point."""
+    rng = np.random.default_rng(seed)
+    kr = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    vr = rng.standard_normal((T, kvH, hd)).astype(np.float32)
+    kg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    cos, sin = O.rope_tables(np.arange(T), hd, 1e4)
+    k, v = O.kv_write(kr, vr, kg, cos, sin, cache_dtype=np.float32)
+    assert (k != k.astype(np.float16).astype(np.float32)).mean() > 0.99
+    return k, v
+
+
 def test_f32_cache_and_mirror():
-    """f32 caches (the reference's own cache type) through the attn_prefill slot drop-in."""
+    """The attn_prefill and attn_gemm slot drop-ins on f32 caches (the reference runners' own
+    cache type), each against the form it replaces: attn_prefill (kernels_dsl.py:1950-2098)
+    reads f32 q and the f32 caches as they are; attn_gemm (prefill_gpu.py:259-313) rounds q
+    (qprep_b) and both caches (srqh_b, :286-288) to f16 before its GEMMs."""
     z = gold("prefill.npz")
-    S, start, hd, nH, kvH = 24, int(z["start_pos"]), 256, 4, 2
+    S, start, hd, nH, kvH, W = 24, int(z["start_pos"]), 256, 4, 2, 16
     cosT, sinT = O.rope_tables(np.arange(64), hd, 1e4)
     cosT[start:start + S], sinT[start:start + S] = z["cos"], z["sin"]
+    k32, v32 = f32_caches(start + S, kvH, hd, 17)
     out = torch.zeros(S * nH * hd, device=DEV, dtype=torch.float32)
-    sa.attn_prefill(t(z["q"].reshape(-1)), t(z["w"]), t(cosT), t(sinT),
-                    t(z["k"].astype(np.float32).reshape(-1)), t(z["v"].astype(np.float32).reshape(-1)),
-                    out, (start, nH, kvH, 16, S), head_dim=hd)
+    sa.attn_prefill(t(z["q"].reshape(-1)), t(z["w"]), t(cosT), t(sinT), t(k32.reshape(-1)), t(v32.reshape(-1)),
+                    out, (start, nH, kvH, W, S), head_dim=hd, workspace=WS)
     torch.cuda.synchronize()
-    contract_close(out.cpu().numpy().reshape(S, nH, hd), z["expected_w16"], "attn_prefill mirror")
+    ref = O.prefill_attention(z["q"], k32, v32, start, kvH, q_gain=z["w"], cos=z["cos"], sin=z["sin"], window=W,
+                              q_round_f16=False)
+    contract_close(out.cpu().numpy().reshape(S, nH, hd), ref, "attn_prefill mirror, f32 caches")
     out16 = torch.zeros(S * nH * hd, device=DEV, dtype=torch.float16)
-    sa.attn_gemm(t(z["q"].reshape(-1)), t(z["w"]), t(cosT), t(sinT),
-                 t(z["k"].astype(np.float32).reshape(-1)), t(z["v"].astype(np.float32).reshape(-1)),
-                 out16, S=S, start_pos=start, n_q_heads=nH, n_kv_heads=kvH, head_dim=hd, window=16, o_in=0.0)
+    sa.attn_gemm(t(z["q"].reshape(-1)), t(z["w"]), t(cosT), t(sinT), t(k32.reshape(-1)), t(v32.reshape(-1)),
+                 out16, S=S, start_pos=start, n_q_heads=nH, n_kv_heads=kvH, head_dim=hd, window=W, o_in=0.0,
+                 workspace=WS)
     torch.cuda.synchronize()
-    contract_close(out16.float().cpu().numpy().reshape(S, nH, hd), z["expected_q16_w16"], "attn_gemm mirror")
+    cfg = sa.AttnConfig(nH, kvH, hd, W)
+    q16 = kernel_q16(z["q"], cfg, z["w"], z["cos"], z["sin"]).astype(np.float32)
+    ref16 = O.prefill_attention(q16, k32, v32, start, kvH, window=W, kv_round_f16=True)
+    contract_close(out16.float().cpu().numpy().reshape(S, nH, hd), ref16, "attn_gemm mirror, f32 caches")
 
 
-@pytest.mark.parametrize("S,start,window", [(1024, 0, 0), (1024, 0, 512), (700, 900, 512), (300, 50, 0)])
-def test_f32_caches_on_the_32_column_kernel(S, start, window):
-    """With a workspace, f32 caches run the 32-column kernel on an f16 copy of the attended
-    rows (from max(0, start+1-W)): the copy rounds as the 16-column kernel's staging does, so
-    the output equals the f16-cache call's bit for bit, in both q modes. Without a workspace
-    (the 16-column kernel on the f32 rows) the output meets the contract against the oracle
-    on the f16-rounded caches."""
-    hd, nH, kvH, T = 256, 8, 2, start + S
-    rng = np.random.default_rng(S + start + window)
+@pytest.mark.parametrize("S,start,window,hd", [(1024, 0, 0, 256), (1024, 0, 512, 256), (700, 900, 512, 256),
+                                               (300, 50, 0, 256), (300, 0, 0, 512), (257, 40, 64, 512)])
+def test_f32_caches(S, start, window, hd):
+    """f32 caches in both forms, against the oracle on the same unrounded f32 caches.
+    * f32 q (attn_prefill's form, G4A_Q_HILO): K enters the score MFMAs as the f16 pair
+      (k_hi, k_lo), so the scores are f32-accurate; the oracle reads q and the caches
+      unrounded. (Rounding K to f16 instead puts thousands of these outputs beyond the
+      contract: with scale 1.0 and |q.k| in the tens a 2^-11 relative error in k moves a
+      score by ~0.1.)
+    * f16 q (the GEMM form): the caches are rounded to f16 as its srqh_b does, so the output
+      equals the call on f16-rounded caches bit for bit and meets the contract against the
+      oracle with that rounding (kv_round_f16).
+    * Without the workspace their f16 copy lives in, the C ABI refuses the call."""
+    nH, kvH = (8, 2) if hd == 256 else (8, 1)
+    T = start + S
+    rng = np.random.default_rng(S + start + window + hd)
     q = rng.standard_normal((S, nH, hd)).astype(np.float32)
     qg = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
-    k32 = rng.standard_normal((T + 2, kvH, hd)).astype(np.float32)  # not f16-representable
-    v32 = rng.standard_normal((T + 2, kvH, hd)).astype(np.float32)
-    k16, v16 = k32.astype(np.float16), v32.astype(np.float16)
+    k32, v32 = f32_caches(T + 2, kvH, hd, S + window)  # rows past T are never attended
     cos, sin = O.rope_tables(np.arange(start, T), hd, 1e4 if window else 1e6)
     cfg = sa.AttnConfig(nH, kvH, hd, window)
     kw = dict(q_gain=qg, rope_cos=cos, rope_sin=sin)
-    for hilo in (False, True):
-        a = run(q, k32, v32, start, cfg, out_dtype=torch.float32, q_hilo=hilo, **kw)
-        b = run(q, k16, v16, start, cfg, out_dtype=torch.float32, q_hilo=hilo, **kw)
-        assert np.array_equal(a, b), f"f32 vs f16 caches, hilo={hilo}: max |d| {np.abs(a - b).max()}"
+    ref32 = O.prefill_attention(q, k32, v32, start, kvH, q_gain=qg, cos=cos, sin=sin, window=window,
+                                q_round_f16=False)
+    got32 = run(q, k32, v32, start, cfg, out_dtype=torch.float32, q_hilo=True, **kw)
+    err = contract_close(got32, ref32, f"f32 q, f32 caches S={S} start={start} W={window} hd={hd}")
+    print(f"f32 q on f32 caches: max |d| {err:.2e}")
     q16 = kernel_q16(q, cfg, qg, cos, sin).astype(np.float32)
-    ref = O.prefill_attention(q16, k16.astype(np.float32), v16.astype(np.float32), start, kvH, window=window)
-    contract_close(run(q, k32, v32, start, cfg, out_dtype=torch.float32, split=False, **kw),
-                   ref, f"f32 caches unsplit S={S} start={start} W={window}")
-    contract_close(run(q, k32, v32, start, cfg, out_dtype=torch.float32, **kw), ref,
-                   f"f32 caches S={S} start={start} W={window}")
+    ref16 = O.prefill_attention(q16, k32, v32, start, kvH, window=window, kv_round_f16=True)
+    got16 = run(q, k32, v32, start, cfg, out_dtype=torch.float32, **kw)
+    contract_close(got16, ref16, f"f16 q, f32 caches S={S} start={start} W={window} hd={hd}")
+    same = run(q, k32.astype(np.float16), v32.astype(np.float16), start, cfg, out_dtype=torch.float32, **kw)
+    assert np.array_equal(got16, same), f"f16 q: f32 vs f16-rounded caches, max |d| {np.abs(got16 - same).max()}"
+    lib = sa._lib.load()
+    c = cfg.c(sa._lib.KV_F32 | sa._lib.OUT_F32 | sa._lib.Q_HILO)
+    qd, kd, vd = t(q), t(k32), t(v32)
+    o = torch.empty(S, nH, hd, device=DEV)
+    rc = lib.g4a_prefill(ctypes.byref(c), S, start, ctypes.c_void_p(qd.data_ptr()), None, None, None,
+                         ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()),
+                         ctypes.c_void_p(o.data_ptr()), None, 0, None)
+    assert rc == -3, f"f32 caches without a workspace: rc {rc}, expected G4A_EWORKSPACE"
+
+
+def test_prefill_mirrors_allocate_nothing():
+    """The runner-owned workspace contract (runner.py:102-109, prefill_gpu.py:229-256: every
+    buffer persistent, kernels never allocate) for the attn_prefill / attn_gemm drop-ins: with
+    the workspace reserved up front (the split partials and the f32 caches' f16 copy of an
+    S 300 call), 10 calls in a row leave torch.cuda.memory_allocated() where it was, and a
+    HIP graph captured over both calls replays -- several times, with the program's own
+    eager work and synchronisations between the replays -- to the eager results bit for bit."""
+    S, start, hd, nH, kvH, W = 300, 0, 256, 8, 2, 0
+    rng = np.random.default_rng(31)
+    q = t(rng.standard_normal((S * nH * hd,)).astype(np.float32))
+    qg = t((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    cosT, sinT = (t(x) for x in O.rope_tables(np.arange(S), hd, 1e6))
+    k32, v32 = (t(x.reshape(-1)) for x in f32_caches(S, kvH, hd, 5))
+    cfg = sa.AttnConfig(nH, kvH, hd, W)
+    need = max(sa.prefill_ws_bytes(S, start, cfg, kv_f32=True, q_hilo=True),
+               sa.prefill_ws_bytes(S, start, cfg, kv_f32=True))
+    assert need > 0
+    ws = sa.Workspace(DEV).reserve(need)
+    out = torch.empty(S * nH * hd, device=DEV)
+    out16 = torch.empty(S * nH * hd, device=DEV, dtype=torch.float16)
+
+    def calls():
+        sa.attn_prefill(q, qg, cosT, sinT, k32, v32, out, (start, nH, kvH, W, S), head_dim=hd, workspace=ws)
+        sa.attn_gemm(q, qg, cosT, sinT, k32, v32, out16, S=S, start_pos=start, n_q_heads=nH, n_kv_heads=kvH,
+                     head_dim=hd, window=W, o_in=0.0, workspace=ws)
+
+    calls()
+    torch.cuda.synchronize()
+    ref, ref16 = out.clone(), out16.clone()
+    before = torch.cuda.memory_allocated()
+    for _ in range(10):
+        calls()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == before, "an eager call allocated device memory"
+    assert torch.equal(out, ref) and torch.equal(out16, ref16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        calls()
+    torch.cuda.synchronize()
+    after_capture = torch.cuda.memory_allocated()
+    for r in range(4):
+        out.zero_()
+        out16.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {r}: attn_prefill output differs from the eager call"
+        assert torch.equal(out16, ref16), f"replay {r}: attn_gemm output differs from the eager call"
+    assert torch.cuda.memory_allocated() == after_capture, "a replay allocated device memory"
+    with pytest.raises(RuntimeError, match="reserved"):
+        ws.get(need + 1)
 
 
 @pytest.mark.parametrize("S", [512, 1024, 2048])

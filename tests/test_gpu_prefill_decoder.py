@@ -196,3 +196,34 @@ def test_generate_is_prefill_then_resident_steps(tmp_path):
     st3 = D.DecoderStack(m, max_seq=64, device=DEV)
     dev = torch.tensor(ids, dtype=torch.int32, device=DEV)
     assert host(st3.generate(dev, 6)).tolist() == want
+
+
+def test_reserved_stack_replays_generate_in_a_graph(tmp_path):
+    """DecoderStack.reserve(max_S) sizes and pins every buffer prefill/step use, so a HIP
+    graph of a whole generate() call replays to the eager tokens -- several times, with eager
+    work between the replays -- without allocating, and a longer prompt afterwards is refused
+    instead of silently reallocating the buffers the graph points at."""
+    write_model(tmp_path, full=True, seed=15, H=256, ple_d=128, vocab=512)
+    m = load_manifest(tmp_path)
+    ids = [int(t) for t in np.random.default_rng(16).integers(0, 512, size=40)]
+    want = host(D.DecoderStack(m, max_seq=64, device=DEV).generate(ids, 6)).tolist()
+    st = D.DecoderStack(m, max_seq=64, device=DEV).reserve(48)
+    dev = torch.tensor(ids, dtype=torch.int32, device=DEV)
+    assert host(st.generate(dev, 6)).tolist() == want  # eager, on the reserved buffers
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        toks = st.generate(dev, 6)
+    torch.cuda.synchronize()
+    mem = torch.cuda.memory_allocated()
+    for r in range(3):
+        toks.fill_(-1)
+        st.tok.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert host(toks).tolist() == want, f"replay {r}"
+    assert torch.cuda.memory_allocated() == mem
+    with pytest.raises(RuntimeError, match="reserved"):
+        st.prefill(list(range(49)), 0)

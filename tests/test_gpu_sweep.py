@@ -14,6 +14,7 @@ from helpers import contract_close
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+WS = sa.Workspace(DEV)  # grows to the largest call; shared by the cases (one stream)
 GROUPS = [(2, 2), (4, 1), (4, 2), (8, 2), (8, 1), (8, 8), (2, 1)]
 
 
@@ -89,7 +90,7 @@ def test_prefill_sweep(i, nH, kvH, hd, S, start, W):
     cfg = sa.AttnConfig(nH, kvH, hd, W)
     q16 = sa.qprep(t(q), cfg, q_gain=t(qg), rope_cos=t(c), rope_sin=t(s))
     out = sa.prefill(t(q), t(k), t(v), start, cfg, q_gain=t(qg), rope_cos=t(c), rope_sin=t(s),
-                     out_dtype=torch.float32)
+                     out_dtype=torch.float32, workspace=WS)
     torch.cuda.synchronize()
     ref = O.prefill_attention(q16.cpu().numpy().astype(np.float32), k, v, start, kvH, window=W)
     contract_close(out.cpu().numpy(), ref, f"case {i}")

@@ -262,6 +262,28 @@ def test_prefill_last_row_equals_decode():
     np.testing.assert_allclose(pre[-1], dec, atol=1e-6)
 
 
+def test_prefill_cache_rounding_is_the_gemm_forms():
+    """kv_round_f16 (the GEMM form's srqh_b on both caches, prefill_gpu.py:286-288) is a no-op
+    on f16 caches, equals the oracle on explicitly f16-rounded f32 caches, and moves the
+    output well beyond the contract with scale 1.0 -- why the fused form (which reads its f32
+    caches as they are) must not round K."""
+    z = load("prefill.npz")
+    S, start = z["q"].shape[0], int(z["start_pos"])
+    kw = dict(q_gain=z["w"], cos=z["cos"], sin=z["sin"], window=16, q_round_f16=False)
+    k16, v16 = z["k"], z["v"]
+    assert k16.dtype == np.float16
+    np.testing.assert_array_equal(O.prefill_attention(z["q"], k16, v16, start, 2, kv_round_f16=True, **kw),
+                                  O.prefill_attention(z["q"], k16, v16, start, 2, **kw))
+    rng = np.random.default_rng(3)
+    k32 = (k16.astype(np.float32) * (1 + 2e-3 * rng.standard_normal(k16.shape))).astype(np.float32)
+    v32 = (v16.astype(np.float32) * (1 + 2e-3 * rng.standard_normal(v16.shape))).astype(np.float32)
+    rounded = O.prefill_attention(z["q"], k32, v32, start, 2, kv_round_f16=True, **kw)
+    np.testing.assert_array_equal(
+        rounded, O.prefill_attention(z["q"], k32.astype(np.float16), v32.astype(np.float16), start, 2, **kw))
+    exact = O.prefill_attention(z["q"], k32, v32, start, 2, **kw)
+    assert np.abs(rounded - exact).max() > 2e-3
+
+
 # ---------------------------------------------------------------- planted mistakes
 def _g4e2b_err(window):
     z = load("g4e2b_decode.npz")
