@@ -20,6 +20,7 @@ min-of-5 at the BLAS default thread count and at one thread.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -492,6 +493,55 @@ def copy_calibration(steps):
                       "launches": steps}), flush=True)
 
 
+def roofline_probes(steps, warmup):
+    """Measured denominators beside the published peaks (the library's roofline probes,
+    g4a_probe_read / g4a_probe_mfma): a read-only stream of 8 MiB, 64 MiB and 512 MiB, each
+    call on a region no call in the previous 1 GiB touched (the MALL flushed first, so every
+    call reads cold from HBM), best over 256-2048 workgroups; and 32x32x16 f16 MFMAs from
+    registers on every SIMD (2 and 4 waves a SIMD, the better). Returns the JSON object."""
+    from slang_amd import _lib
+    lib = _lib.load()
+    sink = torch.empty(lib.g4a_probe_sink_bytes(), dtype=torch.uint8, device="cuda")
+    arena = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+    base = arena.data_ptr()
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe: {lib.g4a_last_error().decode()}")
+
+    def stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    out = {}
+    for mib in (8, 64, 512):
+        size, n = mib << 20, max(2, 1024 // mib)
+        best = None
+        for wg in (256, 512, 1024, 2048):
+            fns = [lambda off=i * size, wg=wg: check(lib.g4a_probe_read(ctypes.c_void_p(base + off), size, wg,
+                                                                         ctypes.c_void_p(sink.data_ptr()), stream()))
+                   for i in range(n)]
+            ms = graph_time_ms(fns, max(n, 16), warmup)
+            if best is None or ms < best[0]:
+                best = (ms, wg)
+        out[f"read_{mib}MiB"] = {"us": round(best[0] * 1e3, 3), "GB/s": round(size / best[0] / 1e6, 1),
+                                 "workgroups": best[1]}
+    iters, best = 2000, None
+    for wgs in (256, 512):  # one or two 512-thread workgroups a CU: 2 or 4 waves a SIMD
+        fn = lambda wgs=wgs: check(lib.g4a_probe_mfma(wgs, iters, ctypes.c_void_p(sink.data_ptr()), stream()))  # noqa: E731
+        ms = graph_time_ms([fn], 4, 1, flush=False)
+        tf = wgs * 8 * iters * 8 * 32768 / (ms * 1e-3) / 1e12
+        if best is None or tf > best[0]:
+            best = (tf, wgs)
+    out["mfma_f16"] = {"TFLOP/s": round(best[0], 1), "workgroups": best[1], "waves_per_simd": best[1] // 128}
+    del arena
+    torch.cuda.empty_cache()
+    return {"hbm_GB/s": out["read_512MiB"]["GB/s"], "read_8MiB_cold_us": out["read_8MiB"]["us"],
+            "mfma_f16_TFLOP/s": out["mfma_f16"]["TFLOP/s"], "detail": out,
+            "note": "measured on this GPU by the library's roofline probes: a read-only 16-byte "
+                    "non-temporal stream (cold: 1 GiB rotation, MALL flushed) and register-operand "
+                    "v_mfma_f32_32x32x16_f16 on every SIMD; the published peaks stay `peak`"}
+
+
 def load_traffic():
     """HBM bytes per decode call from the committed PMC summary (profiles/traffic.json), or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -601,6 +651,8 @@ def main():
                          "or hd 512 (nH 8 / kvH 1, the E2B global layers)")
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config 4 batched decode row (for profiling its kernels)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the measured roofline denominators (read-only stream, MFMA loop)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -632,6 +684,9 @@ def main():
                           "decoder_e2b_prefill": prefill_row(pre), "decoder_e2b_generate": generate_row(gen)}),
               flush=True)
         return
+    if args.roofline_only:
+        print(json.dumps({"peak_measured": roofline_probes(args.steps, args.warmup)}), flush=True)
+        return
     if args.batched_only:
         ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
         print(json.dumps({"decode_4": {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
@@ -656,6 +711,12 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "kernels": "decode_kernel + decode_merge_kernel (one g4a_decode call)"},
     }
+    pm = roofline_probes(args.steps, args.warmup)
+    rec["roofline"].update({"peak_measured": pm["hbm_GB/s"], "frac_measured": round(gbs / pm["hbm_GB/s"], 4),
+                            "floor_8MiB_cold_us": pm["read_8MiB_cold_us"],
+                            "note": "peak_measured: a read-only stream of 512 MiB on this GPU; floor_8MiB_cold_us: "
+                                    "the same stream over the headline's 8 MiB, cold (see peak_measured)"})
+    rec["peak_measured"] = pm
     prefill_host = None
     if not args.only_headline:
         sec = {}
@@ -680,7 +741,8 @@ def main():
                 prefill_host = host
             tf = fl / (msp * 1e-3) / 1e12
             sec[tag] = {"us_per_call": round(msp * 1e3, 3), "TFLOP/s": round(tf, 2),
-                        "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4), "flops": fl,
+                        "mfma_frac": round(tf / F16_PEAK_TFLOPS, 4),
+                        "mfma_frac_measured": round(tf / pm["mfma_f16_TFLOP/s"], 4), "flops": fl,
                         "note": "one 8 MiB cache re-read by every call (MFMA-bound; the cache of a "
                                 "prefill layer was just written by its kv_write)"}
         for mode, mkw in PREFILL_MODES.items():

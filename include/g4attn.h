@@ -63,6 +63,16 @@ typedef struct g4a_cfg {
 const char* g4a_strerror(int code);
 /* Detail of the last failure on the calling thread ("" if none). */
 const char* g4a_last_error(void);
+/*
+ * Interface version of the loaded library: G4A_VERSION of the header it was built from.
+ *   1  the first release;
+ *   2  g4a_gemm_mat.alpha and g4a_norm_in.mult take over what were padding bytes (0 is
+ *      read as 1, so zero-initialise both structs); g4a_prefill refuses f32 caches and
+ *      head_dim 512 without a workspace (G4A_EWORKSPACE) and keeps K at f32 accuracy on
+ *      f32 caches with G4A_Q_HILO; the fused norm prologues refuse x_out / z_out overlapping
+ *      their inputs.
+ */
+#define G4A_VERSION 2
 int g4a_version(void);
 
 /*
@@ -295,10 +305,11 @@ int g4a_gemm16_ws(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_ma
  * biased codes, :150-156; :200-206 the lm_head with in_q = out_q = 0). Rows are packed as
  * for g4a_dequant; bits 2, 4 or 8; n_in a multiple of 128/bits. x f32 [n_in], 16-byte
  * aligned; out f32 [n_out]. With in_q > 0 and 4/8-bit rows of at most 64 16-byte chunks
- * (or a norm prologue, in the fused GEMVs below) the row sum is formed in integers over
- * srq's grid index of x and is exact: out = srq(f32(f32(D * in_q) * w_scale), out_q), D =
- * sum (q - zp) * clamp(rint(x / in_q)); the f32 accumulation of the reference rounds its
- * partial sums, so the two can differ in the last bits before the output srq.
+ * (or a norm prologue, in the fused GEMVs below) the row sum is formed in int32 over srq's
+ * grid index of x, exactly at any row length: out = srq(f32(f32(D) * in_q) * w_scale, out_q),
+ * D = sum (q - zp) * clamp(rint(x / in_q)), rounded to f32 once; the f32 accumulation of the
+ * reference rounds its partial sums, so the two can differ in the last bits before the output
+ * srq.
  */
 int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
               const float* w_scale, float out_q, float* out, void* stream);
@@ -429,6 +440,22 @@ int g4a_geglu16(int n, const void* gate16, const void* up16, float gate_q, float
  */
 int g4a_plegate16(int n_rows, int d, const void* lin16, float lin_q, const float* ple, int ple_stride,
                   float out_q, void* out16, void* stream);
+
+/*
+ * ---- Roofline probes (measurement only; no counterpart in the reference) ------------------
+ * The denominators the kernels above are measured against, taken on the GPU they run on.
+ * sink: device memory of g4a_probe_sink_bytes() bytes that receives values derived from the
+ * work (so none of it is dead); its contents mean nothing.
+ *   g4a_probe_read  reads bytes (a multiple of 4096, at most 2 GiB) from p once, with 16-byte
+ *                   non-temporal loads over `workgroups` workgroups of 256 threads (0: 2048,
+ *                   at most 4096): the best any kernel reading that much from HBM can do.
+ *   g4a_probe_mfma  `workgroups` workgroups of 512 threads (at most 4096), each wave issuing
+ *                   8 * iters v_mfma_f32_32x32x16_f16 (32768 FLOP each) from registers, with
+ *                   8 independent accumulator chains: the reachable dense f16 MFMA rate.
+ */
+size_t g4a_probe_sink_bytes(void);
+int g4a_probe_read(const void* p, size_t bytes, int workgroups, void* sink, void* stream);
+int g4a_probe_mfma(int workgroups, int iters, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

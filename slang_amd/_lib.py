@@ -33,6 +33,7 @@ EXPORTS = (
     "g4a_qgemv", "g4a_qgemv_geglu", "g4a_qgemv_gelu_mul", "g4a_gemv_f16", "g4a_rms_norm", "g4a_geglu",
     "g4a_embed", "g4a_embed_rows", "g4a_softcap_argmax_ws_bytes", "g4a_softcap_argmax",
     "g4a_rows_tail", "g4a_geglu16", "g4a_plegate16",
+    "g4a_probe_sink_bytes", "g4a_probe_read", "g4a_probe_mfma",
 )
 
 # g4a_gemm16_ws: the workspace's leading ticket words (g4attn.h)
@@ -176,6 +177,12 @@ def load() -> ctypes.CDLL:
     lib.g4a_softcap_argmax_ws_bytes.restype = ctypes.c_size_t
     lib.g4a_softcap_argmax_ws_bytes.argtypes = [i]
     lib.g4a_softcap_argmax.argtypes = [i, P, f, P, P, ctypes.c_size_t, P]
+    lib.g4a_probe_sink_bytes.restype = ctypes.c_size_t
+    lib.g4a_probe_sink_bytes.argtypes = []
+    lib.g4a_probe_read.restype = ctypes.c_int
+    lib.g4a_probe_read.argtypes = [P, ctypes.c_size_t, i, P, P]
+    lib.g4a_probe_mfma.restype = ctypes.c_int
+    lib.g4a_probe_mfma.argtypes = [i, i, P, P]
     _lib = lib
     return lib
 

@@ -62,6 +62,6 @@ const char* g4a_strerror(int code) {
 
 const char* g4a_last_error(void) { return g4a::g_last_error; }
 
-int g4a_version(void) { return 1; }
+int g4a_version(void) { return G4A_VERSION; }
 
 }  // extern "C"

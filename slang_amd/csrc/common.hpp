@@ -5,6 +5,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/g4attn.h"
 
 namespace g4a {
@@ -22,6 +24,11 @@ constexpr float kNegInf = -__builtin_huge_valf();
 void set_error(const char* fmt, ...);
 int hip_error(hipError_t e, const char* what);
 bool check_cfg(const g4a_cfg* cfg, bool need_group_le8);
+// two non-NULL arrays of `bytes` bytes each that share memory
+inline bool overlaps(const void* p, const void* q, size_t bytes) {
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return p && q && a < b + bytes && b < a + bytes;
+}
 
 // ---------------------------------------------------------------- lane shuffles
 // DPP row_ror:n (rotate right by n lanes within each row of 16 lanes).

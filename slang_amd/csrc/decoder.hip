@@ -87,6 +87,27 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (LPR == 64) v = add32(v);
     return v;
 }
+// group_sum in int32 (the integer dot products' partial sums): exact at any magnitude
+template <int N>
+__device__ __forceinline__ int dpp_ror_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, 0x120 + N, 0xF, 0xF, false);
+}
+template <int LPR>
+__device__ __forceinline__ int group_sum_i(int v) {
+    v += dpp_ror_i<8>(v);
+    v += dpp_ror_i<4>(v);
+    v += dpp_ror_i<2>(v);
+    v += dpp_ror_i<1>(v);
+    if constexpr (LPR >= 32) {
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        v = (int)p[0] + (int)p[1];
+    }
+    if constexpr (LPR == 64) {
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        v = (int)p[0] + (int)p[1];
+    }
+    return v;
+}
 
 // acc += sum_j q_j * x[j] over the VPC values of one 16-byte chunk, x from LDS in the
 // interleaved layout below. Codes go through byte lanes (v_cvt_f32_ubyteN after one mask):
@@ -316,11 +337,16 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         }
     }
     const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
+    // IDOT sums stay int32 to the end (exact at any row length); the others are f32
     float acc[NM][RPW];
+    int iacc[NM][RPW];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.0f;
+        for (int r = 0; r < RPW; ++r) {
+            acc[m][r] = 0.0f;
+            iacc[m][r] = 0;
+        }
     for (int c = sub; c < nch; c += T) {
         if (c != sub) load_w(c);
         if constexpr (IDOT) {
@@ -328,7 +354,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             for (int m = 0; m < NM; ++m) {
                 const u32x4_t* xk = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const signed char*>(xs) + m * n_in) + c;
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) acc[m][r] += (float)chunk_idot<BITS>(wv[m][r], xk, nch, 0);
+                for (int r = 0; r < RPW; ++r) iacc[m][r] = chunk_idot<BITS>(wv[m][r], xk, nch, iacc[m][r]);
             }
         } else if (stage) {
 #pragma unroll
@@ -357,7 +383,10 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[m][r] = group_sum<T >= 64 ? 64 : T>(acc[m][r]);
+        for (int r = 0; r < RPW; ++r) {
+            if constexpr (IDOT) iacc[m][r] = group_sum_i<T >= 64 ? 64 : T>(iacc[m][r]);
+            else acc[m][r] = group_sum<T >= 64 ? 64 : T>(acc[m][r]);
+        }
         sx[m] = group_sum<64>(sx[m]);  // direct loads only (0 when staged)
     }
     if constexpr (T > 64) {  // the group's waves through LDS (one group per 128/256 threads)
@@ -367,7 +396,7 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) red[slot][m][r] = acc[m][r];
+                for (int r = 0; r < RPW; ++r) red[slot][m][r] = IDOT ? __builtin_bit_cast(float, iacc[m][r]) : acc[m][r];
                 xsum_red[slot][m] = sx[m];
             }
         }
@@ -376,10 +405,17 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         for (int m = 0; m < NM; ++m) {
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
-                float t = 0.0f;
+                if constexpr (IDOT) {
+                    int t = 0;
 #pragma unroll
-                for (int k = 0; k < T / 64; ++k) t += red[grp * (T / 64) + k][m][r];
-                acc[m][r] = t;
+                    for (int k = 0; k < T / 64; ++k) t += __builtin_bit_cast(int, red[grp * (T / 64) + k][m][r]);
+                    iacc[m][r] = t;
+                } else {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < T / 64; ++k) t += red[grp * (T / 64) + k][m][r];
+                    acc[m][r] = t;
+                }
             }
             float t = 0.0f;
 #pragma unroll
@@ -397,11 +433,12 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
         if (sub == r && row < g.n_out) {
-            // IDOT: the integer sum (exact in f32 while below 2^24) times the input step
-            const float d0 = IDOT ? (acc[0][r] - zsx[0]) * g.in_q : acc[0][r] - zsx[0];
+            // IDOT: D = sum - zp * sum k, exact in int32 (zp * sum k is an integer, exact in f32
+            // for the <= 4096 staged codes), rounded to f32 once, times the input step
+            const float d0 = IDOT ? (float)(iacc[0][r] - (int)zsx[0]) * g.in_q : acc[0][r] - zsx[0];
             float y = srq(esc[0] * d0, g.out_q);
             if constexpr (EPI == 1) {
-                const float d1 = IDOT ? (acc[NM - 1][r] - zsx[NM - 1]) * g.in_q2 : acc[NM - 1][r] - zsx[NM - 1];
+                const float d1 = IDOT ? (float)(iacc[NM - 1][r] - (int)zsx[NM - 1]) * g.in_q2 : acc[NM - 1][r] - zsx[NM - 1];
                 const float yb = srq(esc[NM - 1] * d1, g.out_q2);
                 y = srq(gelu_tanh(y) * yb, g.epi_q);
             } else if constexpr (EPI == 2) {
@@ -702,6 +739,13 @@ static int norm_in_set(const g4a_norm_in* pro, int n_in, QgemvArgs& g) {
         set_error("norm prologue: a, res, w1, x_out non-NULL, n_in <= 2048, q2 and eps >= 0");
         return G4A_EINVAL;
     }
+    // workgroup 0 stores x and z while the others still read a, res and w1
+    const size_t vb = (size_t)n_in * sizeof(float);
+    for (const void* out : {(const void*)pro->x_out, (const void*)pro->z_out})
+        if (overlaps(out, pro->a, vb) || overlaps(out, pro->res, vb) || overlaps(out, pro->w1, vb)) {
+            set_error("norm prologue: x_out and z_out must not overlap a, res or w1");
+            return G4A_EINVAL;
+        }
     g.pa = pro->a;
     g.pres = pro->res;
     g.pw1 = pro->w1;

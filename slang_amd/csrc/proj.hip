@@ -144,18 +144,17 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
             w1v[k] = ok ? g.pw1[i] : 0.0f;
             w2v[k] = ok ? g.pw2[i] : 0.0f;
         }
-        const float inv_n = 1.0f / (float)n;
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(pv[k], pv[k], ss);
-        const float d1 = sqrtf(wg_sum(ss, pred) * inv_n + g.peps);
+        const float d1 = sqrtf(wg_sum(ss, pred) / (float)n + g.peps);
         float ss2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             rv[k] = (rv[k] + pv[k] / d1 * w1v[k]) * g.pmult;  // x, zeros past hidden
             ss2 = __builtin_fmaf(rv[k], rv[k], ss2);
         }
-        const float d2 = sqrtf(wg_sum(ss2, pred) * inv_n + g.peps);
+        const float d2 = sqrtf(wg_sum(ss2, pred) / (float)n + g.peps);
         float s2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
@@ -713,6 +712,13 @@ static int qkv_run(int hidden, int q_dim, int kv_dim, const float* a, const floa
             set_error("qkv norm prologue: vectors must be 16-byte aligned");
             return G4A_EINVAL;
         }
+        // workgroup 0 stores x and z while the others still read a, res and w1
+        const size_t vb = (size_t)hidden * sizeof(float);
+        for (const void* out : {(const void*)pro->x_out, (const void*)pro->z_out})
+            if (overlaps(out, pro->a, vb) || overlaps(out, pro->res, vb) || overlaps(out, pro->w1, vb)) {
+                set_error("qkv norm prologue: x_out and z_out must not overlap a, res or w1");
+                return G4A_EINVAL;
+            }
         a = pro->a;  // checked as the input below; the prologue makes the real one
         sum_a = pro->a;
     }

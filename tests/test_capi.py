@@ -40,7 +40,7 @@ def test_cfg_struct_layout_matches_header():
 
 
 def test_strerror_and_version(lib):
-    assert lib.g4a_version() >= 1
+    assert lib.g4a_version() == 2  # G4A_VERSION of include/g4attn.h
     for code in (0, -1, -2, -3, -4):
         assert lib.g4a_strerror(code)
 

@@ -404,3 +404,31 @@ def test_split_gemm_workspace_shared_across_shapes():
         torch.cuda.synchronize()
         assert torch.equal(o1, o2), f"M {M} K {K} n {n}: shared workspace result differs"
         assert not shared.buf[:sa._lib.GEMM_TICKET_BYTES].any(), "tickets left non-zero"
+
+
+def test_norm_prologue_refuses_overlapping_outputs():
+    """The norm prologues store x (and z) from workgroup 0 while every other workgroup still
+    reads a, res and w1, so an output that overlaps one of them would race: g4a_qkv_gemv_norm
+    and the fused GEMVs refuse it (G4A_EINVAL) before launching -- the residual ping-pong of
+    the decode step makes it easy to pass res as x_out by mistake."""
+    from slang_amd.decoder import norm_in, qgemv_gelu_mul
+    hidden, qd, kvd = 256, 64, 8
+    _, _, qb, kb, vb, sc = gemv_case(7, hidden, qd, kvd)
+    rng = np.random.default_rng(3)
+    dp, dx2 = t(rng.standard_normal(hidden).astype(np.float32)), t(rng.standard_normal(hidden).astype(np.float32))
+    dw = t(np.ones(hidden, np.float32))
+    dqb, dsc = dev_words(qb), t(sc)
+    kw = dict(k_bits=dev_words(kb), v_bits=dev_words(vb), q_out=0.03125, k_out=0.0234375, v_out=0.0156)
+    for x_out in (dx2, dp, dx2[8:]):
+        pro = norm_in(dp, dx2, dw, x_out, w2=dw, q2=0.05)
+        with pytest.raises(Exception, match="must not overlap"):
+            sa.qkv_gemv(None, None, dqb, dsc, qd, kvd, pro=pro, hidden=hidden, **kw)
+    z_out = torch.empty(hidden, device=DEV)
+    pro = norm_in(dp, dx2, dw, z_out, w2=dw, z_out=dw, q2=0.05)
+    with pytest.raises(Exception, match="must not overlap"):
+        sa.qkv_gemv(None, None, dqb, dsc, qd, kvd, pro=pro, hidden=hidden, **kw)
+    words = dev_words(rng.integers(0, 2**32, size=qd * hidden // 8, dtype=np.uint64).astype(np.uint32))
+    pro = norm_in(dp, dx2, dw, dx2, q2=0.05)
+    with pytest.raises(Exception, match="must not overlap"):
+        qgemv_gelu_mul(None, words, t(np.ones(qd, np.float32)), t(np.ones(qd, np.float32)), hidden, qd, bits=4,
+                       in_q=0.05, pro=pro)

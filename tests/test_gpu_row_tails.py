@@ -9,6 +9,8 @@ width (1536) and at the ends of the range (8, 4096). The updated residual is hel
 operand to the oracle's f16(srq(., q2)) or one grid step beside it for a few values that sit
 on a rounding midpoint.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -40,9 +42,17 @@ def srq16_close(got16, ref16, step, what, frac=0.05):
 @pytest.mark.parametrize("mode", ["none", "srq", "norm", "norm16"])
 @pytest.mark.parametrize("add", [True, False])
 def test_rows_tail_matches_oracle(rows, n, mode, add):
-    if mode == "none" and not add:
-        pytest.skip("no residual add and no operand: nothing to do (the library refuses it)")
     print(f"rows_tail rows {rows} n {n} mode {mode} add {add}", flush=True)
+    if mode == "none" and not add:
+        # no residual add and no operand: nothing to do, which the C ABI refuses before launching
+        h = t(np.zeros((rows, n), np.float32))
+        rc = _lib.load().g4a_rows_tail(rows, n, None, 0.0, None, 1.0, 1e-6, ctypes.c_void_p(h.data_ptr()),
+                                       MODES["none"], None, 0.0, None, None)
+        assert rc == -1, f"rc {rc}, expected G4A_EINVAL"
+        assert "x16 or a mode" in _lib.load().g4a_last_error().decode()
+        with pytest.raises(Exception, match="x16 or a mode"):
+            rows_tail(h)
+        return
     rng = np.random.default_rng(rows * 7 + n + len(mode) + add)
     hid = rng.standard_normal((rows, n)).astype(np.float32)
     x16 = (rng.standard_normal((rows, n)) * 3).astype(np.float16) if add else None
