@@ -350,6 +350,11 @@ def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, int
               "plegate_out": 0.03, "pleproj_in": 0.03, "pleproj_out": 0.01}
         if not shared:
             sc.update(k_out=0.02, v_out=0.02)
+        # the GELU tables of the two gate grids, as export.py:30-33 writes them (:150, :161)
+        for tag, step in (("gate", sc["gate_out"]), ("plegate", sc["plegate_out"])):
+            gv = (np.arange(256) - 128).astype(np.float64) * step
+            put(f"L{L}.gelu_{tag}",
+                (0.5 * gv * (1.0 + np.tanh(0.7978845608028654 * (gv + 0.044715 * gv ** 3)))).astype(np.float32), "f32")
         layers.append({"index": L, "sliding": not glob, "head_dim": hd, "q_dim": q_dim, "intermediate": inter,
                        "shared": shared, "kv_source": src, "rope_theta": 1e6 if glob else 1e4,
                        "rope_cutoff": 64 if glob else hd // 2, "scales": sc})

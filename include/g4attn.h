@@ -70,7 +70,8 @@ const char* g4a_last_error(void);
  *      read as 1, so zero-initialise both structs); g4a_prefill refuses f32 caches and
  *      head_dim 512 without a workspace (G4A_EWORKSPACE) and keeps K at f32 accuracy on
  *      f32 caches with G4A_Q_HILO; the fused norm prologues refuse x_out / z_out overlapping
- *      their inputs.
+ *      their inputs; g4a_qgemv_geglu, g4a_qgemv_gelu_mul, g4a_gemm16_geglu, g4a_geglu16 and
+ *      g4a_plegate16 take the layer's GELU table (gelu_lut, before the stream).
  */
 #define G4A_VERSION 2
 int g4a_version(void);
@@ -273,10 +274,10 @@ int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a_gemm_mat* 
  * u = f16(A . w_up^T): f16(clamp(round(gelu(srq(g, gate_q)) * srq(u, up_q) / out_q), -128,
  * 127)), or f16(gelu(..) * ..) when out_q is 0 -- the same values as g4a_gemm16 on the two
  * matrices followed by g4a_geglu16, without writing or reading g and u. w_gate and w_up are
- * f16 [n][K]; K and n multiples of 64.
+ * f16 [n][K]; K and n multiples of 64. gelu_lut as for g4a_geglu16.
  */
 int g4a_gemm16_geglu(int M, int K, const void* a_f16, const void* w_gate_f16, const void* w_up_f16, int n,
-                     float gate_q, float up_q, float out_q, void* out_f16, void* stream);
+                     float gate_q, float up_q, float out_q, void* out_f16, const float* gelu_lut, void* stream);
 
 #define G4A_GEMM_TICKET_BYTES 2048
 size_t g4a_gemm16_ws_bytes(int M, int K, int n_mats, const g4a_gemm_mat* mats);
@@ -338,19 +339,28 @@ typedef struct {
     float mult;
 } g4a_norm_in;
 /*
+ * GELU of an srq'd value: gelu_lut, when given, is the layer's 256-entry table of the srq grid
+ * the value sits on, lut[k + 128] = f32(gelu_tanh(k * step)) evaluated in float64 -- the
+ * exported L{L}.gelu_gate / L{L}.gelu_plegate (export.py:30-33, :150, :161) -- and GELU of a
+ * grid value v is lut[clamp(round(v / step), -128, 127) + 128], as every runner kernel forms it
+ * (geglu_b kernels_dsl.py:283, plegate_76 :867, gateup_74/95 :1292/:1373, plegate_b :1785). NULL
+ * (or a zero step) computes gelu_tanh in f32 instead (reference.py:34-35).
+ *
  * The MLP's gate/up pair with its GeGLU in one pass over x (gateup_74/95; reference.py:176-181):
- *   out[o] = srq(gelu_tanh(g[o]) * u[o], out_q),
- *   g = the g4a_qgemv output of the gate rows (gate_in_q, gate_out_q), u that of the up rows.
+ *   out[o] = srq(gelu(g[o]) * u[o], out_q),
+ *   g = the g4a_qgemv output of the gate rows (gate_in_q, gate_out_q), u that of the up rows;
+ *   gelu_lut: the table of the gate_out_q grid (L{L}.gelu_gate) or NULL.
  */
 int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
                     const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
                     const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
-                    const g4a_norm_in* pro, void* stream);
-/* g4a_qgemv with the per-layer-embedding gate's epilogue: out[o] = gelu_tanh(y[o]) * mul[o]
- * (plegate_76; reference.py:186-187, mul = the layer's per-layer input). pro as above. */
+                    const g4a_norm_in* pro, const float* gelu_lut, void* stream);
+/* g4a_qgemv with the per-layer-embedding gate's epilogue: out[o] = gelu(y[o]) * mul[o]
+ * (plegate_76; reference.py:186-187, mul = the layer's per-layer input). pro as above;
+ * gelu_lut the table of the out_q grid (L{L}.gelu_plegate) or NULL. */
 int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
                        const float* w_scale, float out_q, const float* mul, float* out,
-                       const g4a_norm_in* pro, void* stream);
+                       const g4a_norm_in* pro, const float* gelu_lut, void* stream);
 /*
  * g4a_qkv_gemv with its input made in the kernel from the previous layer's tail, so the
  * layer-end add and the next input norm (rmssrq_69 after pleproj_77, runner.py:373-407)
@@ -426,20 +436,22 @@ int g4a_rows_tail(int n_rows, int n, const void* x16, float x_q, const float* w1
                   float* hidden, int mode, const float* w2, float q2, void* y16, void* stream);
 /*
  * geglu_b (kernels_dsl.py:259-290; prefill_gpu.py:373-375) over n values (a multiple of 8):
- *   y = gelu_tanh(srq(f32(gate16), gate_q)) * srq(f32(up16), up_q)
+ *   y = gelu(srq(f32(gate16), gate_q)) * srq(f32(up16), up_q)
  *   out16 = f16(clamp(round(y / out_q), -128, 127)) -- the code on out_q's grid, which the down
  *   GEMM scales back with alpha = out_q --, or f16(y) when out_q is 0.
+ * gelu_lut: the table of the gate_q grid (L{L}.gelu_gate; see g4a_qgemv_geglu) or NULL.
  */
 int g4a_geglu16(int n, const void* gate16, const void* up16, float gate_q, float up_q, float out_q,
-                void* out16, void* stream);
+                void* out16, const float* gelu_lut, void* stream);
 /*
  * plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242; prefill_gpu.py:381-384) over n_rows
  * rows of d values (a multiple of 8):
- *   out16[s][o] = f16(srq(gelu_tanh(srq(f32(lin16[s][o]), lin_q)) * ple[s * ple_stride + o], out_q))
- * ple: the layer's slice of the per-layer inputs [S][nL][d] (ple_stride = nL * d).
+ *   out16[s][o] = f16(srq(gelu(srq(f32(lin16[s][o]), lin_q)) * ple[s * ple_stride + o], out_q))
+ * ple: the layer's slice of the per-layer inputs [S][nL][d] (ple_stride = nL * d); gelu_lut the
+ * table of the lin_q grid (L{L}.gelu_plegate; see g4a_qgemv_geglu) or NULL.
  */
 int g4a_plegate16(int n_rows, int d, const void* lin16, float lin_q, const float* ple, int ple_stride,
-                  float out_q, void* out16, void* stream);
+                  float out_q, void* out16, const float* gelu_lut, void* stream);
 
 /*
  * ---- Roofline probes (measurement only; no counterpart in the reference) ------------------

@@ -9,6 +9,9 @@ It restates gemma4_150/reference.py's ReferenceSRQ over the exported model forma
 (export.py:64-181) instead of the checkpoint:
 
   * gelu_tanh ........................................ reference.py:34-35
+  * gelu_lut / gelu_of_srq: the runners' per-layer GELU table of an srq grid, looked up
+    by the grid index ............................... export.py:30-33; kernels_dsl.py:283,
+                                                       867, 1292, 1373, 1785
   * rms_norm (x / sqrt(mean(x^2) + eps) * w) .......... reference.py:38-43
   * _qlin: srq(W @ srq(x, in_s), out_s), W = (q - 2^(bits-1)) * row_scale
                                                        reference.py:96-101
@@ -32,7 +35,9 @@ the primitives above (SRQ grids make a flipped code in one stage legitimately mo
 later one).
 
 Pinning (tests/test_oracle_decoder.py): gelu_tanh against the erf form of GELU and its
-limits; rms_norm against a float64 loop and its scale invariance; qlin against a
+limits; gelu_lut against the identity gelu(x) - gelu(-x) = x, gelu(0) = 0, a float64 value
+of math.tanh per entry and the f32 gelu_tanh of the grid values, and gelu_of_srq's index
+(a shifted index is caught); rms_norm against a float64 loop and its scale invariance; qlin against a
 pure-Python triple loop over unpacked codes, and against the zero-point closed form;
 hand-packed embedding words; the lm_head block order against a row-major re-pack;
 argmax ties. The batched prefill's stages: gemm16 against a float64 triple loop (with alpha,
@@ -56,6 +61,32 @@ def gelu_tanh(v):
     v = np.asarray(v, np.float32)
     return (0.5 * v * (1.0 + np.tanh(np.float32(0.7978845608028654) * (v + np.float32(0.044715) * v ** 3)))
             ).astype(np.float32)
+
+
+def gelu_lut(out_scale):
+    """The runners' GELU table of one srq grid (export.py:30-33, written per layer for the gate
+    and the per-layer-embedding gate, :150, :161): entry k + 128 is the tanh-form GELU of the
+    grid value k * out_scale (k in [-128, 127]) evaluated in float64, then cast to f32."""
+    g = (np.arange(256) - 128).astype(np.float64) * float(out_scale)
+    return (0.5 * g * (1.0 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3)))).astype(np.float32)
+
+
+def gelu_of_srq(v, s, lut=None):
+    """GELU of values v already on the srq grid of step s, as the runner kernels form it
+    (geglu_b kernels_dsl.py:283, plegate_76 :867, gateup_74/95 :1292/:1373, plegate_b :1785):
+    lut[clamp(round(v / s), -128, 127) + 128] from the layer's table when there is one and
+    s > 0, else gelu_tanh(v) in f32 (reference.py:34-35, and the runners when s is 0)."""
+    if lut is None or s == 0.0:
+        return gelu_tanh(v)
+    k = np.clip(np.round(np.asarray(v, np.float32) / np.float32(s)), -128, 127).astype(np.int64)
+    return np.asarray(lut, np.float32)[k + 128]
+
+
+def layer_lut(man, L, which):
+    """Layer L's exported table L{L}.gelu_gate / L{L}.gelu_plegate, or None when the model
+    carries none (then GELU is reference.py's f32 gelu_tanh)."""
+    name = f"L{L}.gelu_{which}"
+    return man.tensor(name) if name in man.tensors else None
 
 
 def rms_norm(x, w=None, eps=EPS):
@@ -133,7 +164,8 @@ def post_attention(man, L, x, attn):
     gb = bits_of(man, f"L{L}.gate_bits", inter, H)
     st["gate"] = qlin(st["y2"], t("gate_bits"), t("gate_scale"), H, gb, sc["gate_in"], sc["gate_out"])
     st["up"] = qlin(st["y2"], t("up_bits"), t("up_scale"), H, gb, sc["up_in"], sc["up_out"])
-    st["geglu"] = srq(gelu_tanh(st["gate"]) * st["up"], sc["down_in"]).astype(np.float32)
+    st["geglu"] = srq(gelu_of_srq(st["gate"], sc["gate_out"], layer_lut(man, L, "gate")) * st["up"],
+                      sc["down_in"]).astype(np.float32)
     st["down"] = qlin(st["geglu"], t("down_bits"), t("down_scale"), inter,
                       bits_of(man, f"L{L}.down_bits", H, inter), sc["down_in"], sc["down_out"])
     st["x2"] = (st["x1"] + rms_norm(st["down"], t("down_nw"))).astype(np.float32)
@@ -149,7 +181,8 @@ def ple_block(man, L, x2, ple_in_L, gate_out=None, g=None, proj=None):
     pl = t("pleproj_w12s")
     st = {}
     st["plegate"] = qlin(x2, t("plegate_codes"), t("plegate_rowscale"), H, 8, sc["plegate_in"], sc["plegate_out"])
-    st["pleg"] = (gelu_tanh(st["plegate"] if gate_out is None else gate_out) * ple_in_L).astype(np.float32)
+    st["pleg"] = (gelu_of_srq(st["plegate"] if gate_out is None else gate_out, sc["plegate_out"],
+                              layer_lut(man, L, "plegate")) * ple_in_L).astype(np.float32)
     st["pleproj"] = qlin(st["pleg"] if g is None else g, t("pleproj_codes"), t("pleproj_rowscale"), d, 8,
                          sc["pleproj_in"], sc["pleproj_out"])
     st["x3"] = ((x2 + rms_norm(st["pleproj"] if proj is None else proj, pl[:H])) * pl[2 * H]).astype(np.float32)
@@ -197,21 +230,23 @@ def tail_operand(hidden, mode, w2=None, q2=0.0):
     return srq(z, q2).astype(np.float16)
 
 
-def geglu_codes(g16, u16, gate_q, up_q, out_q):
+def geglu_codes(g16, u16, gate_q, up_q, out_q, lut=None):
     """geglu_b (kernels_dsl.py:259-290): y = gelu(srq(f32(gate), gate_q)) * srq(f32(up), up_q),
     stored as its code on out_q's grid, f16(clamp(round(y / out_q), -128, 127)) (f16(y) when
-    out_q is 0); the down GEMM scales it back with alpha = out_q (prefill_gpu.py:376-377)."""
-    y = (gelu_tanh(srq(np.asarray(g16, np.float16).astype(np.float32), gate_q))
+    out_q is 0); the down GEMM scales it back with alpha = out_q (prefill_gpu.py:376-377).
+    lut: the layer's GELU table (gelu_of_srq)."""
+    y = (gelu_of_srq(srq(np.asarray(g16, np.float16).astype(np.float32), gate_q), gate_q, lut)
          * srq(np.asarray(u16, np.float16).astype(np.float32), up_q)).astype(np.float32)
     if out_q == 0.0:
         return y.astype(np.float16)
     return np.clip(np.round(y / np.float32(out_q)), -128.0, 127.0).astype(np.float16)
 
 
-def plegate_operand(lin16, lin_q, ple_L, out_q):
+def plegate_operand(lin16, lin_q, ple_L, out_q, lut=None):
     """plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242; prefill_gpu.py:381-384):
-    f16(srq(gelu(srq(f32(lin), lin_q)) * ple, out_q)), ple the layer's per-layer inputs [S][d]."""
-    g = gelu_tanh(srq(np.asarray(lin16, np.float16).astype(np.float32), lin_q))
+    f16(srq(gelu(srq(f32(lin), lin_q)) * ple, out_q)), ple the layer's per-layer inputs [S][d];
+    lut: the layer's GELU table (gelu_of_srq)."""
+    g = gelu_of_srq(srq(np.asarray(lin16, np.float16).astype(np.float32), lin_q), lin_q, lut)
     return srq((g * np.asarray(ple_L, np.float32)).astype(np.float32), out_q).astype(np.float16)
 
 

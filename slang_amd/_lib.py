@@ -149,7 +149,7 @@ def load() -> ctypes.CDLL:
     lib.g4a_gemm16_ws.restype = ctypes.c_int
     lib.g4a_gemm16_ws.argtypes = [i, i, P, i, ctypes.POINTER(G4AGemmMat), P, ctypes.c_size_t, P]
     lib.g4a_gemm16_geglu.restype = ctypes.c_int
-    lib.g4a_gemm16_geglu.argtypes = [i, i, P, P, P, i, f, f, f, P, P]
+    lib.g4a_gemm16_geglu.argtypes = [i, i, P, P, P, i, f, f, f, P, P, P]
     lib.g4a_qgemv.restype = ctypes.c_int
     lib.g4a_qgemv.argtypes = [i, i, i, P, f, P, P, f, P, P]
     lib.g4a_gemv_f16.restype = ctypes.c_int
@@ -157,9 +157,9 @@ def load() -> ctypes.CDLL:
     lib.g4a_rms_norm.restype = ctypes.c_int
     lib.g4a_qgemv_geglu.restype = ctypes.c_int
     npro = ctypes.POINTER(G4ANormIn)
-    lib.g4a_qgemv_geglu.argtypes = [i, i, i, P, P, P, f, f, P, P, f, f, f, P, npro, P]
+    lib.g4a_qgemv_geglu.argtypes = [i, i, i, P, P, P, f, f, P, P, f, f, f, P, npro, P, P]
     lib.g4a_qgemv_gelu_mul.restype = ctypes.c_int
-    lib.g4a_qgemv_gelu_mul.argtypes = [i, i, i, P, f, P, P, f, P, P, npro, P]
+    lib.g4a_qgemv_gelu_mul.argtypes = [i, i, i, P, f, P, P, f, P, P, npro, P, P]
     lib.g4a_rms_norm.argtypes = [i, i, P, f, P, P, f, f, P, P, f, i, P, P, P]
     lib.g4a_geglu.restype = ctypes.c_int
     lib.g4a_geglu.argtypes = [i, P, P, f, P, P]
@@ -170,9 +170,9 @@ def load() -> ctypes.CDLL:
     lib.g4a_rows_tail.restype = ctypes.c_int
     lib.g4a_rows_tail.argtypes = [i, i, P, f, P, f, f, P, i, P, f, P, P]
     lib.g4a_geglu16.restype = ctypes.c_int
-    lib.g4a_geglu16.argtypes = [i, P, P, f, f, f, P, P]
+    lib.g4a_geglu16.argtypes = [i, P, P, f, f, f, P, P, P]
     lib.g4a_plegate16.restype = ctypes.c_int
-    lib.g4a_plegate16.argtypes = [i, i, P, f, P, i, f, P, P]
+    lib.g4a_plegate16.argtypes = [i, i, P, f, P, i, f, P, P, P]
     lib.g4a_softcap_argmax.restype = ctypes.c_int
     lib.g4a_softcap_argmax_ws_bytes.restype = ctypes.c_size_t
     lib.g4a_softcap_argmax_ws_bytes.argtypes = [i]

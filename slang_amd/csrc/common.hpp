@@ -156,10 +156,20 @@ __device__ __forceinline__ float gelu_tanh16(float v) {
     const float z2 = -1.5957691216057308f * (v + 0.044715f * v * v * v);  // -2 c (..)
     return v / (1.0f + __builtin_amdgcn_exp2f(z2 * 1.4426950408889634f));
 }
+// GELU of v, a value already on the srq grid of step s, as the reference runners form it
+// (geglu_b kernels_dsl.py:283, plegate_76 :867, gateup_74/95 :1292/:1373, plegate_b :1785):
+// from the layer's 256-entry table, lut[k + 128] = f32(gelu(k s)) evaluated in float64
+// (export.py:30-33), at the grid index k = clamp(round(v / s), -128, 127) -- exactly srq's
+// code, since v = k s to within an f32 rounding. Without a table, or on a zero step (where
+// the runners compute it too), gelu_tanh16.
+__device__ __forceinline__ float gelu_srq(float v, float s, const float* lut) {
+    if (!lut || s == 0.0f) return gelu_tanh16(v);
+    return lut[(int)fminf(fmaxf(rintf(v / s), -128.0f), 127.0f) + 128];
+}
 // geglu_b's element (kernels_dsl.py:259-290) from the f16 gate and up products g, u:
 // y = gelu(srq(g, gq)) * srq(u, uq), stored as its code on oq's grid (f16(y) when oq is 0)
-__device__ __forceinline__ half_t geglu_code(float g, float u, float gq, float uq, float oq) {
-    const float y = pin(gelu_tanh16(srq(g, gq)) * srq(u, uq));
+__device__ __forceinline__ half_t geglu_code(float g, float u, float gq, float uq, float oq, const float* lut) {
+    const float y = pin(gelu_srq(srq(g, gq), gq, lut) * srq(u, uq));
     return oq == 0.0f ? (half_t)y : (half_t)fminf(fmaxf(rintf(y / oq), -128.0f), 127.0f);
 }
 

@@ -40,6 +40,7 @@ struct QgemvArgs {
     const float* scale2;
     float in_q2, out_q2, epi_q;
     const float* mul;  // EPI 2
+    const float* lut;  // EPI 1, 2: the layer's GELU table of the out_q grid (gelu_srq), or NULL
     // norm prologue (pa != NULL, staged kernels only): x = res + rms(pa) * w1, stored to xout by
     // workgroup 0; z = rms(x) * w2 (w2 != NULL) or x; the GEMV input is f16 ? f16(srq(f16(z),
     // q2)) : srq(z, q2), stored to zout (if given) by workgroup 0 -- the rms_kernel arithmetic
@@ -440,9 +441,9 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             if constexpr (EPI == 1) {
                 const float d1 = IDOT ? (float)(iacc[NM - 1][r] - (int)zsx[NM - 1]) * g.in_q2 : acc[NM - 1][r] - zsx[NM - 1];
                 const float yb = srq(esc[NM - 1] * d1, g.out_q2);
-                y = srq(gelu_tanh(y) * yb, g.epi_q);
+                y = srq(gelu_srq(y, g.out_q, g.lut) * yb, g.epi_q);
             } else if constexpr (EPI == 2) {
-                y = gelu_tanh(y) * emul;
+                y = gelu_srq(y, g.out_q, g.lut) * emul;
             }
             g.out[row] = y;
         }
@@ -792,7 +793,7 @@ extern "C" int g4a_qgemv(int bits, int n_in, int n_out, const float* x, float in
 extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, const uint32_t* gate_bits,
                                const float* gate_scale, float gate_in_q, float gate_out_q, const uint32_t* up_bits,
                                const float* up_scale, float up_in_q, float up_out_q, float out_q, float* out,
-                               const g4a_norm_in* pro, void* stream) {
+                               const g4a_norm_in* pro, const float* gelu_lut, void* stream) {
     if (pro && pro->a) x = pro->a;  // checked as the input; the prologue makes the real one
     if (bits == 16) {
         set_error("bits 16 not supported for the gate/up pair");
@@ -812,12 +813,13 @@ extern "C" int g4a_qgemv_geglu(int bits, int n_in, int n_out, const float* x, co
     g.in_q2 = up_in_q;
     g.out_q2 = up_out_q;
     g.epi_q = out_q;
+    g.lut = gelu_lut;
     return qgemv_run(bits, 1, g, stream);
 }
 
 extern "C" int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x, float in_q, const uint32_t* w_bits,
                                   const float* w_scale, float out_q, const float* mul, float* out,
-                                  const g4a_norm_in* pro, void* stream) {
+                                  const g4a_norm_in* pro, const float* gelu_lut, void* stream) {
     if (pro && pro->a) x = pro->a;
     if (bits == 16) {
         set_error("bits 16 not supported with the gelu epilogue");
@@ -832,6 +834,7 @@ extern "C" int g4a_qgemv_gelu_mul(int bits, int n_in, int n_out, const float* x,
     QgemvArgs g = qgemv_args(n_in, n_out, x, in_q, w_bits, w_scale, out_q, out);
     if ((rc = norm_in_set(pro, n_in, g)) != G4A_OK) return rc;
     g.mul = mul;
+    g.lut = gelu_lut;
     return qgemv_run(bits, 2, g, stream);
 }
 

@@ -160,24 +160,24 @@ __global__ __launch_bounds__(256) void rows_tail_wave_kernel(TailArgs a, int n_r
     }
 }
 
-// geglu_b: g = srq(f32(gate), gate_q), u = srq(f32(up), up_q), y = gelu_tanh(g) * u;
-// out = f16(clamp(round(y / out_q), -128, 127)) -- the code on out_q's grid, which the down
-// GEMM scales back by alpha = out_q -- or f16(y) when out_q is 0.
+// geglu_b: g = srq(f32(gate), gate_q), u = srq(f32(up), up_q), y = gelu(g) * u (gelu from the
+// layer's table when given, gelu_srq); out = f16(clamp(round(y / out_q), -128, 127)) -- the code
+// on out_q's grid, which the down GEMM scales back by alpha = out_q -- or f16(y) when out_q is 0.
 __global__ __launch_bounds__(256) void geglu16_kernel(int n8, const half8* gate, const half8* up, float gq, float uq,
-                                                      float oq, half8* out) {
+                                                      float oq, half8* out, const float* lut) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n8) return;
     const half8 g = gate[i], u = up[i];
     half8 o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = geglu_code((float)g[j], (float)u[j], gq, uq, oq);
+    for (int j = 0; j < 8; ++j) o[j] = geglu_code((float)g[j], (float)u[j], gq, uq, oq, lut);
     out[i] = o;
 }
 
-// plegate_b + srqh_b: out[s][o] = f16(srq(gelu_tanh(srq(f32(lin[s][o]), lin_q)) * ple[s*stride + o], out_q)),
-// d values per row (a multiple of 8).
+// plegate_b + srqh_b: out[s][o] = f16(srq(gelu(srq(f32(lin[s][o]), lin_q)) * ple[s*stride + o], out_q)),
+// d values per row (a multiple of 8); gelu from the layer's table when given (gelu_srq).
 __global__ __launch_bounds__(256) void plegate16_kernel(int n8, int d, const half8* lin, float lq, const float* ple,
-                                                        int stride, float oq, half8* out) {
+                                                        int stride, float oq, half8* out, const float* lut) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n8) return;
     const int s = (8 * i) / d, o = (8 * i) % d;
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void plegate16_kernel(int n8, int d, const hal
     const float pv[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
     half8 y;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = (half_t)srq(pin(gelu_tanh16(srq((float)x[j], lq)) * pv[j]), oq);
+    for (int j = 0; j < 8; ++j) y[j] = (half_t)srq(pin(gelu_srq(srq((float)x[j], lq), lq, lut) * pv[j]), oq);
     out[i] = y;
 }
 
@@ -245,7 +245,7 @@ extern "C" int g4a_rows_tail(int n_rows, int n, const void* x16, float x_q, cons
 }
 
 extern "C" int g4a_geglu16(int n, const void* gate16, const void* up16, float gate_q, float up_q, float out_q,
-                           void* out16, void* stream) {
+                           void* out16, const float* gelu_lut, void* stream) {
     if (n <= 0 || n % 8 || !gate16 || !up16 || !out16 ||
         (((uintptr_t)gate16 | (uintptr_t)up16 | (uintptr_t)out16) & 15)) {
         set_error("n (%d) a positive multiple of 8; gate, up, out non-NULL and 16-byte aligned", n);
@@ -258,14 +258,14 @@ extern "C" int g4a_geglu16(int n, const void* gate16, const void* up16, float ga
     const int n8 = n / 8;
     hipLaunchKernelGGL(geglu16_kernel, dim3((n8 + 255) / 256), dim3(256), 0, (hipStream_t)stream, n8,
                        reinterpret_cast<const half8*>(gate16), reinterpret_cast<const half8*>(up16), gate_q, up_q,
-                       out_q, reinterpret_cast<half8*>(out16));
+                       out_q, reinterpret_cast<half8*>(out16), gelu_lut);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "geglu16 launch");
     return G4A_OK;
 }
 
 extern "C" int g4a_plegate16(int n_rows, int d, const void* lin16, float lin_q, const float* ple, int ple_stride,
-                             float out_q, void* out16, void* stream) {
+                             float out_q, void* out16, const float* gelu_lut, void* stream) {
     if (n_rows <= 0 || d <= 0 || d % 8 || ple_stride < d || ple_stride % 4 || (int64_t)n_rows * d > 0x7fffffff) {
         set_error("n_rows, d (a multiple of 8) positive, ple_stride >= d and a multiple of 4");
         return G4A_EINVAL;
@@ -281,7 +281,7 @@ extern "C" int g4a_plegate16(int n_rows, int d, const void* lin16, float lin_q, 
     const int n8 = n_rows * d / 8;
     hipLaunchKernelGGL(plegate16_kernel, dim3((n8 + 255) / 256), dim3(256), 0, (hipStream_t)stream, n8, d,
                        reinterpret_cast<const half8*>(lin16), lin_q, ple, ple_stride, out_q,
-                       reinterpret_cast<half8*>(out16));
+                       reinterpret_cast<half8*>(out16), gelu_lut);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "plegate16 launch");
     return G4A_OK;

@@ -252,6 +252,7 @@ struct Gemm16Args {
     unsigned* ticket;  // [tiles], zero between calls
     float* part;       // [tiles][splits][NB * 8][256] float4: the f32 partial tiles
     float gq, uq, oq;  // the gate/up form: geglu_b's steps
+    const float* lut;  // ... and the layer's GELU table of the gq grid (gelu_srq), or NULL
 };
 
 constexpr int kCpolSC1 = 16;  // device scope: the access bypasses the per-XCD caches
@@ -443,7 +444,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
                 for (int i = 0; i < 4; ++i) {
                     const float gv = (float)(half_t)pin(alpha * acc[0][mb][4 * q + i]);
                     const float uv = (float)(half_t)pin(alpha * acc[1][mb][4 * q + i]);
-                    y[i] = geglu_code(gv, uv, g.gq, g.uq, g.oq);
+                    y[i] = geglu_code(gv, uv, g.gq, g.uq, g.oq, g.lut);
                 }
                 *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(g.out[0]) + (size_t)m * N + n) = y;
             }
@@ -614,7 +615,8 @@ extern "C" int g4a_gemm16(int M, int K, const void* a_f16, int n_mats, const g4a
 }
 
 extern "C" int g4a_gemm16_geglu(int M, int K, const void* a_f16, const void* w_gate_f16, const void* w_up_f16, int n,
-                                float gate_q, float up_q, float out_q, void* out_f16, void* stream) {
+                                float gate_q, float up_q, float out_q, void* out_f16, const float* gelu_lut,
+                                void* stream) {
     if (M <= 0 || K <= 0 || K % 64 || n <= 0 || n % 64) {
         set_error("M (%d) positive, K (%d) a positive multiple of 64, n (%d) a positive multiple of 64", M, K, n);
         return G4A_EINVAL;
@@ -646,6 +648,7 @@ extern "C" int g4a_gemm16_geglu(int M, int K, const void* a_f16, const void* w_g
     g.gq = gate_q;
     g.uq = up_q;
     g.oq = out_q;
+    g.lut = gelu_lut;
     hipLaunchKernelGGL((gemm16_kernel<64, 128, 2, false, true>), dim3(g.tiles), dim3(256), 0, (hipStream_t)stream, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "gemm16_geglu launch");

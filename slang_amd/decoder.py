@@ -62,11 +62,23 @@ def norm_in(a, res, w1, x_out, *, w2=None, z_out=None, q2: float = 0.0, f16: boo
                           _ptr(z_out) if z_out is not None else None, float(q2), int(f16), float(eps), float(mult))
 
 
+def _lut(t):
+    """A layer's GELU table (f32 [256]) for the C ABI, or None."""
+    if t is None:
+        return None
+    _need(t, "gelu_lut", torch.float32)
+    if t.numel() != 256:
+        raise ValueError("a GELU table holds 256 values")
+    return _ptr(t)
+
+
 def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int | None = None, out=None,
-                pro=None):
+                pro=None, gelu_lut=None):
     """out = srq(gelu(qgemv(x, *gate)) * qgemv(x, *up), out_q) in one pass (gateup_74/95,
     reference.py:176-181); gate and up are (words, scale, in_q, out_q). pro: a norm_in(...)
-    prologue that makes x (then x may be None)."""
+    prologue that makes x (then x may be None). gelu_lut: the layer's GELU table of the gate's
+    out_q grid (L{L}.gelu_gate, export.py:30-33), looked up as the runners do; None computes
+    gelu_tanh."""
     (gw, gs, gi, go), (uw, us, ui, uo) = gate, up
     if pro is None:
         _need(x, "x", torch.float32)
@@ -77,13 +89,15 @@ def qgemv_geglu(x, gate, up, n_in: int, n_out: int, *, out_q: float, bits: int |
         out = torch.empty(n_out, dtype=torch.float32, device=gw.device)
     check(_lib.load().g4a_qgemv_geglu(bits, n_in, n_out, _ptr(x) if x is not None else None, _ptr(gw), _ptr(gs),
                                       float(gi), float(go), _ptr(uw), _ptr(us), float(ui), float(uo), float(out_q),
-                                      _ptr(out), ctypes.byref(pro) if pro is not None else None, _stream()))
+                                      _ptr(out), ctypes.byref(pro) if pro is not None else None, _lut(gelu_lut),
+                                      _stream()))
     return out
 
 
 def qgemv_gelu_mul(x, words, scale, mul, n_in: int, n_out: int, *, in_q: float = 0.0, out_q: float = 0.0,
-                   bits: int | None = None, out=None, pro=None):
-    """out = gelu(qgemv(x)) * mul (plegate_76; reference.py:186-187); pro as for qgemv_geglu."""
+                   bits: int | None = None, out=None, pro=None, gelu_lut=None):
+    """out = gelu(qgemv(x)) * mul (plegate_76; reference.py:186-187); pro and gelu_lut (here the
+    table of out_q's grid, L{L}.gelu_plegate) as for qgemv_geglu."""
     if pro is None:
         _need(x, "x", torch.float32)
     _need(words, "words", _WORDS)
@@ -93,7 +107,8 @@ def qgemv_gelu_mul(x, words, scale, mul, n_in: int, n_out: int, *, in_q: float =
         out = torch.empty(n_out, dtype=torch.float32, device=words.device)
     check(_lib.load().g4a_qgemv_gelu_mul(bits, n_in, n_out, _ptr(x) if x is not None else None, float(in_q),
                                          _ptr(words), _ptr(scale), float(out_q), _ptr(mul), _ptr(out),
-                                         ctypes.byref(pro) if pro is not None else None, _stream()))
+                                         ctypes.byref(pro) if pro is not None else None, _lut(gelu_lut),
+                                         _stream()))
     return out
 
 
@@ -183,27 +198,28 @@ def rows_tail(hidden, x16=None, *, x_q: float = 0.0, w1=None, mult: float = 1.0,
     return y16
 
 
-def geglu16(gate16, up16, gate_q: float, up_q: float, out_q: float, out=None):
-    """geglu_b (kernels_dsl.py:259-290): f16 code round(gelu(srq(g, gate_q)) * srq(u, up_q) / out_q)."""
+def geglu16(gate16, up16, gate_q: float, up_q: float, out_q: float, out=None, gelu_lut=None):
+    """geglu_b (kernels_dsl.py:259-290): f16 code round(gelu(srq(g, gate_q)) * srq(u, up_q) / out_q);
+    gelu_lut the layer's table of gate_q's grid (qgemv_geglu)."""
     _need(gate16, "gate", torch.float16)
     _need(up16, "up", torch.float16)
     if out is None:
         out = torch.empty_like(gate16)
     check(_lib.load().g4a_geglu16(gate16.numel(), _ptr(gate16), _ptr(up16), float(gate_q), float(up_q),
-                                  float(out_q), _ptr(out), _stream()))
+                                  float(out_q), _ptr(out), _lut(gelu_lut), _stream()))
     return out
 
 
-def plegate16(lin16, lin_q: float, ple, ple_stride: int, out_q: float, out=None):
+def plegate16(lin16, lin_q: float, ple, ple_stride: int, out_q: float, out=None, gelu_lut=None):
     """plegate_b then srqh_b (kernels_dsl.py:1767-1786, 233-242): f16(srq(gelu(srq(lin, lin_q)) *
     ple, out_q)) over lin16 f16 [S][d]; ple points at the layer's slice of [S][nL][d] (row stride
-    ple_stride values)."""
+    ple_stride values); gelu_lut the layer's table of lin_q's grid (qgemv_geglu)."""
     _need(lin16, "lin", torch.float16)
     S, d = lin16.shape
     if out is None:
         out = torch.empty_like(lin16)
     check(_lib.load().g4a_plegate16(S, d, _ptr(lin16), float(lin_q), _ptr(ple), int(ple_stride), float(out_q),
-                                    _ptr(out), _stream()))
+                                    _ptr(out), _lut(gelu_lut), _stream()))
     return out
 
 
@@ -280,6 +296,10 @@ class DecoderStack:
             w["gate_bits_n"] = packed_bits(w["gate_bits"], H, s.intermediate)
             w["down_bits_n"] = packed_bits(w["down_bits"], s.intermediate, H)
             w["o_bits_n"] = packed_bits(w["o_bits"], s.q_dim, H)
+            # the exporter's GELU tables of the gate and per-layer-embedding gate grids
+            # (export.py:30-33, :150, :161), used as the runners use them; absent: gelu_tanh
+            for n in ("gelu_gate", "gelu_plegate"):
+                w[n] = t(n) if f"L{L}.{n}" in man.tensors else None
             self.w.append(w)
         f32 = lambda *shape: torch.zeros(*shape, dtype=torch.float32, device=device)  # noqa: E731
         inter = max(s.intermediate for s in man.layers)
@@ -348,7 +368,7 @@ class DecoderStack:
                     (w["up_bits"], w["up_scale"], sc["up_in"], sc["up_out"]), H, inter, out_q=sc["down_in"],
                     bits=w["gate_bits_n"], out=gg,
                     pro=norm_in(self.o, xin, w["o_w1"], xalt, w2=w["o_w2"], z_out=self.y2, q2=sc["gate_in"],
-                                f16=True))
+                                f16=True), gelu_lut=w["gelu_gate"])
         snap("x1", xalt)
         snap("y2", self.y2)
         snap("geglu", gg)
@@ -358,7 +378,7 @@ class DecoderStack:
         # x2 = x1 + rms(down) * w: the per-layer-embedding gate kernel's prologue, back into xin
         qgemv_gelu_mul(None, w["plegate_codes"], w["plegate_rowscale"], self.ple_in[L], H, self.d,
                        in_q=sc["plegate_in"], out_q=sc["plegate_out"], bits=8, out=self.pleg,
-                       pro=norm_in(self.down, xalt, w["down_nw"], xin))
+                       pro=norm_in(self.down, xalt, w["down_nw"], xin), gelu_lut=w["gelu_plegate"])
         snap("x2", xin)
         snap("pleg", self.pleg)
         qgemv(self.pleg, w["pleproj_codes"], w["pleproj_rowscale"], self.d, H, in_q=sc["pleproj_in"],
@@ -493,7 +513,8 @@ class DecoderStack:
             snap(t, "x1", hid)
             snap(t, "y2", y2)
             gg = take("gg16", S, it)
-            gemm16_geglu(y2, wd["gate"], wd["up"], sc["gate_out"], sc["up_out"], sc["down_in"], out=gg)
+            gemm16_geglu(y2, wd["gate"], wd["up"], sc["gate_out"], sc["up_out"], sc["down_in"], out=gg,
+                         gelu_lut=w["gelu_gate"])
             if t is not None:  # the two products on their own, for the stage checks
                 g16, u16 = take("g16", S, it), take("u16", S, it)
                 gemm16(y2, [(wd["gate"], g16, None), (wd["up"], u16, None)], gws)
@@ -508,7 +529,8 @@ class DecoderStack:
             snap(t, "hh", hh)
             plin, gph, pp = take("plin", S, d), take("gph", S, d), take("pp16", S, H)
             gemm16(hh, [(wd["plegate"], plin, None)], gws)
-            plegate16(plin, sc["plegate_out"], ple[:, L], nL * d, sc["pleproj_in"], out=gph)
+            plegate16(plin, sc["plegate_out"], ple[:, L], nL * d, sc["pleproj_in"], out=gph,
+                      gelu_lut=w["gelu_plegate"])
             gemm16(gph, [(wd["pleproj"], pp, None)], gws)
             snap(t, "plin", plin)
             snap(t, "gph", gph)

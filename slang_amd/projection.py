@@ -239,10 +239,11 @@ def gemm16(a16, mats, workspace: GemmWorkspace | None = None):
                             _stream()))
 
 
-def gemm16_geglu(a16, w_gate, w_up, gate_q: float, up_q: float, out_q: float, out=None):
+def gemm16_geglu(a16, w_gate, w_up, gate_q: float, up_q: float, out_q: float, out=None, gelu_lut=None):
     """The MLP's gate and up GEMMs with geglu_b in one launch (g4a_gemm16_geglu;
     prefill_gpu.py:365-371): f16 code of gelu(srq(f16(a.Wg^T), gate_q)) * srq(f16(a.Wu^T), up_q)
-    on out_q's grid, [M][n], the values gemm16 + geglu16 give."""
+    on out_q's grid, [M][n], the values gemm16 + geglu16 give. gelu_lut: the layer's GELU table
+    of gate_q's grid (L{L}.gelu_gate), or None for gelu_tanh."""
     _need(a16, "a16", torch.float16)
     _need(w_gate, "w_gate", torch.float16)
     _need(w_up, "w_up", torch.float16)
@@ -255,8 +256,14 @@ def gemm16_geglu(a16, w_gate, w_up, gate_q: float, up_q: float, out_q: float, ou
     _need(out, "out", torch.float16)
     if out.numel() != M * n:
         raise ValueError("out must hold M*n values")
+    lut = None
+    if gelu_lut is not None:
+        _need(gelu_lut, "gelu_lut", torch.float32)
+        if gelu_lut.numel() != 256:
+            raise ValueError("a GELU table holds 256 values")
+        lut = _ptr(gelu_lut)
     check(_lib.load().g4a_gemm16_geglu(M, K, _ptr(a16), _ptr(w_gate), _ptr(w_up), n, float(gate_q), float(up_q),
-                                       float(out_q), _ptr(out), _stream()))
+                                       float(out_q), _ptr(out), lut, _stream()))
     return out
 
 

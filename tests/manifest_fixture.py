@@ -11,6 +11,7 @@ import os
 
 import numpy as np
 
+from oracle.decoder import gelu_lut
 from oracle.projection import pack_values
 
 # (sliding, head_dim, rope_cutoff, shared, kv_source): two own-cache layers (a sliding
@@ -44,11 +45,12 @@ class _Writer:
 
 
 def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHEDULE, seed=0,
-                extra_odd_tensor=True, full=False, vocab=512, ple_d=32, mlp_bits=(4, 2, 4, 2)):
+                extra_odd_tensor=True, full=False, vocab=512, ple_d=32, mlp_bits=(4, 2, 4, 2), gelu_tables=True):
     """Write the model; returns (manifest dict, {tensor name: array}) for the checks.
-    full: also the tensors of the rest of the decoder (export.py:86-98, 113-160): the
+    full: also the tensors of the rest of the decoder (export.py:86-98, 113-161): the
     embedding and per-layer-embedding tables, lm_head blocks, o_proj, the MLP (layer L's
-    gate/up/down rows mlp_bits[L]-bit), the int8 per-layer-embedding linears and the norms."""
+    gate/up/down rows mlp_bits[L]-bit), the int8 per-layer-embedding linears, the norms and
+    (gelu_tables) the per-layer GELU tables of the gate grids."""
     rng = np.random.default_rng(seed)
     os.makedirs(out_dir, exist_ok=True)
     w = _Writer(os.path.join(out_dir, "weights.bin"))
@@ -111,6 +113,9 @@ def write_model(out_dir, H=256, n_heads=4, kv_heads=1, window=64, schedule=SCHED
                 put(f"L{L}.{tag}_rowscale", rsc(n_out, 0.002), "f32")
             sc.update(gate_in=0.05, gate_out=0.02, up_in=0.04, up_out=0.02, down_in=0.01, down_out=0.02,
                       plegate_in=0.05, plegate_out=0.03, pleproj_in=0.03, pleproj_out=0.01)
+            if gelu_tables:  # export.py:150, :161: the GELU tables of the two gate grids
+                put(f"L{L}.gelu_gate", gelu_lut(sc["gate_out"]), "f32")
+                put(f"L{L}.gelu_plegate", gelu_lut(sc["plegate_out"]), "f32")
         layers.append({"index": L, "sliding": sliding, "head_dim": hd, "q_dim": q_dim,
                        "intermediate": 4 * H, "shared": shared, "kv_source": src,
                        "rope_theta": 1e4 if sliding else 1e6, "rope_cutoff": cutoff, "scales": sc})

@@ -182,11 +182,11 @@ def test_gemm16_split_plan(lib):
     need = ws(1024, 2048, 1536)
     assert lib.g4a_gemm16_ws(1024, 2048, f, 1, tab(1536), f, need - 16, None) == -3
     assert lib.g4a_gemm16_ws(1024, 2048, f, 1, tab(1536), ctypes.c_void_p(0x10010), need, None) == -1  # alignment
-    # g4a_gemm16_geglu(M, K, a, w_gate, w_up, n, gate_q, up_q, out_q, out, stream)
-    assert lib.g4a_gemm16_geglu(16, 96, f, f, f, 128, 0.1, 0.1, 0.1, f, None) == -1  # K % 64
-    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 96, 0.1, 0.1, 0.1, f, None) == -1  # n % 64
-    assert lib.g4a_gemm16_geglu(16, 128, f, None, f, 128, 0.1, 0.1, 0.1, f, None) == -1
-    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 128, 0.1, -0.1, 0.1, f, None) == -1
+    # g4a_gemm16_geglu(M, K, a, w_gate, w_up, n, gate_q, up_q, out_q, out, gelu_lut, stream)
+    assert lib.g4a_gemm16_geglu(16, 96, f, f, f, 128, 0.1, 0.1, 0.1, f, None, None) == -1  # K % 64
+    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 96, 0.1, 0.1, 0.1, f, None, None) == -1  # n % 64
+    assert lib.g4a_gemm16_geglu(16, 128, f, None, f, 128, 0.1, 0.1, 0.1, f, None, None) == -1
+    assert lib.g4a_gemm16_geglu(16, 128, f, f, f, 128, 0.1, -0.1, 0.1, f, None, None) == -1
 
 
 def test_gemm_mat_struct_layout():
@@ -231,17 +231,21 @@ def test_decoder_argument_errors(lib):
     assert lib.g4a_softcap_argmax(8, FAKE, f(-1), FAKE, FAKE, 64, None) == E
     assert lib.g4a_softcap_argmax_ws_bytes(262144) == 64 * 8 and lib.g4a_softcap_argmax_ws_bytes(0) == 0
     assert lib.g4a_softcap_argmax(262144, FAKE, f(30), FAKE, FAKE, 511, None) == -3        # workspace
-    # fused GEMV variants: the same checks, and their own operands
-    assert lib.g4a_qgemv_geglu(4, 48, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(0), FAKE, None, None) == E
-    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, None, f(0), f(0), f(0), FAKE, None, None) == E
-    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(-1), FAKE, None,
+    # fused GEMV variants: the same checks, and their own operands (..., pro, gelu_lut, stream)
+    assert lib.g4a_qgemv_geglu(4, 48, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(0), FAKE, None, None,
                                None) == E
-    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), None, FAKE, None, None) == E
-    assert lib.g4a_qgemv_gelu_mul(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, FAKE, None, None) == U
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, None, f(0), f(0), f(0), FAKE, None, None,
+                               None) == E
+    assert lib.g4a_qgemv_geglu(4, 64, 4, FAKE, FAKE, FAKE, f(0), f(0), FAKE, FAKE, f(0), f(0), f(-1), FAKE, None,
+                               None, None) == E
+    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), None, FAKE, None, None, None) == E
+    assert lib.g4a_qgemv_gelu_mul(16, 64, 4, FAKE, f(0), FAKE, FAKE, f(0), FAKE, FAKE, None, None, None) == U
     pro = _lib.G4ANormIn(FAKE.value, FAKE.value, None, None, FAKE.value, None, 0.0, 0, 1e-6)  # no w1
-    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
+    assert lib.g4a_qgemv_gelu_mul(4, 64, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None,
+                                  None) == E
     pro.w1 = FAKE.value
-    assert lib.g4a_qgemv_gelu_mul(4, 4096, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None) == E
+    assert lib.g4a_qgemv_gelu_mul(4, 4096, 4, None, f(0), FAKE, FAKE, f(0), FAKE, FAKE, ctypes.byref(pro), None,
+                                  None) == E
 
 
 def test_decode_noalloc_limit(lib):

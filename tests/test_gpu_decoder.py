@@ -73,21 +73,28 @@ def test_qgemv_integer_dot_is_exact(bits, n_in, n_out):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("table", [False, True])
 @pytest.mark.parametrize("bits,n_in,n_out", [(4, 1536, 6144), (2, 1536, 12288), (4, 256, 1024), (8, 512, 64)])
-def test_qgemv_geglu_and_gelu_mul(bits, n_in, n_out):
+def test_qgemv_geglu_and_gelu_mul(bits, n_in, n_out, table):
+    """The gate/up GEMV with its GeGLU and the per-layer-embedding gate GEMV with gelu * mul,
+    with reference.py's f32 gelu_tanh, or (table) with GELU taken from the exporter's float64
+    table of the gate's output grid by the srq code, as gateup_74/95 and plegate_76 do
+    (kernels_dsl.py:867, 1292, 1373)."""
     rng = np.random.default_rng(bits + n_out)
     gw, uw = (pack_values(rng.integers(0, 1 << bits, size=(n_out, n_in)), bits) for _ in range(2))
     gs, us = ((0.01 * (1 + rng.random(n_out))).astype(np.float32) for _ in range(2))
     x = (2 * rng.standard_normal(n_in)).astype(np.float32)
     wd = lambda a: dev(a).view(torch.int32).reshape(-1)  # noqa: E731
+    lut = OD.gelu_lut(0.02) if table else None
     got = host(D.qgemv_geglu(dev(x), (wd(gw), dev(gs), 0.05, 0.02), (wd(uw), dev(us), 0.04, 0.03), n_in, n_out,
-                             out_q=0.01, bits=bits))
+                             out_q=0.01, bits=bits, gelu_lut=dev(lut) if table else None))
     g = qlin_codes(x, gw, gs, n_in, bits, 0.05, 0.02)
     u = qlin_codes(x, uw, us, n_in, bits, 0.04, 0.03)
-    chain_close(got, lambda a, b: OD.gelu_tanh(a) * b, [g, u], f"gate/up {bits}-bit", step=0.01)
+    chain_close(got, lambda a, b: OD.gelu_of_srq(a, 0.02, lut) * b, [g, u], f"gate/up {bits}-bit", step=0.01)
     mul = rng.standard_normal(n_out).astype(np.float32)
-    got = host(D.qgemv_gelu_mul(dev(x), wd(gw), dev(gs), dev(mul), n_in, n_out, in_q=0.05, out_q=0.02, bits=bits))
-    chain_close(got, lambda a: OD.gelu_tanh(a) * mul, [g], f"gelu_mul {bits}-bit")
+    got = host(D.qgemv_gelu_mul(dev(x), wd(gw), dev(gs), dev(mul), n_in, n_out, in_q=0.05, out_q=0.02, bits=bits,
+                                gelu_lut=dev(lut) if table else None))
+    chain_close(got, lambda a: OD.gelu_of_srq(a, 0.02, lut) * mul, [g], f"gelu_mul {bits}-bit")
 
 
 def test_gemv_f16_parity():
@@ -181,12 +188,15 @@ def _stage_checks(m, L, t, ple_in):
     gb = bits("gate_bits", inter, H)
     gate = qlin_codes(g["y2"], w("gate_bits"), w("gate_scale"), H, gb, sc["gate_in"], sc["gate_out"])
     up = qlin_codes(g["y2"], w("up_bits"), w("up_scale"), H, gb, sc["up_in"], sc["up_out"])
-    chain_close(g["geglu"], lambda a, b: OD.gelu_tanh(a) * b, [gate, up], what + " gate/up/geglu", step=sc["down_in"])
+    lut_g, lut_p = OD.layer_lut(m, L, "gate"), OD.layer_lut(m, L, "plegate")
+    chain_close(g["geglu"], lambda a, b: OD.gelu_of_srq(a, sc["gate_out"], lut_g) * b, [gate, up],
+                what + " gate/up/geglu", step=sc["down_in"])
     srq_close(g["down"], OD.qlin(g["geglu"], w("down_bits"), w("down_scale"), inter, bits("down_bits", H, inter),
                                  sc["down_in"]), sc["down_out"], what + " down")
     contract_close(g["x2"], g["x1"] + OD.rms_norm(g["down"], w("down_nw")), what + " x2")
     pgate = qlin_codes(g["x2"], w("plegate_codes"), w("plegate_rowscale"), H, 8, sc["plegate_in"], sc["plegate_out"])
-    chain_close(g["pleg"], lambda a: OD.gelu_tanh(a) * ple_in[L], [pgate], what + " plegate")
+    chain_close(g["pleg"], lambda a: OD.gelu_of_srq(a, sc["plegate_out"], lut_p) * ple_in[L], [pgate],
+                what + " plegate")
     srq_close(g["pleproj"], OD.qlin(g["pleg"], w("pleproj_codes"), w("pleproj_rowscale"), d, 8, sc["pleproj_in"]),
               sc["pleproj_out"], what + " pleproj")
     contract_close(g["x3"], (g["x2"] + OD.rms_norm(g["pleproj"], pl[:H])) * pl[2 * H], what + " x3")

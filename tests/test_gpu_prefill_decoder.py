@@ -116,8 +116,8 @@ def layer_checks(m, st, L, g, prev_x3, ple_gpu, S):
     wu = OP.dequant_f16(w("up_bits"), w("up_scale"), H, it, gb)
     gemm_close(g["g16"], g["y2"], wg, what + " gate GEMM")
     gemm_close(g["u16"], g["y2"], wu, what + " up GEMM")
-    codes_close(g["gg16"], OD.geglu_codes(g["g16"], g["u16"], sc["gate_out"], sc["up_out"], sc["down_in"]),
-                what + " geglu codes")
+    codes_close(g["gg16"], OD.geglu_codes(g["g16"], g["u16"], sc["gate_out"], sc["up_out"], sc["down_in"],
+                                          lut=OD.layer_lut(m, L, "gate")), what + " geglu codes")
     wd = OP.dequant_f16(w("down_bits"), w("down_scale"), it, H, bits("down_bits", H, it))
     gemm_close(g["d16"], g["gg16"], wd, what + " down GEMM", sc["down_in"])
     contract_close(g["x2"], OD.rmsadd(g["x1"], g["d16"], sc["down_out"], w("down_nw")), what + " x2")
@@ -125,7 +125,8 @@ def layer_checks(m, st, L, g, prev_x3, ple_gpu, S):
     srq16_close(g["hh"], g["x2"], sc["plegate_in"], what + " plegate operand")
     wpg = OP.dequant_f16(w("plegate_codes"), w("plegate_rowscale"), H, d, 8)
     gemm_close(g["plin"], g["hh"], wpg, what + " plegate GEMM")
-    gate = OD.gelu_tanh(OD.srq(g["plin"].astype(np.float32), sc["plegate_out"])) * ple_gpu[:, L]
+    gate = OD.gelu_of_srq(OD.srq(g["plin"].astype(np.float32), sc["plegate_out"]), sc["plegate_out"],
+                          OD.layer_lut(m, L, "plegate")) * ple_gpu[:, L]
     srq16_close(g["gph"], gate, sc["pleproj_in"], what + " pleproj operand")
     wpp = OP.dequant_f16(w("pleproj_codes"), w("pleproj_rowscale"), d, H, 8)
     gemm_close(g["pp16"], g["gph"], wpp, what + " pleproj GEMM")

@@ -432,3 +432,36 @@ def test_norm_prologue_refuses_overlapping_outputs():
     with pytest.raises(Exception, match="must not overlap"):
         qgemv_gelu_mul(None, words, t(np.ones(qd, np.float32)), t(np.ones(qd, np.float32)), hidden, qd, bits=4,
                        in_q=0.05, pro=pro)
+
+
+@pytest.mark.parametrize("out_q", [0.0, 0.05])
+def test_gelu_tables_give_the_oracles_codes_exactly(out_q):
+    """With the exporter's GELU table of the gate grid (export.py:30-33) the prefill MLP tail is
+    the runners' arithmetic exactly -- no f32 tanh on either side -- so the fused gate/up GEMM,
+    geglu16 and plegate16 equal the oracle's geglu_b codes and plegate_b operands bit for bit
+    on the GPU's own f16 products (geglu_b kernels_dsl.py:283, plegate_b :1785)."""
+    from slang_amd.decoder import geglu16, plegate16
+    import oracle.decoder as OD
+    rng = np.random.default_rng(11)
+    M, K, n, d = 300, 512, 640, 256
+    a16 = sa.srqh(t(rng.standard_normal((M, K)).astype(np.float32)), 0.0625)
+    wg, wu = [sa.dequant(dev_words(words(rng, n * K // 8)), t(rng.random(n).astype(np.float32) * 0.01 + 0.02),
+                         K, n) for _ in range(2)]
+    gq, uq = 0.05, 0.04
+    lut = OD.gelu_lut(gq)
+    fused = sa.gemm16_geglu(a16, wg, wu, gq, uq, out_q, gelu_lut=t(lut))
+    g16 = torch.empty(M, n, device=DEV, dtype=torch.float16)
+    u16 = torch.empty_like(g16)
+    sa.gemm16(a16, [(wg, g16, None), (wu, u16, None)])
+    unfused = geglu16(g16, u16, gq, uq, out_q, gelu_lut=t(lut))
+    torch.cuda.synchronize()
+    want = OD.geglu_codes(g16.cpu().numpy(), u16.cpu().numpy(), gq, uq, out_q, lut=lut)
+    np.testing.assert_array_equal(unfused.cpu().numpy(), want)
+    np.testing.assert_array_equal(fused.cpu().numpy(), want)
+    lin = (0.3 * rng.standard_normal((M, d))).astype(np.float16)
+    ple = rng.standard_normal((M, 3, d)).astype(np.float32)
+    lq, oq = 0.03, 0.02
+    lut_p = OD.gelu_lut(lq)
+    got = plegate16(t(lin), lq, t(ple)[:, 1], 3 * d, oq, gelu_lut=t(lut_p))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), OD.plegate_operand(lin, lq, ple[:, 1], oq, lut=lut_p))

@@ -21,6 +21,41 @@ def test_gelu_tanh_against_erf_gelu_and_limits():
     assert OD.gelu_tanh(np.float32(1.0)) > 0.84 and OD.gelu_tanh(np.float32(-1.0)) < -0.15  # odd part
 
 
+def test_gelu_lut_is_the_exporters_float64_table():
+    """gelu_lut (export.py:30-33): every entry the float64 tanh-form GELU of the grid value
+    k * s cast to f32 -- checked entry by entry with math.tanh, by the exact identity
+    gelu(x) - gelu(-x) = x and gelu(0) = 0 of the float64 values, and within a few f32 ulps of
+    reference.py's f32 gelu_tanh of the same grid values, over scales the runners use."""
+    for s in (0.0017, 0.02, 0.0534, 0.25, 1.0 / 3):
+        lut = OD.gelu_lut(s)
+        assert lut.dtype == np.float32 and lut.shape == (256,) and lut[128] == 0.0
+        for k in (-128, -77, -1, 1, 5, 64, 127):
+            x = k * s
+            want = np.float32(0.5 * x * (1.0 + math.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3))))
+            assert lut[k + 128] == want, (s, k)
+        x = (np.arange(1, 128) * s).astype(np.float64)
+        odd = lut[128 + np.arange(1, 128)].astype(np.float64) - lut[128 - np.arange(1, 128)].astype(np.float64)
+        assert np.abs(odd - x).max() <= 4 * np.spacing(np.float32(x.max()))  # two f32 roundings
+        grid = ((np.arange(256) - 128) * np.float32(s)).astype(np.float32)
+        f32 = OD.gelu_tanh(grid)
+        assert np.abs(f32 - lut).max() <= 8 * np.spacing(np.abs(lut).max())
+
+
+def test_gelu_of_srq_indexes_the_grid():
+    """gelu_of_srq looks up values already on the grid by their code (kernels_dsl.py:283);
+    without a table, or on a zero step, it is gelu_tanh. An index shifted by one is caught."""
+    s = np.float32(0.05)
+    lut = OD.gelu_lut(s)
+    k = np.arange(-128, 128)
+    v = OD.srq((k * s).astype(np.float32), s)
+    np.testing.assert_array_equal(OD.gelu_of_srq(v, s, lut), lut)
+    assert OD.gelu_of_srq(np.float32(400.0), s, lut) == lut[255]   # clamped like srq
+    np.testing.assert_array_equal(OD.gelu_of_srq(v, s, None), OD.gelu_tanh(v))
+    np.testing.assert_array_equal(OD.gelu_of_srq(v, 0.0, lut), OD.gelu_tanh(v))
+    shifted = np.asarray(lut)[np.clip(k + 129, 0, 255)]
+    assert np.abs(shifted - OD.gelu_of_srq(v, s, lut)).max() > 10 * np.spacing(np.float32(1.0))
+
+
 def test_rms_norm_against_float64_loop_and_invariants():
     rng = np.random.default_rng(0)
     x = rng.standard_normal((3, 40)).astype(np.float32)
