@@ -656,6 +656,8 @@ def main():
                          "or hd 512 (nH 8 / kvH 1, the E2B global layers)")
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config 4 batched decode row (for profiling its kernels)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only single-sequence decode rows (2G, 2S, T 16K / 32K, T 8448) for profiling")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the measured roofline denominators (read-only stream, MFMA loop)")
     args = ap.parse_args()
@@ -691,6 +693,15 @@ def main():
         return
     if args.roofline_only:
         print(json.dumps({"peak_measured": roofline_probes(args.steps, args.warmup)}), flush=True)
+        return
+    if args.decode_only:
+        out = {}
+        for tag, T, win, th, n in (("decode_2g", 4096, 0, 1e6, 64), ("decode_2s", 4096, 512, 1e4, 64),
+                                   ("decode_1seq_16k", 16384, 0, 1e6, 16), ("decode_1seq_32k", 32768, 0, 1e6, 8),
+                                   ("decode_5g", 8448, 0, 1e6, 32)):
+            msd, nbd, _ = decode_case(sa, T, win, th, max(args.steps, 2 * n), args.warmup, n, gen)
+            out[tag] = {"us_per_call": round(msd * 1e3, 3), "GB/s": round(nbd / msd / 1e6, 2)}
+        print(json.dumps(out), flush=True)
         return
     if args.batched_only:
         ms4, nb4, toks = batched_decode_case(sa, args.steps, args.warmup, gen)
@@ -764,6 +775,20 @@ def main():
                                      "fused32": "config 3 as attn_prefill on its own f32 caches: f32 q, K at "
                                                 "f32 accuracy (high and low f16 parts)",
                                      "hd512": "S 1024 at hd 512, nH 8 / kvH 1 (E2B global layer shape)"}[mode]}
+        for T in (16384, 32768):  # one sequence, long context: 512 MiB of rotated caches
+            msl, nbl, _ = decode_case(sa, T, 0, 1e6, max(args.steps, 64), args.warmup, (512 << 20) // (T * 2048), gen)
+            sec[f"decode_1seq_{T // 1024}k"] = {"us_per_call": round(msl * 1e3, 3), "GB/s": round(nbl / msl / 1e6, 2),
+                                                "hbm_frac": round(nbl / msl / 1e6 / HBM_PEAK_GBS, 4),
+                                                "hbm_frac_measured": round(nbl / msl / 1e6 / pm["hbm_GB/s"], 4),
+                                                "kv_bytes": nbl,
+                                                "note": f"one sequence at T {T}, global, nH 8/kvH 2, f16 caches, "
+                                                        f"{(512 << 20) // (T * 2048)} rotated caches, MALL flushed first"}
+        msh, flh, _ = prefill_case(sa, 8192, 0, 1e6, 4, 1, gen, nH=8, kvH=1, hd=512)
+        tfh = flh / (msh * 1e-3) / 1e12
+        sec["prefill_hd512g_8k"] = {"us_per_call": round(msh * 1e3, 3), "TFLOP/s": round(tfh, 2),
+                                    "mfma_frac": round(tfh / F16_PEAK_TFLOPS, 4),
+                                    "mfma_frac_measured": round(tfh / pm["mfma_f16_TFLOP/s"], 4), "flops": flh,
+                                    "note": "S 8192 at hd 512, nH 8 / kvH 1, global (E2B global layer shape)"}
         ms4, nb4, toks = batched_decode_case(sa, max(8, args.steps // 16), args.warmup, gen)
         sec["decode_4"] = {"us_per_call": round(ms4 * 1e3, 3), "GB/s": round(nb4 / ms4 / 1e6, 2),
                            "hbm_frac": round(nb4 / ms4 / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": nb4,
