@@ -51,6 +51,8 @@ struct PrefillArgs {
     float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
 };
 
+// Most a column's running maximum lags its true maximum by (log2 units): P <= 2^15 < 65504
+constexpr float kMaxLag = 15.0f;
 // LDS operand reads issued ahead of their MFMAs in prefill_kernel_w32: score product
 // (one K read per MFMA) and P.V product (two transposed V reads per MFMA); 2-8 and 3-7
 // measured within +-2 % at S 1024 and S 8192
@@ -102,9 +104,11 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
 // swizzled position: c ^ (r % 32) for K, whose reads take one chunk of 32 consecutive rows,
 // and c ^ vswz(r % 4) for V, whose transposed reads take 2 (16 lanes) or 4 (32 lanes)
 // adjacent chunks of 4 consecutive rows: vswz = {0, 10, 12, 6} puts those rows' 32-byte
-// pairs in distinct 128-byte and their 64-byte quads in distinct 256-byte bank windows. The O^T accumulators (256 dims x 32 columns)
-// live in AGPRs; the running maximum is only moved when a score exceeds it by more than
-// 2^8, so rescaling them is rare and P stays <= 256 in f16.
+// pairs in distinct 128-byte and their 64-byte quads in distinct 256-byte bank windows.
+// The running maximum of a column lags: it moves only when a score exceeds it by more than
+// 2^kMaxLag, and then every column of the wave takes its own current maximum (the rescale
+// of the O^T accumulators is one wave-wide pass either way), so rescales stay rare and P
+// stays <= 2^kMaxLag, inside f16's range.
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
@@ -521,10 +525,10 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[kt][r]);
         mloc = max32(mloc) * a.scale_log2;  // the column's other half sits in lane ^ 32
-        // move the running max only when a score passes it by more than 2^8
-        const bool bump = mloc > m_use + 8.0f;
+        // move the running maxima only when a score passes one by more than 2^kMaxLag
+        const bool bump = mloc > m_use + kMaxLag;
         if (__any(bump)) {
-            const float m_new = bump ? mloc : m_use;
+            const float m_new = fmaxf(m_use, mloc);
             const float corr = m_use == kNegInf ? 0.0f : fexp2(m_use - m_new);
             l_run *= corr;
             if (started) {
@@ -806,9 +810,9 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[r]);
         mloc = max32(mloc) * a.scale_log2;
-        const bool bump = mloc > m_use + 8.0f;  // the running max moves only past 2^8
+        const bool bump = mloc > m_use + kMaxLag;  // the running maxima move only past 2^kMaxLag
         if (__any(bump)) {
-            const float m_new = bump ? mloc : m_use;
+            const float m_new = fmaxf(m_use, mloc);
             const float corr = m_use == kNegInf ? 0.0f : fexp2(m_use - m_new);
             l_run *= corr;
             if (started) {
@@ -888,16 +892,280 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
     }
 }
 
+// prefill_kernel_w32h: hd 512 with every wave holding all 512 dims of its 32 columns (128
+// columns a workgroup: G heads x 128/G positions), the GEMM form's plain mode (f16 q from
+// qprep_kernel, f16 caches). Per 32-key tile a wave runs 32 score MFMAs (two accumulator
+// chains over alternate k-steps, added at the end) and 32 P.V MFMAs into 16 O^T tiles of
+// 32 dims -- 256 accumulator registers, which live in AGPRs, with q (128 registers) in
+// VGPRs: one wave a SIMD, no partner wave and no per-tile score exchange, and each K/V
+// tile staged in LDS serves twice the columns of prefill_kernel_w32d's. The tile's LDS
+// layout, DMA, masks and softmax are prefill_kernel_w32d's.
+// acc += a . b with the accumulator in AGPRs (the file's MFMAs are built in VGPR form). The
+// leading s_nop covers a VALU write of a or b just before (2 wait states); the MFMA pipe
+// takes 32 cycles an instruction, so it costs no issue slot the pipe could have used.
+__device__ __forceinline__ void mfma32_acc(float16v& acc, half8 a, half8 b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int G, typename OUTT>
+__global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
+    constexpr int HD = 512, KT = 32, NCOL = 128, BQ = NCOL / G;
+    constexpr int ROWB = HD * 2;      // 1 KiB rows
+    constexpr int TILEB = KT * ROWB;  // one K or V tile: 32 KiB
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n32 = lane & 31, h = lane >> 5;
+    const int T_total = a.start_pos + a.S;
+    const PrefillUnit wu = prefill_unit<BQ, KT>(a, lane);
+    const int kh = wu.kh, qb = wu.qb, piece = wu.piece, n_pieces = wu.n_pieces;
+
+    const int p0 = a.start_pos + qb * BQ;
+    const int kv_hi = min(p0 + BQ, T_total);
+    const int wg_lo = a.window > 0 ? max(0, p0 + 1 - a.window) : 0;
+    const int n_tiles = (kv_hi - wg_lo + KT - 1) / KT;
+    int t0 = 0, t1 = n_tiles;
+    if (a.split_tiles > 0) {
+        t0 = piece * a.split_tiles;
+        t1 = min(t0 + a.split_tiles, n_tiles);
+    }
+
+    // ---- this lane's query column (head hh, position offset pl) and 8-dim half h
+    const int c = 32 * wave + n32;
+    const int hh = c % G, pl = c / G;
+    const int s_raw = qb * BQ + pl;
+    const bool col_ok = s_raw < a.S;
+    const int s_idx = col_ok ? s_raw : a.S - 1;
+    const int pos = a.start_pos + s_idx;
+
+    // K/V rows through buffer resources (rows >= kv_hi read as zeros); wave w moves rows
+    // 8w .. 8w + 7 of each, one 1 KiB row per instruction
+    const int rowg = a.n_kv_heads * HD * 2;
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const half_t*>(a.kc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const half_t*>(a.vc) + (size_t)kh * HD, (uint32_t)(kv_hi - a.kv_row0) * rowg);
+    // (the lane index passes through an empty asm each time, so the 16 source offsets are
+    // formed per tile rather than held in registers across the loop)
+    auto issue = [&](int t, int buf) {
+        const int kb = wg_lo + t * KT - a.kv_row0;
+        char* kdst = lds + buf * 2 * TILEB;
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * wave + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kdst + r * ROWB), 16,
+                                                     (kb + r) * rowg + 16 * (ln ^ (r & 31)), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(kdst + TILEB + r * ROWB),
+                                                     16, (kb + r) * rowg + 16 * (ln ^ vswz(r)), 0, 0, 0);
+        }
+    };
+
+    // ---- q: lane (column c, half h) holds dims 16s + 8h .. +7 (s < 32), the B operand
+    // layout; the loads go out before the first tile's
+    half8 qf[32];
+    {
+        const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
+        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * ROWB + 16 * h;
+#pragma unroll
+        for (int s = 0; s < 32; ++s) qf[s] = bload_h8(rq, qo + 32 * s);
+        if (t0 < t1) issue(t0, t0 & 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (!col_ok) {
+#pragma unroll
+            for (int s = 0; s < 32; ++s) qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
+
+    // ---- key ranges: this wave [w_lo, wp1], this column [col_lo, pos]
+    const int wp0 = p0 + (32 * wave) / G;
+    const int wp1 = min(p0 + (32 * wave + 31) / G, T_total - 1);
+    const int w_lo = a.window > 0 ? max(0, wp0 + 1 - a.window) : 0;
+    const int col_lo = a.window > 0 ? pos + 1 - a.window : 0;
+
+    // LDS read offsets. K operand k-step s of this lane: row n32, chunk (2s + h) ^ n32, i.e.
+    // byte kofs ^ 32s with kofs = 1024 n32 + 16 (h ^ n32). Transposed V reads (as
+    // prefill_kernel_w32's): row 16u + 8i + vr0, chunk (4dt + vc0) ^ vsw, i.e. byte
+    // (vofs ^ 64dt) + 1024 (16u + 8i) with vofs = 1024 vr0 + 16 (vc0 ^ vsw) + vb0. Both offsets
+    // pass through an empty asm every tile, so the compiler forms the 32 + 16 XORs in the
+    // loop instead of holding 48 hoisted addresses.
+    const int m16 = lane & 15, half16 = (lane >> 4) & 1;
+    const int vr0 = 4 * h + (m16 >> 2);
+    const int vc0 = 2 * half16 + ((m16 & 3) >> 1);
+    const int vb0 = 8 * (m16 & 1);
+    const int kofs0 = 1024 * n32 + 16 * (h ^ n32);
+    const int vofs0 = 1024 * vr0 + 16 * (vc0 ^ vswz(vr0)) + vb0;
+
+    float16v oacc[16];  // O^T[32dt + 8(r/4) + 4h + r%4][column]
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) oacc[dt] = float16v{};
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) asm volatile("" : "+a"(oacc[dt]));
+    float m_use = kNegInf, l_run = 0.0f;
+    bool started = false;
+    for (int t = t0; t < t1; ++t) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's rows of tile t are in LDS
+        __syncthreads();                                    // all rows; tile t-1 consumed
+        if (t + 1 < t1) issue(t + 1, (t + 1) & 1);
+        const int kb = wg_lo + t * KT;
+        if (kb > wp1 || kb + KT - 1 < w_lo) continue;  // no key of this tile for this wave
+        int kofs = (t & 1) * 2 * TILEB + kofs0, vofs = (t & 1) * 2 * TILEB + TILEB + vofs0;
+        asm volatile("" : "+v"(kofs), "+v"(vofs));
+
+        // S^T = K . Q^T over 32 k-steps of 16 dims, even and odd steps in two chains
+        float16v se = float16v{}, so = float16v{};
+        {
+#pragma unroll
+            for (int s0 = 0; s0 < 32; s0 += 4) {
+                half8 kv[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) kv[s] = *reinterpret_cast<const half8*>(lds + (kofs ^ (32 * (s0 + s))));
+#pragma unroll
+                for (int s = 0; s < 4; s += 2) {
+                    se = mfma32(kv[s], qf[s0 + s], se);
+                    so = mfma32(kv[s + 1], qf[s0 + s + 1], so);
+                }
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);
+#pragma unroll
+            for (int i = 0; i < 32 - kQkAhead; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
+        }
+        float sacc[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = se[r] + so[r];
+        // scores of this lane: key kb + 4h + 8(r/4) + r%4 of its column, log2 domain
+        const bool masked = (kb + KT - 1 > wp0) || (a.window > 0 && kb < wp1 + 1 - a.window);
+        if (masked) {
+            const int rel_hi = pos - (kb + 4 * h), rel_lo = col_lo - (kb + 4 * h);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int o = 8 * (r >> 2) + (r & 3);
+                sacc[r] = (o <= rel_hi && o >= rel_lo) ? sacc[r] : kNegInf;
+            }
+        }
+        float mloc = kNegInf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[r]);
+        mloc = max32(mloc) * a.scale_log2;
+        const bool bump = mloc > m_use + kMaxLag;  // the running maxima move only past 2^kMaxLag
+        if (__any(bump)) {
+            const float m_new = fmaxf(m_use, mloc);
+            const float corr = m_use == kNegInf ? 0.0f : fexp2(m_use - m_new);
+            l_run *= corr;
+            if (started) {
+                // one 16-register tile at a time: copied to VGPRs, scaled, pinned back into
+                // AGPRs (left to itself the compiler moves all 256 through VGPRs and spills)
+                asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"  // the last MFMA's writes, as in the epilogue
+                             : "+a"(oacc[0]), "+a"(oacc[1]), "+a"(oacc[2]), "+a"(oacc[3]), "+a"(oacc[4]),
+                               "+a"(oacc[5]), "+a"(oacc[6]), "+a"(oacc[7]), "+a"(oacc[8]), "+a"(oacc[9]),
+                               "+a"(oacc[10]), "+a"(oacc[11]), "+a"(oacc[12]), "+a"(oacc[13]), "+a"(oacc[14]),
+                               "+a"(oacc[15]));
+#pragma unroll
+                for (int dt = 0; dt < 16; ++dt) {
+                    float16v x = oacc[dt];
+                    asm volatile("" : "+v"(x));
+                    x *= corr;
+                    asm volatile("" : "+v"(x));
+                    oacc[dt] = x;
+                    asm volatile("" : "+a"(oacc[dt]));
+                }
+            }
+            m_use = m_new;
+        }
+        started = true;
+        const float msub = m_use == kNegInf ? 0.0f : m_use;
+        half8 pb[2];
+        float ps = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float pv = fexp2(__builtin_fmaf(sacc[8 * u + i], a.scale_log2, -msub));
+                ps += pv;
+                pb[u][i] = (half_t)pv;
+            }
+        l_run += ps;
+
+        // O^T += V^T . P^T over two 16-key steps, 16 dims tiles each
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int d0 = 0; d0 < 16; d0 += 4) {
+                half8 av[4];
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    const char* vp = lds + (vofs ^ (64 * (d0 + dd))) + 16 * u * ROWB;
+                    const half4 lo = lds_tr16(reinterpret_cast<const half_t*>(vp));
+                    const half4 hi = lds_tr16(reinterpret_cast<const half_t*>(vp + 8 * ROWB));
+                    av[dd] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) mfma32_acc(oacc[d0 + dd], av[dd], pb[u]);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPvAhead, 0);
+#pragma unroll
+        for (int i = 0; i < 32 - kPvAhead; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kPvAhead, 0);
+    }
+
+    // ---- epilogue: the 512 dims of this wave's 32 columns. The accumulators are read by
+    // VALU instructions below, which must not issue within 18 wait states of the last MFMA
+    // writing them (the compiler does not see the asm MFMAs); the asm also orders every read
+    // after the wait, since each accumulator passes through it.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                 : "+a"(oacc[0]), "+a"(oacc[1]), "+a"(oacc[2]), "+a"(oacc[3]), "+a"(oacc[4]), "+a"(oacc[5]),
+                   "+a"(oacc[6]), "+a"(oacc[7]), "+a"(oacc[8]), "+a"(oacc[9]), "+a"(oacc[10]), "+a"(oacc[11]),
+                   "+a"(oacc[12]), "+a"(oacc[13]), "+a"(oacc[14]), "+a"(oacc[15]));
+    const float l_tot = add32(l_run);
+    if (n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
+        // blocks of 32 columns x 256 dims, [wave][dim half][dt % 8][j][lane] half4: the
+        // layout prefill_kernel_w32d writes for its (pair, dim half) waves
+        const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
+        const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 4 * lane;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
+                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
+                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+        if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
+        return;
+    }
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (col_ok) {
+        OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(orow + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
+            }
+    }
+}
+
 // Merge of the pieces of split query blocks (the decode merge identity per column): with
 // each piece holding o_p = O_p / l_p, out = sum_p o_p l_p 2^(m_p - M) / sum_p l_p 2^(m_p - M),
 // M = max_p m_p, then srq and the output type. One workgroup per (query block, wave block of
 // 32 columns x 256 dims, kv head), laid out like the partials: thread (k, lane) owns the
 // lane's 4-dim runs k, k+4, .. (k < 4) of all 32 dims tiles, so every load instruction reads
 // a contiguous 512-byte run. At most 8 pieces. HD 256: wave block w = columns 32w..; HD 512
-// (prefill_kernel_w32d): columns 32(w/2).., dims 256(w%2)..
-template <typename OUTT, int HD>
+// (prefill_kernel_w32d, NCOL 64, and prefill_kernel_w32h, NCOL 128): columns 32(w/2)..,
+// dims 256(w%2)..
+template <typename OUTT, int HD, int NCOL>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-    constexpr int KT = HD == 256 ? 64 : 32, NCOL = HD == 256 ? 128 : 64, MAXP = 8;
+    constexpr int KT = HD == 256 ? 64 : 32, MAXP = 8;
     const int qb = blockIdx.x, w = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, k0 = tid >> 6;
     const int c = (HD == 256 ? 32 * w : 32 * (w >> 1)) + (lane & 31), h = lane >> 5;
@@ -966,6 +1234,19 @@ static prefill_fn pick_w32(bool out32, bool hilo, bool klo) {
     if (hilo) return klo ? pick_w32_out<HD, G, true, true>(out32) : pick_w32_out<HD, G, true, false>(out32);
     return klo ? pick_w32_out<HD, G, false, true>(out32) : pick_w32_out<HD, G, false, false>(out32);
 }
+template <int G>
+static prefill_fn pick_w32h(bool out32) {
+    return out32 ? prefill_kernel_w32h<G, float> : prefill_kernel_w32h<G, half_t>;
+}
+static prefill_fn pick_g_w32h(int G, bool out32) {
+    switch (G) {
+        case 1: return pick_w32h<1>(out32);
+        case 2: return pick_w32h<2>(out32);
+        case 4: return pick_w32h<4>(out32);
+        case 8: return pick_w32h<8>(out32);
+    }
+    return nullptr;
+}
 template <int HD>
 static prefill_fn pick_g(int G, bool out32, bool hilo, bool klo) {
     switch (G) {
@@ -999,15 +1280,17 @@ struct PrefillSplit {
 // G4A_Q_HILO the low parts too). hd 256 on f16 caches runs unsplit without a workspace
 // (its q prologue fused in).
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// query columns a workgroup of the kernel that runs the call holds
+static int prefill_ncol(int HD, bool hilo) { return HD == 256 || !hilo ? 128 : 64; }
 static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     PrefillSplit p{0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const int HD = (int)cfg->head_dim;
     if ((HD != 256 && HD != 512) || S <= 0 || cfg->n_kv_heads == 0) return p;
     const int G = (int)(cfg->n_q_heads / cfg->n_kv_heads);
-    const int NCOL = HD == 256 ? 128 : 64, KT = HD == 256 ? 64 : 32;
+    const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
+    const int NCOL = prefill_ncol(HD, hilo), KT = HD == 256 ? 64 : 32;
     if (G < 1 || NCOL % G) return p;
     const int BQ = NCOL / G, kvH = (int)cfg->n_kv_heads, W = (int)cfg->window;
-    const bool hilo = (cfg->flags & G4A_Q_HILO) != 0;
     if (cfg->flags & G4A_KV_F32) {
         p.kv_row0 = W > 0 && start_pos + 1 - W > 0 ? start_pos + 1 - W : 0;
         p.kv_rows = start_pos + S - p.kv_row0;
@@ -1131,7 +1414,12 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     }
     const bool split = sp.split_tiles > 0 && ws_ok && ws_bytes >= sp.total;
     const bool klo = kv32 && hilo;  // f32 q on f32 caches: K at f32 accuracy as well
-    const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo) : pick_g<512>(G, out32, hilo, klo);
+    // hd 512: prefill_kernel_w32h for f16 q (its 128 q registers a wave leave no room for
+    // the low parts), prefill_kernel_w32d for G4A_Q_HILO
+    const bool w32h = HD == 512 && !hilo;
+    const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo)
+                          : w32h    ? pick_g_w32h(G, out32)
+                                    : pick_g<512>(G, out32, hilo, klo);
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
@@ -1149,7 +1437,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     a.n_q_heads = (int)cfg->n_q_heads;
     a.n_kv_heads = (int)cfg->n_kv_heads;
     a.window = (int)cfg->window;
-    const int BQ = (HD == 256 ? 128 : 64) / G;
+    const int NCOL = prefill_ncol(HD, hilo), BQ = NCOL / G;
     a.n_qblocks = (S + BQ - 1) / BQ;
     if ((int64_t)(start_pos + S) * cfg->n_kv_heads * HD * 2 > 0x7fffffff ||
         (int64_t)S * cfg->n_q_heads * HD * 4 > 0x7fffffff) {
@@ -1216,9 +1504,12 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "prefill launch");
     if (a.split_tiles > 0) {
-        auto mf = HD == 256 ? (out32 ? prefill_merge_kernel<float, 256> : prefill_merge_kernel<half_t, 256>)
-                            : (out32 ? prefill_merge_kernel<float, 512> : prefill_merge_kernel<half_t, 512>);
-        hipLaunchKernelGGL(mf, dim3(a.n_qblocks, 4, cfg->n_kv_heads), dim3(256), 0, (hipStream_t)stream, a);
+        auto mf = HD == 256 ? (out32 ? prefill_merge_kernel<float, 256, 128> : prefill_merge_kernel<half_t, 256, 128>)
+                  : w32h    ? (out32 ? prefill_merge_kernel<float, 512, 128> : prefill_merge_kernel<half_t, 512, 128>)
+                            : (out32 ? prefill_merge_kernel<float, 512, 64> : prefill_merge_kernel<half_t, 512, 64>);
+        // one workgroup per 32 columns x 256 dims of a query block
+        hipLaunchKernelGGL(mf, dim3(a.n_qblocks, NCOL / 32 * (HD / 256), cfg->n_kv_heads), dim3(256), 0,
+                           (hipStream_t)stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return hip_error(e, "prefill merge launch");
     }

@@ -187,6 +187,21 @@ def test_s300_crosses_tiles_with_srq(hd, window):
               f"S300 srq hilo hd={hd} W={window}")
 
 
+@pytest.mark.parametrize("S,start,window", [(1024, 0, 0), (1024, 0, 512), (2048, 0, 512), (600, 1500, 0),
+                                            (333, 64, 100)])
+def test_hd512_e2b_shape(S, start, window):
+    """The Gemma 4 E2B global-layer shape (nH 8 / kvH 1, hd 512): f16 q on the 128-column
+    kernel (every wave all 512 dims; key split at S 1024 global and at S 600 after 1500
+    cached rows, unsplit one-workgroup-a-block grids at S 2048 W 512), f32 q on the
+    dim-split wave-pair kernel, both against the oracle."""
+    T = start + S
+    q, qg, k, v, cos, sin = config3_inputs(S=T, theta=1e6 if window == 0 else 1e4, seed=S + window,
+                                           nH=8, kvH=1, hd=512)
+    q, cos, sin = q[start:], cos[start:], sin[start:]
+    check_both_modes(q, k, v, start, sa.AttnConfig(8, 1, 512, window), qg, cos, sin,
+                     f"hd512 S={S} start={start} W={window}")
+
+
 @pytest.mark.parametrize("S,start,window", [(100, 700, 512), (37, 0, 0), (1, 0, 0), (1, 900, 0),
                                             (129, 383, 128), (250, 6, 5)])
 @pytest.mark.parametrize("nH,kvH", [(8, 2), (4, 4), (8, 1), (4, 2)])
