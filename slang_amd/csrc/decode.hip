@@ -705,10 +705,16 @@ __global__ __launch_bounds__(256) void decode_merge_list_kernel(DecodeArgs a) {
 constexpr long kDecodeTargetWgs = 512;  // workgroups the worst-case sequence is spread over
 constexpr long kDecodeMinChunk = 16;    // keys per split at least (one 16-key block)
 
+constexpr long kDecodeCus = 256;        // compute units of the MI355X
+
 // Keys per split: spread the worst-case work (every sequence at max_key_len) over about
 // kDecodeTargetWgs workgroups, never below kDecodeMinChunk keys; a chunk of 64 keys
 // (every wave of the workgroup busy) is preferred as long as it still yields 128 or more
-// workgroups. At most 256 splits per sequence, chunk a multiple of the 16-key block.
+// workgroups. A grid just past a whole number of rounds of one workgroup per CU (up to a
+// quarter round more) is pulled back to those rounds with longer splits: the few CUs that
+// would take a second workgroup each stream twice the keys of the rest (config 5's decode,
+// T 8448, kvH 2: 264 workgroups of 64 keys ran 12.3 us a call, 212 of 80 keys 10.8 us).
+// At most 256 splits per sequence, chunk a multiple of the 16-key block.
 static int decode_chunk(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     const long pairs = (long)n_seq * cfg->n_kv_heads;
     long max_active = max_key_len;
@@ -719,6 +725,12 @@ static int decode_chunk(const g4a_cfg* cfg, int n_seq, int max_key_len) {
     long chunk = (kp + target - 1) / target;
     if (chunk < min_chunk) chunk = min_chunk;
     if (chunk < 64 && kp >= 128L * 64) chunk = 64;
+    chunk = (chunk + 15) & ~15L;
+    const long wgs = pairs * ((max_active + chunk - 1) / chunk), whole = wgs / kDecodeCus * kDecodeCus;
+    if (whole > 0 && wgs > whole && wgs - whole <= kDecodeCus / 4 && whole / pairs >= 1) {
+        const long s = whole / pairs;  // splits per pair within the whole rounds
+        chunk = (((max_active + s - 1) / s) + 15) & ~15L;
+    }
     if ((max_active + chunk - 1) / chunk > 256) chunk = (max_active + 255) / 256;
     return (int)((chunk + 15) & ~15L);
 }
