@@ -54,6 +54,24 @@ def flush_mall():
     torch.sum(_FLUSH)
 
 
+WARM_S = 0.3  # seconds of the measured work before each timed region
+
+
+def warm_clocks(run):
+    """Repeat `run` (GPU work, launched asynchronously) until the GPU has been busy with it for
+    WARM_S seconds. From idle the MI355X's shader clock takes a few hundred milliseconds to
+    reach its ~2.35 GHz (rocm-smi: 104 MHz idle, 1.7 GHz, then 2.33-2.35 GHz at 0.3-s
+    samples under load); timed right after a short warm-up, the S 8192 prefill layer read
+    341 us a call against 294 us once the clocks were up. A serving GPU runs at the
+    sustained clock, which is what the timed regions measure."""
+    t0 = time.perf_counter()
+    while True:
+        run()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= WARM_S:
+            return
+
+
 def graph_time_ms(fn_list, steps, warmup, flush=True):
     """Capture `steps` calls (cycling fn_list) in one HIP graph; return mean ms per call.
 
@@ -70,6 +88,8 @@ def graph_time_ms(fn_list, steps, warmup, flush=True):
             fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
     if EAGER:
+        with torch.cuda.stream(stream):
+            warm_clocks(lambda: [fn() for fn in fn_list])
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
@@ -86,8 +106,7 @@ def graph_time_ms(fn_list, steps, warmup, flush=True):
         for i in range(steps):
             fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
-    g.replay()                      # warm replay (untimed)
-    torch.cuda.synchronize()
+    warm_clocks(g.replay)           # warm replays (untimed) until the clocks are up
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
