@@ -95,6 +95,59 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
     }
 }
 
+// The same preparation for hd 512, one wave per row (rows of four waves a workgroup): lane l
+// holds dims 8l .. 8l+7, its RoPE partner (d, d + 256) sits in lane l ^ 32. Only the hd-512
+// kernels read this q, and only from here, so its sum-of-squares order (per lane, then
+// across the wave) need not be prep_q_column's; the RoPE arithmetic is. Eight 16-byte loads
+// a lane, against qprep_kernel's 96 for the same row share.
+__global__ __launch_bounds__(256) void qprep_row512_kernel(const float* q, const float* gain, const float* rcos,
+                                                         const float* rsin, half_t* out, int rows, int n_q_heads,
+                                                         float eps, half_t* out_lo) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const int s_idx = row / n_q_heads;
+    float8v x = load8(q + (size_t)row * 512 + 8 * lane);
+    float8v c = float8v{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f}, sn = float8v{};
+    if (rcos) {
+        c = load8(rcos + (size_t)s_idx * 256 + 8 * (lane & 31));
+        sn = load8(rsin + (size_t)s_idx * 256 + 8 * (lane & 31));
+    }
+    if (gain) {
+        const float8v gv = load8(gain + 8 * lane);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+        const float rs = 1.0f / sqrtf(wave_sum(ss) / 512.0f + eps);  // x * rs * w, as the reference kernels
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = x[i] * rs * gv[i];
+    }
+    half8 hv, lv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float y = __shfl_xor(x[i], 32);
+        // lane < 32: x0 = x, x1 = y; lane >= 32: x1 = x, x0 = y (prep_q_column's fma forms)
+        const float r = lane < 32 ? pin(__builtin_fmaf(x[i], c[i], -(y * sn[i]))) : pin(__builtin_fmaf(x[i], c[i], y * sn[i]));
+        hv[i] = (half_t)r;
+        lv[i] = (half_t)(r - (float)hv[i]);
+    }
+    *reinterpret_cast<half8*>(out + (size_t)row * 512 + 8 * lane) = hv;
+    if (out_lo) *reinterpret_cast<half8*>(out_lo + (size_t)row * 512 + 8 * lane) = lv;
+}
+
+// q to f16 (and its low parts) for S x nH rows on `stream`
+static hipError_t launch_qprep(int HD, long rows, int n_q_heads, const float* q, const float* gain,
+                               const float* rcos, const float* rsin, half_t* out, half_t* out_lo, float eps,
+                               hipStream_t stream) {
+    if (HD == 256)  // one wave (16 rows) per workgroup spreads even short prompts over every CU
+        hipLaunchKernelGGL(qprep_kernel<256>, dim3((unsigned)((rows + 15) / 16)), dim3(64), 0, stream, q, gain, rcos,
+                           rsin, out, (int)rows, n_q_heads, eps, out_lo);
+    else
+        hipLaunchKernelGGL(qprep_row512_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, q, gain, rcos,
+                           rsin, out, (int)rows, n_q_heads, eps, out_lo);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- hd 256
 // prefill_kernel_w32: 32 query columns per wave (128 per workgroup: G heads x 128/G
 // positions) on v_mfma_f32_32x32x16_f16, so each K or V operand read from LDS feeds a
@@ -618,7 +671,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 // accumulates O^T for its own dims -- per wave the registers and the LDS bytes per MFMA of
 // the hd-256 kernel. Tiles of 32 keys (1 KiB rows: K and V 32 KiB each, double buffered:
 // 128 KiB of LDS, plus 16 KiB for the score exchange) are DMA'd as in prefill_kernel_w32.
-// q comes prepared in f16 (qprep_kernel; the RoPE pairs (i, i + 256) would span both waves).
+// q comes prepared in f16 (qprep_row512_kernel; the RoPE pairs (i, i + 256) would span both waves).
 template <int G, typename OUTT, bool HILO, bool KLO>
 __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
     constexpr int HD = 512, KT = 32, NCOL = 64, BQ = NCOL / G;
@@ -894,7 +947,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
 
 // prefill_kernel_w32h: hd 512 with every wave holding all 512 dims of its 32 columns (128
 // columns a workgroup: G heads x 128/G positions), the GEMM form's plain mode (f16 q from
-// qprep_kernel, f16 caches). Per 32-key tile a wave runs 32 score MFMAs (two accumulator
+// qprep_row512_kernel, f16 caches). Per 32-key tile a wave runs 32 score MFMAs (two accumulator
 // chains over alternate k-steps, added at the end) and 32 P.V MFMAs into 16 O^T tiles of
 // 32 dims -- 256 accumulator registers, which live in AGPRs, with q (128 registers) in
 // VGPRs: one wave a SIMD, no partner wave and no per-tile score exchange, and each K/V
@@ -1276,7 +1329,7 @@ struct PrefillSplit {
 };
 // Every mode runs the 32-column kernels (hd 256: prefill_kernel_w32, hd 512:
 // prefill_kernel_w32d). Some need workspace (base > 0): f32 caches the f16 (K high, V, K
-// low) copy of the attended rows (kv16_kernel); hd 512 its q in f16 (qprep_kernel; with
+// low) copy of the attended rows (kv16_kernel); hd 512 its q in f16 (qprep_row512_kernel; with
 // G4A_Q_HILO the low parts too). hd 256 on f16 caches runs unsplit without a workspace
 // (its q prologue fused in).
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1304,8 +1357,9 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
     if ((long)p.n_qblocks * kvH >= 512) return p;
     // a sliding window bounds every block to W/KT + 1 tiles: splitting then pays its q
     // preparation and merge only while the unsplit grid leaves most CUs idle (hd 256, S 2048,
-    // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27; hd 512, S 1024, W 512,
-    // 128 workgroups: 49.9 unsplit against 52.7)
+    // W 512: 34 us unsplit against 45 us split; S 1024: 32 against 27; hd 512 on
+    // prefill_kernel_w32d, S 1024, W 512, 128 workgroups: 49.9 unsplit against 52.7; on
+    // prefill_kernel_w32h, 64 workgroups: 76 unsplit against 43 split)
     if (W > 0 && (long)p.n_qblocks * kvH >= 128) return p;
     int max_tiles = 0;
     for (int qb = 0; qb < p.n_qblocks; ++qb) {
@@ -1316,7 +1370,11 @@ static PrefillSplit prefill_split(const g4a_cfg* cfg, int S, int start_pos) {
         if (nt > max_tiles) max_tiles = nt;
     }
     int st = (max_tiles * 5 + 31) / 32;
-    if (st < 2) st = 2;
+    // at least 2 tiles a piece, 4 for prefill_kernel_w32h's 32-key tiles (hd 512, S 1024,
+    // W 512, 17-tile blocks: 3 tiles a piece 53.5 us a call, 4 tiles 43.4, 5 tiles 47.4;
+    // global, 32-tile blocks: 5 tiles 48.1 us, 7 tiles 52.6)
+    const int st_min = HD == 512 && NCOL == 128 ? 4 : 2;
+    if (st < st_min) st = st_min;
     if (st < (max_tiles + 7) / 8) st = (max_tiles + 7) / 8;  // the merge takes <= 8 pieces
     const int pieces = (max_tiles + st - 1) / st;
     if (pieces <= 1) return p;
@@ -1478,11 +1536,8 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         const size_t q16b = align256((size_t)S * cfg->n_q_heads * HD * sizeof(half_t));
         half_t* q16 = (half_t*)wsp;
         half_t* q16lo = hilo ? (half_t*)(wsp + q16b) : nullptr;
-        const int rows = S * (int)cfg->n_q_heads;
-        hipLaunchKernelGGL(HD == 256 ? qprep_kernel<256> : qprep_kernel<512>, dim3((rows + 15) / 16), dim3(64), 0,
-                           (hipStream_t)stream, q, q_gain, rope_cos, rope_sin, q16, rows, (int)cfg->n_q_heads,
-                           cfg->eps, q16lo);
-        hipError_t e0 = hipGetLastError();
+        const hipError_t e0 = launch_qprep(HD, (long)S * cfg->n_q_heads, (int)cfg->n_q_heads, q, q_gain, rope_cos,
+                                           rope_sin, q16, q16lo, cfg->eps, (hipStream_t)stream);
         if (e0 != hipSuccess) return hip_error(e0, "prefill qprep launch");
         a.q16 = q16;
         a.q16lo = q16lo;
@@ -1542,12 +1597,8 @@ extern "C" int g4a_qprep(const g4a_cfg* cfg, int S, const float* q, const float*
         set_error("S*n_q_heads too large");
         return G4A_EINVAL;
     }
-    // one wave (16 rows) per workgroup spreads even short prompts over every CU
-    const int blocks = (int)((rows + 15) / 16);
-    auto fn = HD == 256 ? qprep_kernel<256> : qprep_kernel<512>;
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64), 0, (hipStream_t)stream, q, q_gain, rope_cos, rope_sin,
-                       (half_t*)q16, (int)rows, (int)cfg->n_q_heads, cfg->eps, (half_t*)nullptr);
-    hipError_t e = hipGetLastError();
+    const hipError_t e = launch_qprep(HD, rows, (int)cfg->n_q_heads, q, q_gain, rope_cos, rope_sin, (half_t*)q16,
+                                      nullptr, cfg->eps, (hipStream_t)stream);
     if (e != hipSuccess) return hip_error(e, "qprep launch");
     return G4A_OK;
 }
