@@ -302,13 +302,16 @@ def stack_case(sa, gen, S=8192, steps=256, n_layers=35):
                     "is given beside it"}
 
 
-def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, inter=6144, window=512):
+def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, window=512, wide_from=15):
     """A Gemma 4 E2B-shaped model in the exported format (export.py:64-181), built in host
     memory over random weights (no checkpoint): 35 layers, every fifth global (hd 512,
     partial RoPE cutoff 64, theta 1e6), the others sliding (hd 256, W 512, theta 1e4),
-    nH 8 / kvH 1, layers 15.. sharing the caches of layers 13/14, 4-bit q/k/v/o and MLP
-    (intermediate 6144), int8 per-layer-embedding linears, 2-bit lm_head over 262144 tokens.
-    Packed rows are uniform random bytes, i.e. uniform codes of any width."""
+    nH 8 / kvH 1, layers 15.. sharing the caches of layers 13/14, 4-bit q/k/v/o, the MLP as
+    the QAT checkpoint packs it (loader.py:25, prefill_gpu.py:191-192): intermediate 6144 at
+    4 bits on layers 0-14, the double-wide 12288 at 2 bits on layers 15-34 (the runner's
+    gateup_95 / down_96 path, runner.py:448-458), int8 per-layer-embedding linears, 2-bit
+    lm_head over 262144 tokens. Packed rows are uniform random bytes, i.e. uniform codes of
+    any width."""
     from slang_amd.manifest import Manifest
     rng = np.random.default_rng(seed)
     parts, tensors, pos, keep = [], {}, 0, {}
@@ -358,8 +361,9 @@ def e2b_manifest(seed=0, vocab=262144, n_layers=35, H=1536, nH=8, ple_d=256, int
             put(f"L{L}.qkv_scales", rsc(q_dim + 2 * hd, 0.01), "f32")
         put(f"L{L}.o_bits", rows(H, q_dim, 4), "u32")
         put(f"L{L}.o_scale", rsc(H, 0.01), "f32")
+        inter, mlp_bits = (6144, 4) if L < wide_from else (12288, 2)
         for tag, n_out, n_in in (("gate", inter, H), ("up", inter, H), ("down", H, inter)):
-            put(f"L{L}.{tag}_bits", rows(n_out, n_in, 4), "u32")
+            put(f"L{L}.{tag}_bits", rows(n_out, n_in, mlp_bits), "u32")
             put(f"L{L}.{tag}_scale", rsc(n_out, 0.01), "f32")
         for tag, n_out, n_in in (("plegate", ple_d, H), ("pleproj", H, ple_d)):
             put(f"L{L}.{tag}_codes", rows(n_out, n_in, 8), "u32")

@@ -151,7 +151,9 @@ __device__ __forceinline__ float chunk_dot(u32x4_t w, const float4v* xq, int str
 // the codes times the int8 k with v_dot4_i32_i8, exact. 4-bit: the even and odd nibbles of
 // word w come out as bytes (codes 0..15) and meet the k of the same values, staged per chunk
 // as 8 dwords (dword 2w: values 8w, 8w+2, 8w+4, 8w+6; dword 2w+1: the odd ones) in two
-// uint4 planes [2][nch]; the zero point is taken out afterwards as in chunk_dot. 8-bit: the
+// uint4 planes [2][nch]; the zero point is taken out afterwards as in chunk_dot. 2-bit: bit
+// pair f of every byte of word w (mask after a shift by 2f) gives values 16w + 4b + f in
+// byte b, against plane f of four [4][nch] (dword w of plane f: those values' k). 8-bit: the
 // biased codes XOR 0x80 are the signed c - 128, against k in row order (one plane).
 template <int BITS>
 __device__ __forceinline__ int chunk_idot(u32x4_t w, const u32x4_t* xk, int stride, int acc) {
@@ -163,6 +165,14 @@ __device__ __forceinline__ int chunk_idot(u32x4_t w, const u32x4_t* xk, int stri
             const uint32_t xe = k < 2 ? x0[2 * k] : x1[2 * k - 4], xo = k < 2 ? x0[2 * k + 1] : x1[2 * k - 3];
             acc = __builtin_amdgcn_sdot4((int)lo, (int)xe, acc, false);
             acc = __builtin_amdgcn_sdot4((int)hi, (int)xo, acc, false);
+        }
+    } else if constexpr (BITS == 2) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const u32x4_t xf = xk[f * stride];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                acc = __builtin_amdgcn_sdot4((int)((w[k] >> (2 * f)) & 0x03030303u), (int)xf[k], acc, false);
         }
     } else {
         const u32x4_t x0 = xk[0];
@@ -185,9 +195,9 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     static_assert(NT == 256 || (T <= 128 && NT <= 1024 && NT % 256 == 0), "workgroup shapes the launches use");
     constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
-    // IDOT (4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
+    // IDOT (2/4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
     // index k, the dot products in integers (chunk_idot), y = scale * (sum - zp * sum k) * in_q
-    static_assert(!IDOT || BITS == 4 || BITS == 8, "integer dot products for 4- and 8-bit rows");
+    static_assert(!IDOT || BITS == 2 || BITS == 4 || BITS == 8, "integer dot products for 2-, 4- and 8-bit rows");
     constexpr float ZP = BITS == 16 || (IDOT && BITS == 8) ? 0.0f : (float)(1 << (BITS - 1));
     const bool stage = IDOT || T <= 64 || g.pa != nullptr;  // workgroup-uniform
     extern __shared__ float4v xs[];      // [NM][VPC/4][nch]
@@ -237,6 +247,8 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             if constexpr (BITS == 4) {
                 const int dw = 2 * (e >> 3) + (e & 1);
                 at = ((dw >> 2) * nch + c) * 16 + (dw & 3) * 4 + ((e & 7) >> 1);
+            } else if constexpr (BITS == 2) {  // plane e % 4, dword e / 16, byte (e % 16) / 4
+                at = ((e & 3) * nch + c) * 16 + (e >> 4) * 4 + ((e & 15) >> 2);
             } else {
                 at = c * 16 + e;
             }
@@ -642,10 +654,12 @@ static hipError_t launch_qgemv(const QgemvArgs& g, hipStream_t s) {
     const bool staged = T <= 64 || g.pa;
     const size_t lds = staged ? (size_t)(EPI == 1 ? 2 : 1) * g.n_in * sizeof(float) : 0;
     const dim3 grid((g.n_out + rows_per_wg - 1) / rows_per_wg);
-    if constexpr (BITS == 4 || BITS == 8) {
-        // integer dot products where x is staged on a grid (every in_q > 0; whole chunks)
-        if (staged && g.in_q > 0.0f && (EPI != 1 || g.in_q2 > 0.0f) && g.n_in % (128 / BITS) == 0) {
-            hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT, true>), grid, dim3(NT), lds, s, g);
+    if constexpr (BITS == 2 || BITS == 4 || BITS == 8) {
+        // integer dot products where x is on a grid (every in_q > 0; whole chunks): x staged as
+        // its int8 grid index, also for the wide rows that otherwise read x straight from memory
+        if (g.in_q > 0.0f && (EPI != 1 || g.in_q2 > 0.0f) && g.n_in % (128 / BITS) == 0) {
+            const size_t lds_i = staged ? lds : (size_t)(EPI == 1 ? 2 : 1) * g.n_in;
+            hipLaunchKernelGGL((qgemv_kernel<BITS, T, RPW, EPI, NT, true>), grid, dim3(NT), lds_i, s, g);
             return hipGetLastError();
         }
     }
@@ -665,7 +679,12 @@ template <int BITS, int EPI>
 static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
     const int c = g.row_chunks;
     if (c <= 16) return launch_qgemv<BITS, 16, 1, EPI>(g, s);
-    if (c <= 32) return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
+    if (c <= 32) {
+        if (BITS == 2 && g.pa)  // the double-wide 2-bit gate/up with its norm prologue: 12288 rows
+                                // at 48 a workgroup of 768 threads, one workgroup a CU
+            return launch_qgemv<BITS, 32, 2, EPI, 768>(g, s);
+        return BITS == 2 ? launch_qgemv<BITS, 32, 8, EPI>(g, s) : launch_qgemv<BITS, 32, 2, EPI>(g, s);
+    }
     if (c <= 64)  // the norm prologue once per 768 threads: fewer workgroups read its operands
                   // (the gate/up GEMV at E2B shape: whole step 1.807 -> 1.769 ms/token with 512
                   // threads, 1.746 with 1024; 768 gives its 6144 rows one workgroup per CU:

@@ -356,9 +356,10 @@ class DecoderStack:
         snap("x0", xin)
         snap("a", self.a)
         snap("attn", attn)
-        # inputs already on their step's grid skip the GEMV's srq (srq(srq(v, s), s) = srq(v, s)
-        # exactly): the attention output carries o_in, the GeGLU output down_in
-        qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=0.0, out_q=sc["o_out"], bits=w["o_bits_n"],
+        # the attention output is already on o_in's grid and the GeGLU output on down_in's; the
+        # GEMVs are told the grid all the same (srq(srq(v, s), s) = srq(v, s) exactly), so they
+        # take the integer dot products: x staged as its int8 grid index
+        qgemv(attn, w["o_bits"], w["o_scale"], s.q_dim, H, in_q=sc["o_in"], out_q=sc["o_out"], bits=w["o_bits_n"],
               out=self.o)
         snap("o", self.o)
         # x1 = x + rms(o) * w1 and the MLP input y2 = f16(srq(f16(rms(x1) * w2), gate_in)) are
@@ -372,7 +373,7 @@ class DecoderStack:
         snap("x1", xalt)
         snap("y2", self.y2)
         snap("geglu", gg)
-        qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=0.0, out_q=sc["down_out"],
+        qgemv(gg, w["down_bits"], w["down_scale"], inter, H, in_q=sc["down_in"], out_q=sc["down_out"],
               bits=w["down_bits_n"], out=self.down)
         snap("down", self.down)
         # x2 = x1 + rms(down) * w: the per-layer-embedding gate kernel's prologue, back into xin
