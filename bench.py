@@ -141,8 +141,8 @@ def make_caches(sa, n, T, theta, gen, window=0):
 
 def decode_case(sa, T, window, theta, steps, warmup, n_caches, gen, device_len=True):
     """One query at position T-1, its key length in a device array; device_len=False gives
-    the length on the host instead (key_len NULL at the C ABI), which measured 0.2-0.3 us
-    slower per call on the box."""
+    the length on the host instead (key_len NULL at the C ABI). The two forms measure within
+    0.2-0.3 us of each other a call, the faster one changing between boxes and runs."""
     caches = make_caches(sa, n_caches, T, theta, gen)
     q = torch.randn(NH, HD, device="cuda", generator=gen)
     qg = 1 + 0.1 * torch.randn(HD, device="cuda", generator=gen)

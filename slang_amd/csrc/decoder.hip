@@ -195,8 +195,9 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     static_assert(NT == 256 || (T <= 128 && NT <= 1024 && NT % 256 == 0), "workgroup shapes the launches use");
     constexpr int NGRP = NT / T;
     constexpr int NM = EPI == 1 ? 2 : 1;  // matrices
-    // IDOT (2/4/8-bit rows, staged x, every in_q > 0; the host checks): x staged as its int8 grid
-    // index k, the dot products in integers (chunk_idot), y = scale * (sum - zp * sum k) * in_q
+    // IDOT (2/4/8-bit rows, every in_q > 0; the host checks): x always staged, as its int8 grid
+    // index k (also for groups wider than a wave), the dot products in integers (chunk_idot),
+    // y = scale * (sum - zp * sum k) * in_q
     static_assert(!IDOT || BITS == 2 || BITS == 4 || BITS == 8, "integer dot products for 2-, 4- and 8-bit rows");
     constexpr float ZP = BITS == 16 || (IDOT && BITS == 8) ? 0.0f : (float)(1 << (BITS - 1));
     const bool stage = IDOT || T <= 64 || g.pa != nullptr;  // workgroup-uniform

@@ -51,12 +51,18 @@ def test_qgemv_parity(bits, n_in, n_out, in_q, out_q):
         contract_close(got, ref, f"qgemv {bits}-bit {n_out}x{n_in}")
 
 
-@pytest.mark.parametrize("bits,n_in,n_out", [(4, 1536, 6144), (4, 2048, 1531), (8, 256, 1536), (8, 512, 77)])
+@pytest.mark.parametrize("bits,n_in,n_out", [
+    (4, 1536, 6144), (4, 2048, 1531), (8, 256, 1536), (8, 512, 77),
+    (2, 1536, 12288),                  # the double-wide MLP's gate / up rows
+    (2, 12288, 1536), (4, 6144, 1536),  # down projections: rows wider than a wave's chunks
+    (4, 4096, 1536),                    # o_proj of an hd-512 layer
+])
 def test_qgemv_integer_dot_is_exact(bits, n_in, n_out):
-    """Staged 4/8-bit GEMVs with in_q > 0 sum codes times the int8 grid index k = srq's
-    clamp(rint(x / in_q)) in integers (v_dot4_i32_i8). With out_q 0 the output is then
-    exactly f32(f32(D * in_q) * scale), D = sum (c - zp) k over the row computed here in int64:
-    a wrong nibble/byte order, zero point or index would change D."""
+    """GEMVs with in_q > 0 sum codes times the int8 grid index k = srq's clamp(rint(x / in_q))
+    in integers (v_dot4_i32_i8), x staged as k in LDS whether a row group covers the row in one
+    pass or not. With out_q 0 the output is then exactly f32(f32(D * in_q) * scale),
+    D = sum (c - zp) k over the row computed here in int64: a wrong 2-bit/nibble/byte order,
+    zero point or index would change D."""
     rng = np.random.default_rng(bits * 31 + n_out)
     codes = rng.integers(0, 1 << bits, size=(n_out, n_in))
     words = pack_values(codes, bits)
