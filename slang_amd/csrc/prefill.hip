@@ -46,13 +46,24 @@ struct PrefillArgs {
     const half_t* q16lo;  // ... and with G4A_Q_HILO its f16 low parts (q - f32(q16))
     int kv_row0;  // prefill_kernel_w32: first row held in kc/vc (rows below it are never read)
     const void* kclo;  // f32 caches: the f16 low parts k - f32(f16(k)) of the f16 K copy in kc
-    half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of 128 x 256 O / l in f16, in the
-                      // accumulator layout [wave][dt][j][lane][4] (see prefill_merge_kernel)
+    half_t* part_o;   // [kvH][n_qblocks][max_pieces] blocks of NCOL x HD O / l in f16, in the
+                      // accumulator layout [wave block][dt][j pair][lane][8] (see prefill_merge_kernel)
     float2* part_ml;  // [kvH][n_qblocks][max_pieces][128 columns] (m, l)
 };
 
 // Most a column's running maximum lags its true maximum by (log2 units): P <= 2^15 < 65504
 constexpr float kMaxLag = 15.0f;
+
+// Rows j0 .. j0 + 7 of a 32x32 accumulator tile (two 4-row groups of one lane) times inv,
+// as one 16-byte f16 store: the split pieces' partial O.
+template <typename ACC>
+__device__ __forceinline__ void store_part8(half_t* dst, const ACC& acc, int j0, float inv) {
+    half8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (half_t)(acc[j0 + i] * inv);
+    *reinterpret_cast<half8*>(dst) = v;
+}
+
 // LDS operand reads issued ahead of their MFMAs in prefill_kernel_w32: score product
 // (one K read per MFMA) and P.V product (two transposed V reads per MFMA); 2-8 and 3-7
 // measured within +-2 % at S 1024 and S 8192
@@ -635,15 +646,12 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     if (n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
         const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
         const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        // one 512-byte run per store instruction: [wave][dt][j][lane] half4
-        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 4 * lane;
+        // one 1 KiB run per store instruction: [wave][dt][j pair][lane] half8
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 8 * lane;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
-                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
-                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
@@ -920,14 +928,11 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
     if (n_pieces > 1) {  // a piece of a split query block: O / l in f16, (m, l) from wave dh 0
         const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
         const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * 256) + 4 * lane;
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * 256) + 8 * lane;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
-                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
-                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0 && dh == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
@@ -1015,15 +1020,41 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
     };
 
     // ---- q: lane (column c, half h) holds dims 16s + 8h .. +7 (s < 32), the B operand
-    // layout; the loads go out before the first tile's
+    // layout. Wave w DMAs the f16 q rows of its 32 columns, whole 1 KiB rows (chunk n of a
+    // row from logical chunk n ^ (column % 32)), into its 16 KiB of the LDS stage that tile
+    // t0 + 1 takes over later, in two rounds of 16 rows (the stage holds half of the
+    // workgroup's 128 KiB of q), and reads each round back in the B-operand layout; tile
+    // t0's DMA goes out after the first round's. (Loaded straight in the operand layout,
+    // every load instruction took 32 bytes from each of 32 rows, and the workgroup's
+    // 128 KiB came through L1 about four times: 9 us of a 48 us call at S 1024.)
     half8 qf[32];
     {
         const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
-        const int qo = (s_idx * a.n_q_heads + kh * G + hh) * ROWB + 16 * h;
+        char* qs = lds + ((t0 + 1) & 1) * 2 * TILEB + wave * 16 * ROWB;
 #pragma unroll
-        for (int s = 0; s < 32; ++s) qf[s] = bload_h8(rq, qo + 32 * s);
-        if (t0 < t1) issue(t0, t0 & 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (int r = 0; r < 2; ++r) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int cj = 32 * wave + 16 * r + j;  // the column whose row this DMA moves
+                const int qo = ((qb * BQ + cj / G) * a.n_q_heads + kh * G + cj % G) * ROWB + 16 * (ln ^ (16 * r + j));
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(qs + j * ROWB),
+                                                         16, qo, 0, 0, 0);
+            }
+            if (r == 0 && t0 < t1) {
+                issue(t0, t0 & 1);
+                asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // the 16 q DMAs before tile t0's
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            if ((n32 >> 4) == r) {
+                const char* qrow = qs + (n32 & 15) * ROWB;
+#pragma unroll
+                for (int s = 0; s < 32; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's 16 KiB free again
+        }
         if (!col_ok) {
 #pragma unroll
             for (int s = 0; s < 32; ++s) qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -1179,18 +1210,15 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
                    "+a"(oacc[12]), "+a"(oacc[13]), "+a"(oacc[14]), "+a"(oacc[15]));
     const float l_tot = add32(l_run);
     if (n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
-        // blocks of 32 columns x 256 dims, [wave][dim half][dt % 8][j][lane] half4: the
+        // blocks of 32 columns x 256 dims, [wave][dim half][dt % 8][j pair][lane] half8: the
         // layout prefill_kernel_w32d writes for its (pair, dim half) waves
         const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
         const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 4 * lane;
+        half_t* po = a.part_o + blk * (NCOL * HD) + (size_t)wave * (32 * HD) + 8 * lane;
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<half4*>(po + (4 * dt + j) * 256) =
-                    half4{(half_t)(oacc[dt][4 * j] * inv_p), (half_t)(oacc[dt][4 * j + 1] * inv_p),
-                          (half_t)(oacc[dt][4 * j + 2] * inv_p), (half_t)(oacc[dt][4 * j + 3] * inv_p)};
+            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
@@ -1212,8 +1240,8 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
 // each piece holding o_p = O_p / l_p, out = sum_p o_p l_p 2^(m_p - M) / sum_p l_p 2^(m_p - M),
 // M = max_p m_p, then srq and the output type. One workgroup per (query block, wave block of
 // 32 columns x 256 dims, kv head), laid out like the partials: thread (k, lane) owns the
-// lane's 4-dim runs k, k+4, .. (k < 4) of all 32 dims tiles, so every load instruction reads
-// a contiguous 512-byte run. At most 8 pieces. HD 256: wave block w = columns 32w..; HD 512
+// lane's 8-dim runs k, k+4, .. (k < 4) of the 16 (dims tile, 4-row pair) runs, so every load
+// instruction reads a contiguous 1 KiB run. At most 8 pieces. HD 256: wave block w = columns 32w..; HD 512
 // (prefill_kernel_w32d, NCOL 64, and prefill_kernel_w32h, NCOL 128): columns 32(w/2)..,
 // dims 256(w%2)..
 template <typename OUTT, int HD, int NCOL>
@@ -1237,14 +1265,14 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     const rsrc_t rml = make_rsrc(a.part_ml + blk0 * NCOL, (uint32_t)n_pieces * NCOL * 8);
     const rsrc_t ro = make_rsrc(a.part_o + blk0 * (NCOL * HD) + (size_t)w * (32 * 256), (uint32_t)n_pieces * NCOL * HD * 2);
     float2 ml[MAXP];
-    half4 ov[MAXP][8];
+    half8 ov[MAXP][4];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) ml[p] = bload_f32x2(rml, (p * NCOL + c) * 8);
 #pragma unroll
     for (int p = 0; p < MAXP; ++p)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)  // run k = k0 + 4i: dims tile k/4, 8-dim group k%4
-            ov[p][i] = __builtin_bit_cast(half4, bload_f32x2(ro, (p * NCOL * HD + (k0 + 4 * i) * 256 + 4 * lane) * 2));
+        for (int i = 0; i < 4; ++i)  // run k = k0 + 4i: dims tile k/2, 4-row pair k%2
+            ov[p][i] = bload_h8(ro, (p * NCOL * HD + (k0 + 4 * i) * 512 + 8 * lane) * 2);
     float wt[MAXP];
     float M = kNegInf;
 #pragma unroll
@@ -1258,21 +1286,27 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
         wt[p] = ml[p].x == kNegInf ? 0.0f : ml[p].y * fexp2(ml[p].x - M);
         L += wt[p];
     }
-    float4v o[8];
+    float4v o[8];  // o[2i + e]: rows 8e.. of run i
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        o[i] = float4v{0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) o[i] = float4v{0, 0, 0, 0};
 #pragma unroll
-        for (int p = 0; p < MAXP; ++p) o[i] += __builtin_convertvector(ov[p][i], float4v) * wt[p];
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int p = 0; p < MAXP; ++p) {
+            const half8 v = ov[p][i];
+            o[2 * i] += float4v{(float)v[0], (float)v[1], (float)v[2], (float)v[3]} * wt[p];
+            o[2 * i + 1] += float4v{(float)v[4], (float)v[5], (float)v[6], (float)v[7]} * wt[p];
+        }
     if (s_idx >= a.S) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + c % G) * HD + dbase;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int k = k0 + 4 * i, d = 32 * (k >> 2) + 8 * (k & 3) + 4 * h;
-        store4(orow + d, srq4(o[i] * inv, a.out_q));
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int k = k0 + 4 * i, d = 32 * (k >> 1) + 16 * (k & 1) + 8 * e + 4 * h;
+            store4(orow + d, srq4(o[2 * i + e] * inv, a.out_q));
+        }
 }
 
 typedef void (*prefill_fn)(PrefillArgs);
