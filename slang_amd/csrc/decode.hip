@@ -263,12 +263,13 @@ void decode_kernel(DecodeArgs a) {
     using VO = VOp<KVT>;
     typedef typename KO::raw kraw_t;
     typedef typename VO::raw vraw_t;
-    // hd 256, f16 caches: K rows are loaded whole, as V rows are (two 512-byte rows per
-    // instruction), and staged in a per-wave LDS block from which the MFMA A operands are
+    // f16 caches: K rows are loaded whole, as V rows are (two 512-byte rows or one 1 KiB row
+    // per instruction), and staged in a per-wave LDS block from which the MFMA A operands are
     // read. Loaded straight in the A layout, each instruction took 64 bytes from each of 16
     // rows; a read-only kernel over config 4's geometry streamed 6.9 TB/s with whole rows
-    // against 6.4 TB/s with that pattern.
-    constexpr bool KROW = HD == 256 && sizeof(KVT) == 2;
+    // against 6.4 TB/s with that pattern. (hd 512: 134 KiB of LDS, one workgroup a CU as
+    // its registers allow anyway.)
+    constexpr bool KROW = sizeof(KVT) == 2;
     constexpr int KSTR = Sh::KSTR;
     constexpr int ARENA = KROW && (Sh::V_HALVES + Sh::K_HALVES) * 2 > Sh::LDS_BYTES
                               ? (Sh::V_HALVES + Sh::K_HALVES) * 2 : Sh::LDS_BYTES;
