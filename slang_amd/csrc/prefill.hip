@@ -55,13 +55,17 @@ struct PrefillArgs {
 constexpr float kMaxLag = 15.0f;
 
 // Rows j0 .. j0 + 7 of a 32x32 accumulator tile (two 4-row groups of one lane) times inv,
-// as one 16-byte f16 store: the split pieces' partial O.
-template <typename ACC>
+// as one 16-byte f16 store: the split pieces' partial O. NT: on the non-temporal policy,
+// which the hd-256 pieces take (their 12 MB of partials at S 1024, with the q rows also
+// stored that way: config 3G 27.2 -> 26.5 us, 3S 25.2 -> 25.55 us) and the hd-512 ones do
+// not (29 MB: 47.3 -> 49.2 us).
+template <bool NT, typename ACC>
 __device__ __forceinline__ void store_part8(half_t* dst, const ACC& acc, int j0, float inv) {
     half8 v;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (half_t)(acc[j0 + i] * inv);
-    *reinterpret_cast<half8*>(dst) = v;
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<half8*>(dst));
+    else *reinterpret_cast<half8*>(dst) = v;
 }
 
 // LDS operand reads issued ahead of their MFMAs in prefill_kernel_w32: score product
@@ -101,7 +105,9 @@ __global__ __launch_bounds__(256) void qprep_kernel(const float* q, const float*
             hv[i] = (half_t)x[s][i];
             lv[i] = (half_t)(x[s][i] - (float)hv[i]);  // the f32-accurate split of G4A_Q_HILO
         }
-        *reinterpret_cast<half8*>(out + (size_t)row * HD + 32 * s + 8 * g) = hv;
+        // non-temporal: the attention kernel reads these rows after this kernel has ended
+        // (with the pieces' partials likewise: config 3G 27.2 -> 26.5 us, 3S 25.2 -> 25.55)
+        __builtin_nontemporal_store(hv, reinterpret_cast<half8*>(out + (size_t)row * HD + 32 * s + 8 * g));
         if (out_lo) *reinterpret_cast<half8*>(out_lo + (size_t)row * HD + 32 * s + 8 * g) = lv;
     }
 }
@@ -651,7 +657,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
+            for (int jp = 0; jp < 2; ++jp) store_part8<true>(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
@@ -932,7 +938,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
+            for (int jp = 0; jp < 2; ++jp) store_part8<false>(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0 && dh == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
@@ -1218,7 +1224,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-            for (int jp = 0; jp < 2; ++jp) store_part8(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
+            for (int jp = 0; jp < 2; ++jp) store_part8<false>(po + (2 * dt + jp) * 512, oacc[dt], 8 * jp, inv_p);
         if (h == 0) a.part_ml[blk * NCOL + c] = make_float2(m_use, l_tot);
         return;
     }
