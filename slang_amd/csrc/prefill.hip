@@ -662,7 +662,32 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         return;
     }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (col_ok) {
+    if constexpr (sizeof(OUTT) == 2) {
+        // f16 rows through LDS: each wave stages its 32 output rows (528-byte stride: the
+        // 8-byte writes of a store instruction fall on distinct banks), then stores two whole
+        // 512-byte rows an instruction. Written straight from the accumulator layout, every
+        // store instruction put 16 bytes into each of 32 rows.
+        constexpr int OSTR = HD * 2 + 16;
+        __syncthreads();  // every wave is done with the last tile's K/V
+        char* ost = lds + wave * 32 * OSTR;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(reinterpret_cast<half_t*>(ost + n32 * OSTR) + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
+            }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int rr = 2 * i + h, cc = 32 * wave + rr;  // lanes 32h..: the wave's row rr
+            const int so = qb * BQ + cc / G;
+            const half8 val = *reinterpret_cast<const half8*>(ost + rr * OSTR + 16 * n32);
+            if (so < a.S)
+                *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.out) +
+                                          ((size_t)so * a.n_q_heads + kh * G + cc % G) * HD + 8 * n32) = val;
+        }
+    } else if (col_ok) {
         OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
