@@ -968,7 +968,30 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32d(PrefillArgs a) {
         return;
     }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (col_ok) {
+    if constexpr (sizeof(OUTT) == 2) {
+        // f16 rows through LDS, as prefill_kernel_w32 stores them: each wave stages the 256
+        // dims of its 32 columns (528-byte stride), then stores two 512-byte runs an instruction
+        constexpr int OSTR = 256 * 2 + 16;
+        __syncthreads();  // every wave is done with the last tile's K/V
+        char* ost = lds + wave * 32 * OSTR;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(reinterpret_cast<half_t*>(ost + n32 * OSTR) + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
+            }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int rr = 2 * i + h, cc = 32 * pr + rr;  // lanes 32h..: the wave's row rr
+            const int so = qb * BQ + cc / G;
+            const half8 val = *reinterpret_cast<const half8*>(ost + rr * OSTR + 16 * n32);
+            if (so < a.S)
+                *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.out) +
+                                          ((size_t)so * a.n_q_heads + kh * G + cc % G) * HD + 256 * dh + 8 * n32) = val;
+        }
+    } else if (col_ok) {
         OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD + 256 * dh;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
@@ -1001,7 +1024,9 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
     constexpr int HD = 512, KT = 32, NCOL = 128, BQ = NCOL / G;
     constexpr int ROWB = HD * 2;      // 1 KiB rows
     constexpr int TILEB = KT * ROWB;  // one K or V tile: 32 KiB
-    __shared__ __attribute__((aligned(1024))) char lds[2 * 2 * TILEB];  // [buffer][K, V]
+    constexpr int OSTR = HD * 2 + 16;  // the epilogue's staged f16 output rows (1040 B apart)
+    constexpr int LDS_BYTES = 2 * 2 * TILEB > 4 * 32 * OSTR ? 2 * 2 * TILEB : 4 * 32 * OSTR;
+    __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // [buffer][K, V]; output rows
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1254,7 +1279,28 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
         return;
     }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (col_ok) {
+    if constexpr (sizeof(OUTT) == 2) {
+        // f16 rows through LDS, as prefill_kernel_w32 stores them: each wave stages its 32
+        // output rows, then stores one whole 1 KiB row an instruction
+        __syncthreads();  // every wave is done with the last tile's K/V
+        char* ost = lds + wave * 32 * OSTR;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4v v = float4v{oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2],
+                                          oacc[dt][4 * j + 3]} * inv;
+                store4(reinterpret_cast<half_t*>(ost + n32 * OSTR) + 32 * dt + 8 * j + 4 * h, srq4(v, a.out_q));
+            }
+#pragma unroll
+        for (int rr = 0; rr < 32; ++rr) {
+            const int cc = 32 * wave + rr, so = qb * BQ + cc / G;
+            const half8 val = *reinterpret_cast<const half8*>(ost + rr * OSTR + 16 * lane);
+            if (so < a.S)
+                *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.out) +
+                                          ((size_t)so * a.n_q_heads + kh * G + cc % G) * HD + 8 * lane) = val;
+        }
+    } else if (col_ok) {
         OUTT* orow = reinterpret_cast<OUTT*>(a.out) + ((size_t)s_idx * a.n_q_heads + kh * G + hh) * HD;
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt)
