@@ -431,14 +431,30 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
     const int N = g.n[p];
     const bool f32 = g.out_f32[p] != 0;
     const float oq = g.out_q[p], alpha = g.alpha[p];
+    // f16 tiles go out through LDS: staged as 128 rows of TN outputs (16 bytes of padding a
+    // row, so the 8-byte writes of an instruction fall on distinct banks), then stored as
+    // whole row segments, 16 bytes a thread; written straight from the accumulator layout,
+    // every store instruction put 16 bytes into each of 32 rows
+    constexpr int OS = TN * 2 + 16;
+    static_assert(BM * OS <= STAGES * STAGEB, "the staged tile fits the operand stages");
+    auto store_staged = [&](half_t* out) {
+        __syncthreads();
+        constexpr int CH = TN / 8;  // 16-byte chunks a row
+#pragma unroll
+        for (int i = 0; i < BM * CH / 256; ++i) {
+            const int idx = 256 * i + tid, r = idx / CH, ch = idx % CH;
+            if (m0 + r < g.M)
+                *reinterpret_cast<half8*>(out + (size_t)(m0 + r) * N + n0 + 8 * ch) =
+                    *reinterpret_cast<const half8*>(lds + r * OS + 16 * ch);
+        }
+    };
     if constexpr (GEGLU) {
+        __syncthreads();  // every wave is done with the last stage's operands
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-            const int m = m0 + 64 * wm + 32 * mb + l32;
-            if (m >= g.M) continue;
+            const int r = 64 * wm + 32 * mb + l32;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int n = n0 + 32 * wn + 8 * q + 4 * h;
                 half4 y;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -446,9 +462,28 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
                     const float uv = (float)(half_t)pin(alpha * acc[1][mb][4 * q + i]);
                     y[i] = geglu_code(gv, uv, g.gq, g.uq, g.oq, g.lut);
                 }
-                *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(g.out[0]) + (size_t)m * N + n) = y;
+                *reinterpret_cast<half4*>(lds + r * OS + (32 * wn + 8 * q + 4 * h) * 2) = y;
             }
         }
+        store_staged(reinterpret_cast<half_t*>(g.out[0]));
+        return;
+    }
+    if (!f32) {
+        __syncthreads();  // every wave is done with the last stage's operands
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int r = 64 * wm + 32 * mb + l32;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    half4 y;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) y[i] = (half_t)pin(alpha * acc[nb][mb][4 * q + i]);
+                    *reinterpret_cast<half4*>(lds + r * OS + ((BN / 2) * wn + 32 * nb + 8 * q + 4 * h) * 2) = y;
+                }
+        }
+        store_staged(reinterpret_cast<half_t*>(g.out[p]));
         return;
     }
 #pragma unroll
@@ -463,10 +498,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(Gemm16Args g) {
                 float4v v;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = (float)(half_t)pin(alpha * acc[nb][mb][4 * q + i]);
-                if (f32)
-                    store4(reinterpret_cast<float*>(g.out[p]) + (size_t)m * N + n, srq4(v, oq));
-                else
-                    store4(reinterpret_cast<half_t*>(g.out[p]) + (size_t)m * N + n, v);
+                store4(reinterpret_cast<float*>(g.out[p]) + (size_t)m * N + n, srq4(v, oq));
             }
     }
 }
