@@ -1019,13 +1019,13 @@ __device__ __forceinline__ void mfma32_acc(float16v& acc, half8 a, half8 b) {
     asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-template <int G, typename OUTT>
+template <int G, typename OUTT, bool QSTAGE, bool OSTAGE>
 __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
     constexpr int HD = 512, KT = 32, NCOL = 128, BQ = NCOL / G;
     constexpr int ROWB = HD * 2;      // 1 KiB rows
     constexpr int TILEB = KT * ROWB;  // one K or V tile: 32 KiB
     constexpr int OSTR = HD * 2 + 16;  // the epilogue's staged f16 output rows (1040 B apart)
-    constexpr int LDS_BYTES = 2 * 2 * TILEB > 4 * 32 * OSTR ? 2 * 2 * TILEB : 4 * 32 * OSTR;
+    constexpr int LDS_BYTES = !OSTAGE || 2 * 2 * TILEB > 4 * 32 * OSTR ? 2 * 2 * TILEB : 4 * 32 * OSTR;
     __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // [buffer][K, V]; output rows
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1076,40 +1076,51 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
     };
 
     // ---- q: lane (column c, half h) holds dims 16s + 8h .. +7 (s < 32), the B operand
-    // layout. Wave w DMAs the f16 q rows of its 32 columns, whole 1 KiB rows (chunk n of a
-    // row from logical chunk n ^ (column % 32)), into its 16 KiB of the LDS stage that tile
-    // t0 + 1 takes over later, in two rounds of 16 rows (the stage holds half of the
-    // workgroup's 128 KiB of q), and reads each round back in the B-operand layout; tile
-    // t0's DMA goes out after the first round's. (Loaded straight in the operand layout,
-    // every load instruction took 32 bytes from each of 32 rows, and the workgroup's
-    // 128 KiB came through L1 about four times: 9 us of a 48 us call at S 1024.)
+    // layout. QSTAGE (the launches with a key split, whose many pieces start at once): wave w
+    // DMAs the f16 q rows of its 32 columns, whole 1 KiB rows (chunk n of a row from logical
+    // chunk n ^ (column % 32)), into its 16 KiB of the LDS stage that tile t0 + 1 takes over
+    // later, in two rounds of 16 rows (the stage holds half of the workgroup's 128 KiB of q),
+    // and reads each round back in the B-operand layout; tile t0's DMA goes out after the
+    // first round's. Loaded straight in the operand layout, every load instruction took 32
+    // bytes from each of 32 rows: S 1024 global 48.2 -> 47.6 us a call with the staging.
+    // Without a split the q rows load straight, all 32 loads at once behind tile t0's DMA:
+    // the staged form, even compiled beside the direct one and not taken, made the S 8192
+    // global kernel 684 -> 707 us (the same tile loop, instruction for instruction).
     half8 qf[32];
     {
         const rsrc_t rq = make_rsrc(a.q16, (uint32_t)a.S * a.n_q_heads * HD * 2);
-        char* qs = lds + ((t0 + 1) & 1) * 2 * TILEB + wave * 16 * ROWB;
+        if constexpr (QSTAGE) {
+            char* qs = lds + ((t0 + 1) & 1) * 2 * TILEB + wave * 16 * ROWB;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
+            for (int r = 0; r < 2; ++r) {
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int cj = 32 * wave + 16 * r + j;  // the column whose row this DMA moves
-                const int qo = ((qb * BQ + cj / G) * a.n_q_heads + kh * G + cj % G) * ROWB + 16 * (ln ^ (16 * r + j));
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(qs + j * ROWB),
-                                                         16, qo, 0, 0, 0);
-            }
-            if (r == 0 && t0 < t1) {
-                issue(t0, t0 & 1);
-                asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // the 16 q DMAs before tile t0's
-            } else {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            }
-            if ((n32 >> 4) == r) {
-                const char* qrow = qs + (n32 & 15) * ROWB;
+                for (int j = 0; j < 16; ++j) {
+                    const int cj = 32 * wave + 16 * r + j;  // the column whose row this DMA moves
+                    const int qo = ((qb * BQ + cj / G) * a.n_q_heads + kh * G + cj % G) * ROWB + 16 * (ln ^ (16 * r + j));
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(qs + j * ROWB),
+                                                             16, qo, 0, 0, 0);
+                }
+                if (r == 0 && t0 < t1) {
+                    issue(t0, t0 & 1);
+                    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // the 16 q DMAs before tile t0's
+                } else {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                }
+                if ((n32 >> 4) == r) {
+                    const char* qrow = qs + (n32 & 15) * ROWB;
 #pragma unroll
-                for (int s = 0; s < 32; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
+                    for (int s = 0; s < 32; ++s) qf[s] = *reinterpret_cast<const half8*>(qrow + 16 * ((2 * s + h) ^ n32));
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's 16 KiB free again
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's 16 KiB free again
+        } else {
+            const int qo = (s_idx * a.n_q_heads + kh * G + hh) * ROWB + 16 * h;
+#pragma unroll
+            for (int s = 0; s < 32; ++s) qf[s] = bload_h8(rq, qo + 32 * s);
+            if (t0 < t1) issue(t0, t0 & 1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         if (!col_ok) {
 #pragma unroll
@@ -1279,9 +1290,12 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32h(PrefillArgs a) {
         return;
     }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if constexpr (sizeof(OUTT) == 2) {
+    if constexpr (OSTAGE && sizeof(OUTT) == 2) {
         // f16 rows through LDS, as prefill_kernel_w32 stores them: each wave stages its 32
-        // output rows, then stores one whole 1 KiB row an instruction
+        // output rows, then stores one whole 1 KiB row an instruction. Launches with a key
+        // split or a window take it (S 1024 global 47.0 -> 44.7 us a call, S 8192 W 512
+        // 181 -> 176 us); the unsplit causal launch stores straight (with the staging its
+        // S 8192 kernel took 705-709 against 684-689 us)
         __syncthreads();  // every wave is done with the last tile's K/V
         char* ost = lds + wave * 32 * OSTR;
 #pragma unroll
@@ -1399,15 +1413,17 @@ static prefill_fn pick_w32(bool out32, bool hilo, bool klo) {
     return klo ? pick_w32_out<HD, G, false, true>(out32) : pick_w32_out<HD, G, false, false>(out32);
 }
 template <int G>
-static prefill_fn pick_w32h(bool out32) {
-    return out32 ? prefill_kernel_w32h<G, float> : prefill_kernel_w32h<G, half_t>;
+static prefill_fn pick_w32h(bool out32, bool qstage, bool ostage) {
+    if (qstage) return out32 ? prefill_kernel_w32h<G, float, true, true> : prefill_kernel_w32h<G, half_t, true, true>;
+    if (ostage) return out32 ? prefill_kernel_w32h<G, float, false, true> : prefill_kernel_w32h<G, half_t, false, true>;
+    return out32 ? prefill_kernel_w32h<G, float, false, false> : prefill_kernel_w32h<G, half_t, false, false>;
 }
-static prefill_fn pick_g_w32h(int G, bool out32) {
+static prefill_fn pick_g_w32h(int G, bool out32, bool qstage, bool ostage) {
     switch (G) {
-        case 1: return pick_w32h<1>(out32);
-        case 2: return pick_w32h<2>(out32);
-        case 4: return pick_w32h<4>(out32);
-        case 8: return pick_w32h<8>(out32);
+        case 1: return pick_w32h<1>(out32, qstage, ostage);
+        case 2: return pick_w32h<2>(out32, qstage, ostage);
+        case 4: return pick_w32h<4>(out32, qstage, ostage);
+        case 8: return pick_w32h<8>(out32, qstage, ostage);
     }
     return nullptr;
 }
@@ -1587,7 +1603,7 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     // the low parts), prefill_kernel_w32d for G4A_Q_HILO
     const bool w32h = HD == 512 && !hilo;
     const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo)
-                          : w32h    ? pick_g_w32h(G, out32)
+                          : w32h    ? pick_g_w32h(G, out32, split, split || cfg->window > 0)
                                     : pick_g<512>(G, out32, hilo, klo);
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
