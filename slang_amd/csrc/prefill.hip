@@ -249,7 +249,7 @@ __device__ __forceinline__ PrefillUnit prefill_unit(const PrefillArgs& a, int la
     return PrefillUnit{kh, qb, piece, n_pieces};
 }
 
-template <int G, typename OUTT, bool HILO, bool KLO>
+template <int G, typename OUTT, bool HILO, bool KLO, bool SPLITK>
 __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     constexpr int HD = 256, KT = 64, NCOL = 128, BQ = NCOL / G;
     constexpr int QMF = HILO ? 2 : 1;  // score MFMAs per K operand (q high, then low parts)
@@ -327,7 +327,10 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
     // sum of squares, is that of prep_q_column (qprep_kernel), so both round q to the
     // same f16 values: lane h holds prep_q_column's k-groups h (even s) and h + 2 (odd s).
     half8 qf[16], ql[HILO ? 16 : 1];
-    if (a.q16) {  // q prepared by qprep_kernel for every piece of the call at once
+    // SPLITK: a launch with a key split, whose q16 comes from qprep_kernel (a template flag,
+    // so each launch runs a kernel with only its own prologue and epilogue: 3S 24.95 -> 23.7 us,
+    // 3G 26.5 -> 26.1 us against one kernel holding both)
+    if constexpr (SPLITK) {  // q prepared by qprep_kernel for every piece of the call at once
         // Wave w DMAs the f16 q rows of its own 32 columns (two 512-byte rows per
         // instruction, chunk n32 of a row from logical chunk n32 ^ (row % 32)) into the LDS
         // stage that tile t0 + 1 takes over later, then reads them back in the B-operand
@@ -649,7 +652,7 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
 
     // ---- epilogue: column sum over both halves, normalise, srq, store 4 dims at a time
     const float l_tot = add32(l_run);
-    if (n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
+    if (SPLITK && n_pieces > 1) {  // a piece of a split query block: O / l in f16 and (m, l) in f32
         const size_t blk = ((size_t)kh * a.n_qblocks + qb) * a.max_pieces + piece;
         const float inv_p = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
         // one 1 KiB run per store instruction: [wave][dt][j pair][lane] half8
@@ -1403,14 +1406,18 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 typedef void (*prefill_fn)(PrefillArgs);
 
 template <int HD, int G, bool HILO, bool KLO>
-static prefill_fn pick_w32_out(bool out32) {
-    if constexpr (HD == 256) return out32 ? prefill_kernel_w32<G, float, HILO, KLO> : prefill_kernel_w32<G, half_t, HILO, KLO>;
-    else return out32 ? prefill_kernel_w32d<G, float, HILO, KLO> : prefill_kernel_w32d<G, half_t, HILO, KLO>;
+static prefill_fn pick_w32_out(bool out32, bool split) {
+    if constexpr (HD == 256) {
+        if (split) return out32 ? prefill_kernel_w32<G, float, HILO, KLO, true> : prefill_kernel_w32<G, half_t, HILO, KLO, true>;
+        return out32 ? prefill_kernel_w32<G, float, HILO, KLO, false> : prefill_kernel_w32<G, half_t, HILO, KLO, false>;
+    } else {
+        return out32 ? prefill_kernel_w32d<G, float, HILO, KLO> : prefill_kernel_w32d<G, half_t, HILO, KLO>;
+    }
 }
 template <int HD, int G>
-static prefill_fn pick_w32(bool out32, bool hilo, bool klo) {
-    if (hilo) return klo ? pick_w32_out<HD, G, true, true>(out32) : pick_w32_out<HD, G, true, false>(out32);
-    return klo ? pick_w32_out<HD, G, false, true>(out32) : pick_w32_out<HD, G, false, false>(out32);
+static prefill_fn pick_w32(bool out32, bool hilo, bool klo, bool split) {
+    if (hilo) return klo ? pick_w32_out<HD, G, true, true>(out32, split) : pick_w32_out<HD, G, true, false>(out32, split);
+    return klo ? pick_w32_out<HD, G, false, true>(out32, split) : pick_w32_out<HD, G, false, false>(out32, split);
 }
 template <int G>
 static prefill_fn pick_w32h(bool out32, bool qstage, bool ostage) {
@@ -1428,12 +1435,12 @@ static prefill_fn pick_g_w32h(int G, bool out32, bool qstage, bool ostage) {
     return nullptr;
 }
 template <int HD>
-static prefill_fn pick_g(int G, bool out32, bool hilo, bool klo) {
+static prefill_fn pick_g(int G, bool out32, bool hilo, bool klo, bool split) {
     switch (G) {
-        case 1: return pick_w32<HD, 1>(out32, hilo, klo);
-        case 2: return pick_w32<HD, 2>(out32, hilo, klo);
-        case 4: return pick_w32<HD, 4>(out32, hilo, klo);
-        case 8: return pick_w32<HD, 8>(out32, hilo, klo);
+        case 1: return pick_w32<HD, 1>(out32, hilo, klo, split);
+        case 2: return pick_w32<HD, 2>(out32, hilo, klo, split);
+        case 4: return pick_w32<HD, 4>(out32, hilo, klo, split);
+        case 8: return pick_w32<HD, 8>(out32, hilo, klo, split);
     }
     return nullptr;
 }
@@ -1602,9 +1609,9 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
     // hd 512: prefill_kernel_w32h for f16 q (its 128 q registers a wave leave no room for
     // the low parts), prefill_kernel_w32d for G4A_Q_HILO
     const bool w32h = HD == 512 && !hilo;
-    const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo)
+    const prefill_fn fn = HD == 256 ? pick_g<256>(G, out32, hilo, klo, split)
                           : w32h    ? pick_g_w32h(G, out32, split, split || cfg->window > 0)
-                                    : pick_g<512>(G, out32, hilo, klo);
+                                    : pick_g<512>(G, out32, hilo, klo, split);
     if (!fn) {
         set_error("no prefill kernel for group size %d", G);
         return G4A_EUNSUPPORTED;
