@@ -42,6 +42,7 @@ struct PrefillArgs {
     // blocks with more tiles leave partials for prefill_merge_kernel
     int split_tiles, max_pieces, pieces_per_head;
     int xcd_runs;  // prefill_kernel_w32 unsplit: 1-D grid, query blocks in contiguous runs per XCD
+    int xcd_heads;  // unsplit causal: 1-D grid, kv head h on XCDs 8h/kvH .., its blocks longest first
     const half_t* q16;  // prefill_kernel_w32: q already prepared in f16 (qprep_kernel), or NULL
     const half_t* q16lo;  // ... and with G4A_Q_HILO its f16 low parts (q - f32(q16))
     int kv_row0;  // prefill_kernel_w32: first row held in kc/vc (rows below it are never read)
@@ -218,6 +219,13 @@ __device__ __forceinline__ PrefillUnit prefill_unit(const PrefillArgs& a, int la
         return (hi - lo + KT - 1) / KT;
     };
     int kh = blockIdx.y, qb = a.n_qblocks - 1 - (int)blockIdx.x, piece = 0, n_pieces = 1;
+    if (a.xcd_heads) {
+        // causal, unsplit: kv head kh on its own 8/kvH XCDs (the dispatcher deals workgroup L
+        // to XCD L % 8), each head's blocks longest first across them
+        const int L = blockIdx.x, x = L % 8, hpx = 8 / a.n_kv_heads;
+        kh = x / hpx;
+        qb = a.n_qblocks - 1 - ((L / 8) * hpx + x % hpx);
+    }
     if (a.xcd_runs) {
         // sliding window, unsplit: a 1-D grid over (kv head, query block) in contiguous runs
         // per XCD, so neighbouring blocks -- which share most of their window's K/V tiles --
@@ -1686,8 +1694,10 @@ extern "C" int g4a_prefill(const g4a_cfg* cfg, int S, int start_pos, const float
         a.part_ml = (float2*)(wsp + sp.o_bytes);
     }
     a.xcd_runs = a.split_tiles == 0 && cfg->window > 0;
+    a.xcd_heads = a.split_tiles == 0 && cfg->window == 0 && 8 % cfg->n_kv_heads == 0 &&
+                  ((int64_t)a.n_qblocks * cfg->n_kv_heads) % 8 == 0;
     const dim3 grid = a.split_tiles > 0 ? dim3(sp.total_pieces * cfg->n_kv_heads)
-                      : a.xcd_runs      ? dim3(a.n_qblocks * cfg->n_kv_heads)
+                      : a.xcd_runs || a.xcd_heads ? dim3(a.n_qblocks * cfg->n_kv_heads)
                                         : dim3(a.n_qblocks, cfg->n_kv_heads);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();
