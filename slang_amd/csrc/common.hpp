@@ -262,6 +262,14 @@ __device__ __forceinline__ void prep_q_column(const float* qr, const float* gain
         }
 }
 
+// Position of workgroup L in a work list cut into 8 contiguous runs, one per XCD (the
+// dispatcher deals workgroup L to XCD L % 8): XCDs x < r take `per` items, the rest per - 1.
+__device__ __forceinline__ int xcd_run_index() {
+    const int N = gridDim.x, L = blockIdx.x, x = L % 8, slot = L / 8;
+    const int per = (N + 7) / 8, r = N - 8 * (per - 1);
+    return x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
+}
+
 // One RoPE pair (d, d + hd/2) of a new k and v row, per thread t = d < hd/2 of the first
 // hd/128 waves (kvnorm, kernels_dsl.py:573-618; kvnorm_b, :1789-1834): k <- RoPE(RMSNorm(k)
 // * gain), v <- RMSNorm(v) without scale. The sums of squares run per wave then over the

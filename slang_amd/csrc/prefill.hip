@@ -188,14 +188,6 @@ __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
 
 __device__ __forceinline__ int vswz(int r) { return (0x6CA0 >> (4 * (r & 3))) & 15; }
 
-// Position of workgroup L in a work list cut into 8 contiguous runs, one per XCD (the
-// dispatcher deals workgroup L to XCD L % 8): XCDs x < r take `per` items, the rest per - 1.
-__device__ __forceinline__ int xcd_run_index() {
-    const int N = gridDim.x, L = blockIdx.x, x = L % 8, slot = L / 8;
-    const int per = (N + 7) / 8, r = N - 8 * (per - 1);
-    return x < r ? x * per + slot : r * per + (x - r) * (per - 1) + slot;
-}
-
 // ---- the workgroup's query block (longest causal rows first) and, with a key split, its
 // piece: the work lists of the 32-column kernels (query blocks of BQ positions, KT-key tiles).
 // The split grid is 1-D: the work list (kv head, block from the longest, piece) is cut into
