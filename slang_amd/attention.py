@@ -239,8 +239,9 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, workspace: 
     accuracy too (attn_prefill's form), where q in f16 converts both caches to f16 as the
     GEMM form's srqh_b does. `workspace` is the caller's scratch (prefill_ws_bytes bytes):
     f32 caches and hd 512 need it, and short prompts split long causal rows over
-    workgroups through it. split=False runs hd 256 on f16 caches unsplit, without it (one
-    kernel, the q prologue fused in).
+    workgroups through it. split=False runs the call unsplit on f16 caches: hd 256 without
+    the workspace (one kernel, the q prologue fused in), hd 512 with only the workspace's
+    f16 q rows (the launch long prompts take).
     """
     S = q.shape[0]
     if q.shape[1:] != (cfg.n_q_heads, cfg.head_dim):
@@ -265,9 +266,12 @@ def prefill(q, k_cache, v_cache, start_pos: int, cfg: AttnConfig, *, workspace: 
     lib = _lib.load()
     ws_bytes = lib.g4a_prefill_ws_bytes(ctypes.byref(c), S, int(start_pos))
     if not split:
-        if kv32 or cfg.head_dim != 256:
-            raise ValueError("split=False is the hd-256 f16-cache call without a workspace")
-        ws_bytes = 0
+        if kv32:
+            raise ValueError("split=False runs on f16 caches")
+        # a workspace below the split's size (g4a_prefill_ws_bytes) but holding the f16 q
+        # rows hd 512 needs runs the call unsplit
+        q16 = (S * cfg.n_q_heads * cfg.head_dim * 2 + 255) // 256 * 256
+        ws_bytes = 0 if cfg.head_dim == 256 else q16 * (2 if q_hilo else 1)
     ws = workspace.get(ws_bytes) if ws_bytes else None
     check(lib.g4a_prefill(ctypes.byref(c), S, int(start_pos), _ptr(q), _ptr(q_gain), _ptr(rope_cos),
                           _ptr(rope_sin), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(ws),

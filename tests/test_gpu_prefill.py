@@ -202,6 +202,30 @@ def test_hd512_e2b_shape(S, start, window):
                      f"hd512 S={S} start={start} W={window}")
 
 
+@pytest.mark.parametrize("S,start,window", [(1024, 0, 0), (1024, 0, 512), (300, 600, 0)])
+def test_hd512_unsplit_launch(S, start, window):
+    """The hd-512 launches long prompts take, forced at test sizes (split=False: a workspace
+    with only the f16 q rows): the causal one runs the 128-column kernel without q or output
+    staging, the windowed one with output staging only. Both q modes against the oracle, and
+    the f16-q result against the split call's within the contract."""
+    T = start + S
+    q, qg, k, v, cos, sin = config3_inputs(S=T, theta=1e6 if window == 0 else 1e4, seed=3 * S + window,
+                                           nH=8, kvH=1, hd=512)
+    q, cos, sin = q[start:], cos[start:], sin[start:]
+    cfg = sa.AttnConfig(8, 1, 512, window)
+    kw = dict(q_gain=qg, rope_cos=cos, rope_sin=sin)
+    q16 = kernel_q16(q, cfg, qg, cos, sin).astype(np.float32)
+    ref16 = O.prefill_attention(q16, k, v, start, 1, window=window, scale=cfg.scale)
+    whole = run(q, k, v, start, cfg, out_dtype=torch.float32, split=False, **kw)
+    contract_close(whole, ref16, f"hd512 unsplit S={S} start={start} W={window} (f16 q)")
+    split = run(q, k, v, start, cfg, out_dtype=torch.float32, **kw)
+    contract_close(split, whole, f"hd512 split vs unsplit S={S} W={window}")
+    ref32 = O.prefill_attention(q, k, v, start, 1, q_gain=qg, cos=cos, sin=sin, window=window,
+                                scale=cfg.scale, q_round_f16=False)
+    whole32 = run(q, k, v, start, cfg, out_dtype=torch.float32, q_hilo=True, split=False, **kw)
+    contract_close(whole32, ref32, f"hd512 unsplit S={S} W={window} (f32 q)")
+
+
 @pytest.mark.parametrize("S,start,window", [(100, 700, 512), (37, 0, 0), (1, 0, 0), (1, 900, 0),
                                             (129, 383, 128), (250, 6, 5)])
 @pytest.mark.parametrize("nH,kvH", [(8, 2), (4, 4), (8, 1), (4, 2)])
