@@ -281,6 +281,11 @@ __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, fl
                                              const float* rcos, const float* rsin, bool v_norm, float eps,
                                              float* red, int t) {
     constexpr int HALF = HD / 2, NW = HALF / 64;
+    // the gain and rotation operands load before the reduction and its barrier (which no
+    // memory access crosses), so they are not a second round trip after it
+    const int tl = t < HALF ? t : 0;
+    const float g0 = k_gain ? k_gain[tl] : 1.0f, g1 = k_gain ? k_gain[tl + HALF] : 1.0f;
+    const float c = rcos ? rcos[tl] : 1.0f, sn = rcos ? rsin[tl] : 0.0f;
     const float sk_w = wave_sum(k0 * k0 + k1 * k1), sv_w = wave_sum(v0 * v0 + v1 * v1);
     if (t < HALF && (t & 63) == 0) {
         red[t >> 6] = sk_w;
@@ -296,14 +301,15 @@ __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, fl
     }
     if (k_gain) {
         const float rs = 1.0f / sqrtf(sk / (float)HD + eps);  // kvnorm's k * rmsk * knorm
-        k0 = k0 * rs * k_gain[t];
-        k1 = k1 * rs * k_gain[t + HALF];
+        k0 = k0 * rs * g0;
+        k1 = k1 * rs * g1;
     }
     if (rcos) {
-        const float c = rcos[t], sn = rsin[t];
+        // explicit fma forms: the two kernels that inline this (g4a_kv_write's and the fused
+        // decode write) must not contract the rotation differently
         const float x0 = k0, x1 = k1;
-        k0 = x0 * c - x1 * sn;
-        k1 = x1 * c + x0 * sn;
+        k0 = __builtin_fmaf(x0, c, -(x1 * sn));
+        k1 = __builtin_fmaf(x1, c, x0 * sn);
     }
     if (v_norm) {
         const float rs = 1.0f / sqrtf(sv / (float)HD + eps);
