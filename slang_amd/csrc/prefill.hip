@@ -388,13 +388,16 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
         if (wave == 0)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rgn, (__attribute__((address_space(3))) void*)shr, 16, 16 * lane, 0, 0, 0);
         if constexpr (ROPE_LDS) {
-            // BQ rows of 512 B per table from token row qb * BQ: 1 KiB per wave instruction
+            // BQ rows of 512 B per table from token row qb * BQ: 1 KiB per wave instruction,
+            // the 16-byte chunk c of row r at c ^ (r % 8), so the rows a quarter-wave reads
+            // (up to 4 positions, 512 B apart) fall on distinct banks
             constexpr int PER_WAVE = (BQ / 2 + 3) / 4;
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j) {
                 const int ins = 4 * j + wave;  // the table's ins-th KiB
                 if (ins < BQ / 2) {
-                    const int go = (qb * BQ * 512) + 1024 * ins + 16 * lane;
+                    const int rr = 2 * ins + (lane >> 5);
+                    const int go = (qb * BQ * 512) + 512 * rr + 16 * ((lane & 31) ^ (rr & 7));
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
                         rc, (__attribute__((address_space(3))) void*)(shr + 1024 + 1024 * ins), 16, go, 0, 0, 0);
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -434,14 +437,16 @@ __global__ __launch_bounds__(256) void prefill_kernel_w32(PrefillArgs a) {
             return float8v{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
         };
         if constexpr (ROPE_LDS) {
-            const float* cl = reinterpret_cast<const float*>(shr + 1024) + pl * 128 + 8 * h;
-            const float* sl = cl + BQ * 128;
+            const char* cl = shr + 1024 + pl * 512;
+            const char* sl = cl + BQ * 512;
+            const int sw = pl & 7;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const float4v c0 = *reinterpret_cast<const float4v*>(cl + 16 * s);
-                const float4v c1 = *reinterpret_cast<const float4v*>(cl + 16 * s + 4);
-                const float4v s0 = *reinterpret_cast<const float4v*>(sl + 16 * s);
-                const float4v s1 = *reinterpret_cast<const float4v*>(sl + 16 * s + 4);
+                const int c0i = 16 * ((4 * s + 2 * h) ^ sw), c1i = 16 * ((4 * s + 2 * h + 1) ^ sw);
+                const float4v c0 = *reinterpret_cast<const float4v*>(cl + c0i);
+                const float4v c1 = *reinterpret_cast<const float4v*>(cl + c1i);
+                const float4v s0 = *reinterpret_cast<const float4v*>(sl + c0i);
+                const float4v s1 = *reinterpret_cast<const float4v*>(sl + c1i);
                 cv[s] = float8v{c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
                 sv[s] = float8v{s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
             }
