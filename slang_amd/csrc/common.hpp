@@ -271,21 +271,26 @@ __device__ __forceinline__ int xcd_run_index() {
 }
 
 // One RoPE pair (d, d + hd/2) of a new k and v row, per thread t = d < hd/2 of the first
-// hd/128 waves (kvnorm, kernels_dsl.py:573-618; kvnorm_b, :1789-1834): k <- RoPE(RMSNorm(k)
-// * gain), v <- RMSNorm(v) without scale. The sums of squares run per wave then over the
+// hd/128 waves (kvnorm, kernels_dsl.py:573-618; kvnorm_b, :1789-1834): k <- RoPE(RMSNorm(
+// srq(k)) * gain), v <- RMSNorm(srq(v)) without scale, from the raw loaded values. The sums of squares run per wave then over the
 // waves in order through `red` (2 x hd/128 floats of LDS), so g4a_kv_write and the fused
 // decode write identical rows. Every wave of the workgroup must call it (one barrier);
 // threads t >= hd/2 pass zeros and ignore the result.
 template <int HD>
 __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, float& v1, const float* k_gain,
                                              const float* rcos, const float* rsin, bool v_norm, float eps,
-                                             float* red, int t) {
+                                             float k_in_q, float v_in_q, float* red, int t) {
     constexpr int HALF = HD / 2, NW = HALF / 64;
-    // the gain and rotation operands load before the reduction and its barrier (which no
-    // memory access crosses), so they are not a second round trip after it
+    // the gain and rotation operands load before srq (whose zero-scale branch waits for
+    // the raw values) and before the reduction's barrier (which no memory access crosses),
+    // so they share the raw row's round trip
     const int tl = t < HALF ? t : 0;
     const float g0 = k_gain ? k_gain[tl] : 1.0f, g1 = k_gain ? k_gain[tl + HALF] : 1.0f;
     const float c = rcos ? rcos[tl] : 1.0f, sn = rcos ? rsin[tl] : 0.0f;
+    k0 = srq(k0, k_in_q);
+    k1 = srq(k1, k_in_q);
+    v0 = srq(v0, v_in_q);
+    v1 = srq(v1, v_in_q);
     const float sk_w = wave_sum(k0 * k0 + k1 * k1), sv_w = wave_sum(v0 * v0 + v1 * v1);
     if (t < HALF && (t & 63) == 0) {
         red[t >> 6] = sk_w;

@@ -353,10 +353,12 @@ void decode_kernel(DecodeArgs a) {
     float nk0 = 0.0f, nk1 = 0.0f, nv0 = 0.0f, nv1 = 0.0f;
     if (owns_new && tid < HALF) {
         const size_t ro = ((size_t)b * a.n_kv_heads + kh) * HD;
-        nk0 = srq(a.k_new[ro + tid], a.k_in_q);
-        nk1 = srq(a.k_new[ro + tid + HALF], a.k_in_q);
-        nv0 = srq(a.v_new[ro + tid], a.v_in_q);
-        nv1 = srq(a.v_new[ro + tid + HALF], a.v_in_q);
+        // raw values: kv_pair_prep applies srq (a zero-scale branch here would wait for
+        // each load before issuing the next and the block loads)
+        nk0 = a.k_new[ro + tid];
+        nk1 = a.k_new[ro + tid + HALF];
+        nv0 = a.v_new[ro + tid];
+        nv1 = a.v_new[ro + tid + HALF];
     }
 
     // ---- block loads through buffer resources over rows [k0, k1) of this kv head: rows
@@ -433,7 +435,8 @@ void decode_kernel(DecodeArgs a) {
     }
     if (owns_new) {  // every wave takes part (one barrier inside)
         kv_pair_prep<HD>(nk0, nk1, nv0, nv1, a.k_gain, a.rcos ? a.rcos + (size_t)b * HALF : nullptr,
-                         a.rsin ? a.rsin + (size_t)b * HALF : nullptr, a.v_norm != 0, a.eps, kv_red, tid);
+                         a.rsin ? a.rsin + (size_t)b * HALF : nullptr, a.v_norm != 0, a.eps, a.k_in_q, a.v_in_q,
+                         kv_red, tid);
         if (tid < HALF) {
             const size_t crow = (size_t)b * a.seq_stride + (size_t)p_new * a.n_kv_heads * HD + (size_t)kh * HD;
             KVT* kcw = reinterpret_cast<KVT*>(a.kc_out) + crow;

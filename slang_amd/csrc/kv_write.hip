@@ -32,11 +32,13 @@ __global__ __launch_bounds__(HD / 2) void kv_write_kernel(KvArgs a) {
     const size_t row = ((size_t)s * a.n_kv_heads + kh) * HD;
     const IT* kin = reinterpret_cast<const IT*>(a.k) + row;
     const IT* vin = reinterpret_cast<const IT*>(a.v) + row;
-    float k0 = srq(ld(kin + t), a.k_in_q), k1 = srq(ld(kin + t + HALF), a.k_in_q);
-    float v0 = srq(ld(vin + t), a.v_in_q), v1 = srq(ld(vin + t + HALF), a.v_in_q);
+    // raw values: kv_pair_prep applies srq once its own operand loads are out (written as
+    // srq(ld(..)) here, each load waited behind the previous one's zero-scale branch)
+    float k0 = ld(kin + t), k1 = ld(kin + t + HALF), v0 = ld(vin + t), v1 = ld(vin + t + HALF);
 
     kv_pair_prep<HD>(k0, k1, v0, v1, a.k_gain, a.rcos ? a.rcos + (size_t)s * HALF : nullptr,
-                     a.rsin ? a.rsin + (size_t)s * HALF : nullptr, a.v_norm != 0, a.eps, red, t);
+                     a.rsin ? a.rsin + (size_t)s * HALF : nullptr, a.v_norm != 0, a.eps, a.k_in_q, a.v_in_q,
+                     red, t);
     const size_t crow = ((size_t)(a.start_pos + s) * a.n_kv_heads + kh) * HD;
     CT* kc = reinterpret_cast<CT*>(a.kc) + crow;
     CT* vc = reinterpret_cast<CT*>(a.vc) + crow;
