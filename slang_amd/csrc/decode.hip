@@ -388,7 +388,10 @@ void decode_kernel(DecodeArgs a) {
         for (int i = 0; i < VLOADS; ++i) vr[i] = VO::load(rv, r + VROWS * i * rsb + voff);
     };
     int blk = k0 + wave * 16;
-    if (blk < k1) load_block(blk);  // in flight during the q prologue (wave-uniform branch)
+    // in flight during the q prologue. Unconditional: a block past k1 reads zeros without
+    // memory traffic. Under a branch, the join left the compiler unsure how many loads
+    // followed q's, so the prologue waited for the block's loads too (vmcnt(4), not 20).
+    load_block(blk);
 
     // ---- q prologue: RMSNorm*gain, RoPE, scale*log2 e, split into f16 high/low rows of
     // the B operand, staged in LDS.
