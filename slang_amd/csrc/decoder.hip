@@ -212,30 +212,59 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // rows past n_out read as zeros through the buffer range
     const uint32_t wbytes = (uint32_t)g.n_out * (uint32_t)nch * 16u;
     const rsrc_t rw[2] = {make_rsrc(g.w, wbytes), make_rsrc(EPI == 1 ? g.w2 : g.w, wbytes)};
-    // weight loads of the first chunk go out before the staging of x
     u32x4_t wv[NM][RPW];
     auto load_w = [&](int c) {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
-                const int row = row0 + r < g.n_out ? row0 + r : g.n_out;  // n_out: past the range
+                // n_out: past the range (zeros, no traffic), also for a lane with no chunk c
+                const int row = row0 + r < g.n_out && c < nch ? row0 + r : g.n_out;
                 wv[m][r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                            rw[m], (row * nch + c) * 16, 0, kCpolNT));
             }
     };
-    if (sub < nch) load_w(sub);
+    // Load order. Loads return in issue order, so a wait for a value also waits for every
+    // load issued before it: the operands of the prologue and of the staging of x go out
+    // first, then the epilogue's per-row operands, then the first weight chunk, which stays
+    // in flight while x is normed and staged. All of them are straight-line buffer loads (a
+    // load under a per-lane or skippable condition leaves the compiler unsure how many loads
+    // follow it, and it then waits for all of them).
+    constexpr int PER = (2048 + NT - 1) / NT;  // prologue values a thread (n_in <= 2048)
+    float av[PER], rv[PER], w1v[PER], w2v[PER];
+    float4v xv[4];  // the first staging batch of x
+    const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
+    if (g.pa) {  // workgroup-uniform
+        const uint32_t nb = (uint32_t)n_in * 4u;
+        const rsrc_t ra = make_rsrc(g.pa, nb), rr = make_rsrc(g.pres, nb), r1 = make_rsrc(g.pw1, nb),
+                     r2 = make_rsrc(g.pw2, g.pw2 ? nb : 0u);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int o = 4 * (tid + NT * k);  // past n_in: zeros
+            av[k] = bload_f32(ra, o);
+            rv[k] = bload_f32(rr, o);
+            w1v[k] = bload_f32(r1, o);
+            w2v[k] = bload_f32(r2, o);
+        }
+    } else if (stage) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xv[k] = bload_f32x4(rx, 16 * (tid + NT * k));
+    }
     // the epilogue's per-row operands (thread r of a group writes row r) come in with the
     // first weight chunk: loaded in the epilogue they cost a memory round trip after the dot
     // products (1.1 us of the gate/up GEMV's 7 us, timestamped)
+    const bool erow = sub < RPW && row0 + sub < g.n_out;
+    const int eo = 4 * (erow ? row0 + sub : g.n_out);  // past the range: zeros
+    const uint32_t ob = (uint32_t)g.n_out * 4u;
     float esc[NM], emul = 0.0f;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) esc[m] = 1.0f;
-    if (sub < RPW && row0 + sub < g.n_out) {
-        if (g.scale) esc[0] = g.scale[row0 + sub];
-        if constexpr (EPI == 1) esc[NM - 1] = g.scale2 ? g.scale2[row0 + sub] : 1.0f;
-        if constexpr (EPI == 2) emul = g.mul[row0 + sub];
-    }
+    esc[0] = bload_f32(make_rsrc(g.scale, g.scale ? ob : 0u), eo);
+    if constexpr (EPI == 1) esc[NM - 1] = bload_f32(make_rsrc(g.scale2, g.scale2 ? ob : 0u), eo);
+    if constexpr (EPI == 2) emul = bload_f32(make_rsrc(g.mul, ob), eo);
+    load_w(sub);
+    __builtin_amdgcn_sched_barrier(0);  // no prologue arithmetic (and its waits) above the weight loads
+    if (!g.scale || !erow) esc[0] = 1.0f;
+    if constexpr (EPI == 1)
+        if (!g.scale2 || !erow) esc[NM - 1] = 1.0f;
     float sx[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) sx[m] = 0.0f;
@@ -271,17 +300,12 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         }
     };
     if (g.pa) {  // workgroup-uniform; n_in <= 2048
-        constexpr int PER = (2048 + NT - 1) / NT;
         __shared__ float pred[2][16];  // one buffer per reduction
-        float av[PER], rv[PER], w1v[PER], w2v[PER];
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = tid + NT * k;
-            const bool ok = i < n_in;
-            av[k] = ok ? g.pa[i] : 0.0f;
-            rv[k] = ok ? g.pres[i] : 0.0f;
-            w1v[k] = ok ? g.pw1[i] : 1.0f;
-            w2v[k] = ok && g.pw2 ? g.pw2[i] : 1.0f;
+        for (int k = 0; k < PER; ++k) {  // the loaded zeros past n_in, and the unit gains
+            const bool ok = tid + NT * k < n_in;
+            if (!ok) w1v[k] = 1.0f;
+            if (!ok || !g.pw2) w2v[k] = 1.0f;
         }
         float ss = 0.0f;
 #pragma unroll
@@ -310,15 +334,11 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             }
         }
     } else if (stage) {
-        // every load of x first, in batches of 4096 values (4 float4 a thread), then the
-        // staging: one L2 round trip per batch instead of one per element
-        for (int b0 = 0; b0 < n_in; b0 += 16 * NT) {
-            float4v xv[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int i = b0 + 4 * (tid + NT * k);
-                xv[k] = i < n_in ? *reinterpret_cast<const float4v*>(g.x + i) : float4v{0, 0, 0, 0};
-            }
+        // every load of x first, in batches of 16 NT values (4 float4 a thread), then the
+        // staging: one L2 round trip per batch instead of one per element. The first batch
+        // was loaded before the weights and is staged outside the loop (inside it, the join
+        // with the loop's own loads would make its wait cover the weights again).
+        auto stage_batch = [&](int b0) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int i = b0 + 4 * (tid + NT * k);
@@ -327,6 +347,12 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
                     for (int e = 0; e < 4; ++e) stage_x(i + e, xv[k][e]);
                 }
             }
+        };
+        stage_batch(0);
+        for (int b0 = 16 * NT; b0 < n_in; b0 += 16 * NT) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xv[k] = bload_f32x4(rx, 4 * (b0 + 4 * (tid + NT * k)));
+            stage_batch(b0);
         }
     }
     float xtot[NM];  // staged: the sum of the whole quantised x, known after the barrier
@@ -350,7 +376,6 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
             sx[m] = 0.0f;
         }
     }
-    const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
     // IDOT sums stay int32 to the end (exact at any row length); the others are f32
     float acc[NM][RPW];
     int iacc[NM][RPW];
