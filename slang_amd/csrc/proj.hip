@@ -110,9 +110,26 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
     const int r0 = row0 - (mat == 0 ? 0 : mat == 1 ? g.q_dim : g.q_dim + g.kv_dim);
     const int nrows = mat == 0 ? g.q_dim : g.kv_dim;
     const int row_bytes = g.hidden / 2;
-    // every operand load first: the input chunks, the packed rows, the scales and the sum
+    // every operand load first: the prologue's operands, the packed rows, then the input
+    // chunks and the sum. Loads return in issue order, so the prologue's operands go out
+    // before the rows: its norms and barriers then run while the rows are in flight.
     const rsrc_t ra = make_rsrc(g.a, (uint32_t)g.hidden * 4);
     const rsrc_t rw = make_rsrc(g.bits[mat], (uint32_t)nrows * row_bytes);
+    constexpr int PER = 8;  // prologue: thread t holds elements t + 256k of each operand
+    float pv[PER], rv[PER], w1v[PER], w2v[PER];
+    if constexpr (PRO) {
+        const uint32_t nb = (uint32_t)g.hidden * 4;  // past hidden: zeros
+        const rsrc_t rpa = make_rsrc(g.pa, nb), rpr = make_rsrc(g.pres, nb), rp1 = make_rsrc(g.pw1, nb),
+                     rp2 = make_rsrc(g.pw2, nb);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int o = 4 * ((int)threadIdx.x + 256 * k);
+            pv[k] = bload_f32(rpa, o);
+            rv[k] = bload_f32(rpr, o);
+            w1v[k] = bload_f32(rp1, o);
+            w2v[k] = bload_f32(rp2, o);
+        }
+    }
     float av[NJ][32];
     u32x4 wv[RPW][NJ];
 #pragma unroll
@@ -123,27 +140,17 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvArgs g) {
             const int off = c < row_bytes / 16 ? (r0 + r) * row_bytes + 16 * c : 0x7fffffff;
             wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kCpolNT);  // read once: non-temporal
         }
+    __builtin_amdgcn_sched_barrier(0);  // no prologue arithmetic (and its waits) above the row loads
     float sa;
     if constexpr (PRO) {
-        // once per workgroup: thread t holds elements t + 256k of each operand; the sums run
-        // per thread, then over the workgroup (block_sum); a is staged in LDS, from which lane c
-        // of every wave takes elements 32c .. 32c+31. The arithmetic is the rms_kernel's:
-        // y = (res + pa / d1 * w1) * mult, z = y / d2 * w2, a = srq(z, q2).
+        // once per workgroup: the sums run per thread, then over the workgroup (block_sum); a
+        // is staged in LDS, from which lane c of every wave takes elements 32c .. 32c+31. The
+        // arithmetic is the rms_kernel's: y = (res + pa / d1 * w1) * mult, z = y / d2 * w2,
+        // a = srq(z, q2).
         static_assert(NJ == 1, "the norm prologue covers hidden <= 2048");
-        constexpr int PER = 8;
         __shared__ float s_a[2048];
         __shared__ float pred[4];
         const int tid = threadIdx.x, n = g.hidden;
-        float pv[PER], rv[PER], w1v[PER], w2v[PER];
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = tid + 256 * k;
-            const bool ok = i < n;
-            pv[k] = ok ? g.pa[i] : 0.0f;
-            rv[k] = ok ? g.pres[i] : 0.0f;
-            w1v[k] = ok ? g.pw1[i] : 0.0f;
-            w2v[k] = ok ? g.pw2[i] : 0.0f;
-        }
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) ss = __builtin_fmaf(pv[k], pv[k], ss);
