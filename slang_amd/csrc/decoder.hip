@@ -232,7 +232,11 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
     // follow it, and it then waits for all of them).
     constexpr int PER = (2048 + NT - 1) / NT;  // prologue values a thread (n_in <= 2048)
     float av[PER], rv[PER], w1v[PER], w2v[PER];
-    float4v xv[4];  // the first staging batch of x
+    // staging batches of x loaded before the weights: all of them (x <= 16384 values) for
+    // the 256-thread groups of the wide rows (the down projection: 12288 inputs are three
+    // batches, each a round trip of its own when loaded after the weights), else the first
+    constexpr int XB = T == 256 ? 4 : 1;
+    float4v xv[XB][4];
     const rsrc_t rx = make_rsrc(g.x, (uint32_t)n_in * 4u);
     if (g.pa) {  // workgroup-uniform
         const uint32_t nb = (uint32_t)n_in * 4u;
@@ -248,7 +252,9 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         }
     } else if (stage) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) xv[k] = bload_f32x4(rx, 16 * (tid + NT * k));
+        for (int b = 0; b < XB; ++b)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xv[b][k] = bload_f32x4(rx, 4 * (16 * NT * b + 4 * (tid + NT * k)));
     }
     // the epilogue's per-row operands (thread r of a group writes row r) come in with the
     // first weight chunk: loaded in the epilogue they cost a memory round trip after the dot
@@ -335,24 +341,26 @@ __global__ __launch_bounds__(NT) void qgemv_kernel(QgemvArgs g) {
         }
     } else if (stage) {
         // every load of x first, in batches of 16 NT values (4 float4 a thread), then the
-        // staging: one L2 round trip per batch instead of one per element. The first batch
-        // was loaded before the weights and is staged outside the loop (inside it, the join
-        // with the loop's own loads would make its wait cover the weights again).
-        auto stage_batch = [&](int b0) {
+        // staging: one L2 round trip per batch instead of one per element. The batches
+        // loaded before the weights are staged outside the loop (inside it, the join with
+        // the loop's own loads would make their waits cover the weights again).
+        auto stage_batch = [&](int b0, const float4v (&xb)[4]) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int i = b0 + 4 * (tid + NT * k);
                 if (i < n_in) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) stage_x(i + e, xv[k][e]);
+                    for (int e = 0; e < 4; ++e) stage_x(i + e, xb[k][e]);
                 }
             }
         };
-        stage_batch(0);
-        for (int b0 = 16 * NT; b0 < n_in; b0 += 16 * NT) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xv[k] = bload_f32x4(rx, 4 * (b0 + 4 * (tid + NT * k)));
-            stage_batch(b0);
+        for (int b = 0; b < XB; ++b)
+            if (16 * NT * b < n_in) stage_batch(16 * NT * b, xv[b]);
+        for (int b0 = 16 * NT * XB; b0 < n_in; b0 += 16 * NT) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xv[0][k] = bload_f32x4(rx, 4 * (b0 + 4 * (tid + NT * k)));
+            stage_batch(b0, xv[0]);
         }
     }
     float xtot[NM];  // staged: the sum of the whole quantised x, known after the barrier
