@@ -272,21 +272,32 @@ __device__ __forceinline__ int xcd_run_index() {
 
 // One RoPE pair (d, d + hd/2) of a new k and v row, per thread t = d < hd/2 of the first
 // hd/128 waves (kvnorm, kernels_dsl.py:573-618; kvnorm_b, :1789-1834): k <- RoPE(RMSNorm(
-// srq(k)) * gain), v <- RMSNorm(srq(v)) without scale, from the raw loaded values. The sums of squares run per wave then over the
-// waves in order through `red` (2 x hd/128 floats of LDS), so g4a_kv_write and the fused
-// decode write identical rows. Every wave of the workgroup must call it (one barrier);
-// threads t >= hd/2 pass zeros and ignore the result.
+// srq(k)) * gain), v <- RMSNorm(srq(v)) without scale, from the raw loaded values. The sums
+// of squares run per wave then over the waves in order through `red` (2 x hd/128 floats of
+// LDS), so g4a_kv_write and the fused decode write identical rows. Every wave of the
+// workgroup must call it (one barrier); threads t >= hd/2 pass zeros and ignore the result.
+// The pair's gain and rotation operands come from kv_pair_ops, which a kernel may call
+// early: loads return in issue order, so operands loaded after other traffic (the fused
+// decode's K/V block) would wait for it.
+struct KvPairOps {
+    float g0, g1, c, sn;
+};
 template <int HD>
-__device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, float& v1, const float* k_gain,
-                                             const float* rcos, const float* rsin, bool v_norm, float eps,
-                                             float k_in_q, float v_in_q, float* red, int t) {
-    constexpr int HALF = HD / 2, NW = HALF / 64;
-    // the gain and rotation operands load before srq (whose zero-scale branch waits for
-    // the raw values) and before the reduction's barrier (which no memory access crosses),
-    // so they share the raw row's round trip
+__device__ __forceinline__ KvPairOps kv_pair_ops(const float* k_gain, const float* rcos, const float* rsin, int t) {
+    constexpr int HALF = HD / 2;
     const int tl = t < HALF ? t : 0;
-    const float g0 = k_gain ? k_gain[tl] : 1.0f, g1 = k_gain ? k_gain[tl + HALF] : 1.0f;
-    const float c = rcos ? rcos[tl] : 1.0f, sn = rcos ? rsin[tl] : 0.0f;
+    KvPairOps o;
+    o.g0 = k_gain ? k_gain[tl] : 1.0f;
+    o.g1 = k_gain ? k_gain[tl + HALF] : 1.0f;
+    o.c = rcos ? rcos[tl] : 1.0f;
+    o.sn = rcos ? rsin[tl] : 0.0f;
+    return o;
+}
+template <int HD>
+__device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, float& v1, const KvPairOps& o,
+                                             bool has_gain, bool has_rope, bool v_norm, float eps, float k_in_q,
+                                             float v_in_q, float* red, int t) {
+    constexpr int HALF = HD / 2, NW = HALF / 64;
     k0 = srq(k0, k_in_q);
     k1 = srq(k1, k_in_q);
     v0 = srq(v0, v_in_q);
@@ -304,17 +315,17 @@ __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, fl
         sk += red[w];
         sv += red[NW + w];
     }
-    if (k_gain) {
+    if (has_gain) {
         const float rs = 1.0f / sqrtf(sk / (float)HD + eps);  // kvnorm's k * rmsk * knorm
-        k0 = k0 * rs * g0;
-        k1 = k1 * rs * g1;
+        k0 = k0 * rs * o.g0;
+        k1 = k1 * rs * o.g1;
     }
-    if (rcos) {
+    if (has_rope) {
         // explicit fma forms: the two kernels that inline this (g4a_kv_write's and the fused
         // decode write) must not contract the rotation differently
         const float x0 = k0, x1 = k1;
-        k0 = __builtin_fmaf(x0, c, -(x1 * sn));
-        k1 = __builtin_fmaf(x1, c, x0 * sn);
+        k0 = __builtin_fmaf(x0, o.c, -(x1 * o.sn));
+        k1 = __builtin_fmaf(x1, o.c, x0 * o.sn);
     }
     if (v_norm) {
         const float rs = 1.0f / sqrtf(sv / (float)HD + eps);
@@ -326,6 +337,16 @@ __device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, fl
     k1 = pin(k1);
     v0 = pin(v0);
     v1 = pin(v1);
+}
+// The same with its operands loaded here: they load before srq (whose zero-scale branch
+// waits for the raw values) and before the reduction's barrier, so they share the raw
+// row's round trip.
+template <int HD>
+__device__ __forceinline__ void kv_pair_prep(float& k0, float& k1, float& v0, float& v1, const float* k_gain,
+                                             const float* rcos, const float* rsin, bool v_norm, float eps,
+                                             float k_in_q, float v_in_q, float* red, int t) {
+    const KvPairOps o = kv_pair_ops<HD>(k_gain, rcos, rsin, t);
+    kv_pair_prep<HD>(k0, k1, v0, v1, o, k_gain != nullptr, rcos != nullptr, v_norm, eps, k_in_q, v_in_q, red, t);
 }
 
 }  // namespace g4a

@@ -351,6 +351,11 @@ void decode_kernel(DecodeArgs a) {
     const int p_new = sp.hi - 1;
     const bool owns_new = KVW && p_new >= k0 && p_new < k1;  // workgroup-uniform
     float nk0 = 0.0f, nk1 = 0.0f, nv0 = 0.0f, nv1 = 0.0f;
+    KvPairOps nops{1.0f, 1.0f, 1.0f, 0.0f};
+    if (owns_new) {  // with the raw row, ahead of the block loads (which they would wait behind)
+        nops = kv_pair_ops<HD>(a.k_gain, a.rcos ? a.rcos + (size_t)b * HALF : nullptr,
+                               a.rsin ? a.rsin + (size_t)b * HALF : nullptr, tid);
+    }
     if (owns_new && tid < HALF) {
         const size_t ro = ((size_t)b * a.n_kv_heads + kh) * HD;
         // raw values: kv_pair_prep applies srq (a zero-scale branch here would wait for
@@ -437,9 +442,8 @@ void decode_kernel(DecodeArgs a) {
         }
     }
     if (owns_new) {  // every wave takes part (one barrier inside)
-        kv_pair_prep<HD>(nk0, nk1, nv0, nv1, a.k_gain, a.rcos ? a.rcos + (size_t)b * HALF : nullptr,
-                         a.rsin ? a.rsin + (size_t)b * HALF : nullptr, a.v_norm != 0, a.eps, a.k_in_q, a.v_in_q,
-                         kv_red, tid);
+        kv_pair_prep<HD>(nk0, nk1, nv0, nv1, nops, a.k_gain != nullptr, a.rcos != nullptr, a.v_norm != 0, a.eps,
+                         a.k_in_q, a.v_in_q, kv_red, tid);
         if (tid < HALF) {
             const size_t crow = (size_t)b * a.seq_stride + (size_t)p_new * a.n_kv_heads * HD + (size_t)kh * HD;
             KVT* kcw = reinterpret_cast<KVT*>(a.kc_out) + crow;
