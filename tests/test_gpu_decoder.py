@@ -32,6 +32,8 @@ def dev(a):
     (2, 1536, 12288, 0.05, 0.02),   # the 2-bit double-wide MLP
     (4, 6144, 1536, 0.01, 0.02),    # down
     (2, 12288, 1536, 0.01, 0.02),
+    (2, 16384, 1000, 0.01, 0.02),   # the widest staged x: all four preloaded batches
+    (4, 10240, 777, 0.01, 0.02),    # 2.5 batches; 320 chunks: some threads take two
     (8, 1536, 256, 0.05, 0.03),     # per-layer-embedding gate
     (8, 256, 1536, 0.03, 0.01),     # per-layer-embedding projection
     (2, 1536, 4099, 0.0, 0.0),      # lm_head rows (ragged count), no srq
@@ -56,6 +58,7 @@ def test_qgemv_parity(bits, n_in, n_out, in_q, out_q):
     (2, 1536, 12288),                  # the double-wide MLP's gate / up rows
     (2, 12288, 1536), (4, 6144, 1536),  # down projections: rows wider than a wave's chunks
     (4, 4096, 1536),                    # o_proj of an hd-512 layer
+    (2, 16384, 1000), (4, 10240, 777),  # x staged in four / two and a half batches
 ])
 def test_qgemv_integer_dot_is_exact(bits, n_in, n_out):
     """GEMVs with in_q > 0 sum codes times the int8 grid index k = srq's clamp(rint(x / in_q))
