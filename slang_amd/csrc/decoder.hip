@@ -725,8 +725,10 @@ static hipError_t qgemv_dispatch(const QgemvArgs& g, hipStream_t s) {
                   // 1.583 -> 1.571 against 1024)
         return BITS >= 4 && g.pa ? launch_qgemv<BITS, 64, 2, EPI, 768>(g, s)
                                  : launch_qgemv<BITS, 64, 2, EPI>(g, s);
-    if (c <= 128)  // with a prologue (the PLE gate): 512 threads, 4 elements of it a thread
-        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 128, 2, EPI, 512>(g, s) : launch_qgemv<BITS, 128, 2, EPI>(g, s);
+    if (c <= 128)  // with a prologue (the PLE gate): 512 threads, 4 elements of it a thread, one
+                   // row a group (its 256 rows in 64 workgroups, not 32: 1.540 -> 1.523 ms a
+                   // step; 128 workgroups of 256 threads gained nothing)
+        return BITS >= 4 && g.pa ? launch_qgemv<BITS, 128, 1, EPI, 512>(g, s) : launch_qgemv<BITS, 128, 2, EPI>(g, s);
     return launch_qgemv<BITS, 256, 3, EPI>(g, s);
 }
 
